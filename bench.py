@@ -1,0 +1,284 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized linear hot path on one MI355X.
+
+A step is one Q4_G64 M=1 GEMV (K=2560, N=10240: the north-star shape) over one
+weight copy.  Weights rotate over >= 512 MB of distinct copies so the 256 MB
+MALL cannot serve them; x, y and the copies are resident in HBM before the
+timed region.
+
+Two measurements, both on the stream the kernel is launched on:
+  * whole job: the K timed steps are replayed from HIP graphs (one graph of one
+    launch per weight copy), bracketed by synchronize; value = algorithmic
+    bytes * K / elapsed, ms_per_step = elapsed / K;
+  * kernel: K further launches with hipEvents attached to each GEMV dispatch
+    (hipExtLaunchKernel), giving the kernel's own average duration for the
+    roofline (algorithmic bytes / duration vs 8 TB/s).
+The CPU baseline is the oracle's C restatement of the same GEMV (same
+semantics, seeded inputs), timed on this host with 1 and all threads.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import ctypes as C
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4_G64 GEMV µs + achieved HBM GB/s (% of peak) at M=1; M=16 verify µs"
+PEAK_GBS = 8000.0
+ROTATE_BYTES = 512 * 1024 * 1024
+
+
+def algorithmic_bytes(qtype_bytes_per_row, N, K, M, G=64):
+    """packed weights + 16-bit scales + x (bf16, once) + y (bf16)."""
+    return N * qtype_bytes_per_row + N * (K // G) * 2 + M * K * 2 + M * N * 2
+
+
+class Hip:
+    """The few HIP runtime calls the bench needs for per-dispatch events."""
+
+    def __init__(self):
+        path = None
+        for cand in ("libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"):
+            try:
+                self.L = C.CDLL(cand)
+                path = cand
+                break
+            except OSError:
+                continue
+        if path is None:
+            raise RuntimeError("libamdhip64.so not found")
+        self.L.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+        self.L.hipEventDestroy.argtypes = [C.c_void_p]
+        self.L.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+        self.L.hipEventSynchronize.argtypes = [C.c_void_p]
+
+    def event(self):
+        e = C.c_void_p()
+        rc = self.L.hipEventCreate(C.byref(e))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreate failed: {rc}")
+        return e
+
+    def elapsed_ms(self, a, b):
+        ms = C.c_float()
+        rc = self.L.hipEventElapsedTime(C.byref(ms), a, b)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
+        return ms.value
+
+    def destroy(self, e):
+        self.L.hipEventDestroy(e)
+
+
+def make_weights(torch, copies, N, K, gen):
+    """Uniform bytes = uniform nibbles in [-8, 7]; fp16 scales log-uniform in [1e-3, 1e-2]."""
+    w = torch.randint(0, 256, (copies, N * K // 2), dtype=torch.uint8, device="cuda", generator=gen)
+    u = torch.rand((copies, N * (K // 64)), device="cuda", generator=gen, dtype=torch.float32)
+    s = torch.exp(math.log(1e-3) + u * math.log(10.0)).to(torch.float16)
+    return w, s
+
+
+def time_kernel(torch, hip, launch, n):
+    """Mean/median per-dispatch duration (us) of n launches with attached events."""
+    ev = [(hip.event(), hip.event()) for _ in range(n)]
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(ev):
+        launch(i, a, b)
+    torch.cuda.synchronize()
+    d = [hip.elapsed_ms(a, b) * 1e3 for a, b in ev]
+    for a, b in ev:
+        hip.destroy(a)
+        hip.destroy(b)
+    return statistics.fmean(d), statistics.median(d)
+
+
+def cpu_baseline(N, K, reps_1t, reps_mt):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    packed, scales = O.gen_weights(O.Q4_G64, N, K, 0x5EED0000, O.SCALE_FP16)
+    x = O.gen_act(1, K, 0x5EED0001)
+    nthreads = O.omp_max_threads()
+    O.qlinear_omp(O.Q4_G64, packed, scales, O.SCALE_FP16, N, K, x, 1)
+    t0 = time.perf_counter()
+    for _ in range(reps_1t):
+        O.qlinear_omp(O.Q4_G64, packed, scales, O.SCALE_FP16, N, K, x, 1)
+    t1 = (time.perf_counter() - t0) / reps_1t
+    O.qlinear_omp(O.Q4_G64, packed, scales, O.SCALE_FP16, N, K, x, nthreads)
+    t0 = time.perf_counter()
+    for _ in range(reps_mt):
+        O.qlinear_omp(O.Q4_G64, packed, scales, O.SCALE_FP16, N, K, x, nthreads)
+    tm = (time.perf_counter() - t0) / reps_mt
+    return t1, tm, nthreads
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4000)
+    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--kernel-launches", type=int, default=2000)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extras", action="store_true", help="skip the M=16 and down-shape lines")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the GEMV shards by output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import viper_amd as va
+
+    L = va.lib()
+    hip = Hip()
+    torch.cuda.set_device(0)
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(0x5EED0000)
+
+    N, K, M = 10240, 2560, 1
+    qtype, G = int(va.QType.Q4_G64), 64
+    copy_bytes = N * K // 2 + N * (K // G) * 2
+    copies = max(2, -(-ROTATE_BYTES // copy_bytes) + 1)
+    W, S = make_weights(torch, copies, N, K, gen)
+    x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    alg = algorithmic_bytes(K // 2, N, K, M)
+    wp = [W[i].data_ptr() for i in range(copies)]
+    spp = [S[i].data_ptr() for i in range(copies)]
+
+    def launch(i, ev0=None, ev1=None):
+        c = i % copies
+        if ev0 is None:
+            rc = L.viper_hip_qlinear(qtype, wp[c], spp[c], 0, G, N, K, x.data_ptr(), M, y.data_ptr(),
+                                     None, None, 0, sp)
+        else:
+            rc = L.viper_hip_qlinear_timed(qtype, wp[c], spp[c], 0, G, N, K, x.data_ptr(), M,
+                                           y.data_ptr(), None, None, 0, ev0, ev1, sp)
+        if rc != 0:
+            raise RuntimeError(f"viper_hip_qlinear failed: {rc}")
+
+    # warmup (eager), then capture one graph that walks every weight copy once
+    for i in range(args.warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(copies):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, args.steps // copies)
+    steps = replays * copies
+
+    # ---- timed region: whole job ------------------------------------------------
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    job_ms = e0.elapsed_time(e1)
+    ms_per_step = job_ms / steps
+    value = alg * steps / (job_ms * 1e-3) / 1e9
+
+    # ---- kernel duration: events attached to each dispatch ---------------------
+    k_mean, k_med = time_kernel(torch, hip, launch, args.kernel_launches)
+    achieved = alg / (k_mean * 1e-6) / 1e9
+
+    extras = {}
+    if not args.no_extras:
+        # M=16 speculative verify (K=2560, N=10240): quantize kernel + GEMM
+        M16 = 16
+        x16 = torch.randn((M16, K), device="cuda", generator=gen).to(torch.bfloat16)
+        y16 = torch.empty((M16, N), dtype=torch.bfloat16, device="cuda")
+        nws = va.workspace_bytes(qtype, N, K, M16)
+        ws16 = torch.empty(nws, dtype=torch.uint8, device="cuda")
+
+        def launch16(i, ev0=None, ev1=None):
+            c = i % copies
+            rc = L.viper_hip_qlinear_timed(qtype, wp[c], spp[c], 0, G, N, K, x16.data_ptr(), M16,
+                                           y16.data_ptr(), None, ws16.data_ptr(), nws, ev0, ev1, sp)
+            if rc != 0:
+                raise RuntimeError(f"M=16 qlinear failed: {rc}")
+        for i in range(50):
+            launch16(i)
+        m16_mean, m16_med = time_kernel(torch, hip, launch16, 400)
+        alg16 = algorithmic_bytes(K // 2, N, K, M16)
+        extras["m16_verify_gemm_us"] = round(m16_mean, 3)
+        extras["m16_verify_gemm_gbs"] = round(alg16 / (m16_mean * 1e-6) / 1e9, 1)
+
+        # down projection shape (K=10240, N=2560), M=1, fused quantize
+        Kd, Nd = 10240, 2560
+        Wd, Sd = make_weights(torch, copies, Nd, Kd, gen)
+        xd = torch.randn((1, Kd), device="cuda", generator=gen).to(torch.bfloat16)
+        yd = torch.empty((1, Nd), dtype=torch.bfloat16, device="cuda")
+        wdp = [Wd[i].data_ptr() for i in range(copies)]
+        sdp = [Sd[i].data_ptr() for i in range(copies)]
+
+        def launchd(i, ev0=None, ev1=None):
+            c = i % copies
+            rc = L.viper_hip_qlinear_timed(qtype, wdp[c], sdp[c], 0, G, Nd, Kd, xd.data_ptr(), 1,
+                                           yd.data_ptr(), None, None, 0, ev0, ev1, sp)
+            if rc != 0:
+                raise RuntimeError(f"down qlinear failed: {rc}")
+        for i in range(50):
+            launchd(i)
+        d_mean, _ = time_kernel(torch, hip, launchd, 400)
+        algd = algorithmic_bytes(Kd // 2, Nd, Kd, 1)
+        extras["down_k10240_n2560_us"] = round(d_mean, 3)
+        extras["down_k10240_n2560_gbs"] = round(algd / (d_mean * 1e-6) / 1e9, 1)
+        del Wd, Sd
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_q4_m1_k2560_n10240.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    cpu = None
+    if not args.no_cpu:
+        t1, tm, nth = cpu_baseline(N, K, reps_1t=10, reps_mt=40)
+        cpu = {"value": round(alg / tm / 1e9, 3), "unit": "GB/s", "cores": nth, "kind": "port",
+               "sample": (f"oracle C restatement (vo_qlinear_omp), Q4_G64 M=1 K={K} N={N}, seeded inputs; "
+                          f"{nth} threads: {tm * 1e3:.2f} ms/GEMV over 40 runs; "
+                          f"1 thread: {t1 * 1e3:.2f} ms/GEMV ({alg / t1 / 1e9:.3f} GB/s) over 10 runs")}
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded: uniform int4 weights, fp16 log-uniform scales, bf16 N(0,1) x)",
+        "config": {"workload": "Q4_G64 GEMV M=1 K=2560 N=10240 (north star), fused bf16->int8 quantize",
+                   "qtype": "Q4_G64", "M": M, "K": K, "N": N, "weight_copies": copies,
+                   "rotation_bytes": copies * copy_bytes, "algorithmic_bytes_per_step": alg,
+                   "timed_region": "HIP graph replays of one launch per weight copy"},
+        "us_per_gemv_kernel": round(k_mean, 3),
+        "us_per_gemv_kernel_median": round(k_med, 3),
+        "us_per_step_whole_job": round(ms_per_step * 1e3, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic},
+        "cpu_baseline": cpu,
+    }
+    out.update(extras)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

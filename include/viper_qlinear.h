@@ -1,0 +1,140 @@
+/*
+ * viper_qlinear.h -- C ABI of the MI355X (gfx950) quantized linear path.
+ *
+ * This is the drop-in boundary under Viper's closed `linear()` switch.  Every
+ * entry point is `extern "C"`, takes plain pointers and sizes, returns an int
+ * equal to a viper::StatusCode value, never throws and allocates nothing.
+ * All pointers are caller-owned device memory; calls are asynchronous and
+ * ordered on `stream` (a hipStream_t, or NULL for the null stream).  Launch
+ * errors are returned at once; device faults surface at the caller's next
+ * synchronising call.  No entry point keeps state between calls, so calls
+ * are re-entrant from any host thread.
+ *
+ * Reference interfaces replaced (itzrnvr/viper):
+ *   viper_hip_qlinear               the Q4_G64 / Q5_G64|Q6_G64 / W8_G32 cases of
+ *                                   ops::linear_forward (src/viper/linear.cpp:16-36,
+ *                                   include/viper/ops.h:30-33), i.e. the
+ *                                   quantize + dp4a GEMV pair the engine calls
+ *                                   directly: rmsnorm_quantize_bf16 / quantize_to_q8
+ *                                   + dp4a_smem_gemv{,_residual}
+ *                                   (kernels/ops/dp4a_smem_kernel.h:10-20) and
+ *                                   linear_q4_multim{,_residual}
+ *                                   (kernels/ops/linear_multim.h:11-20).
+ *   viper_hip_quantize_act          quantize_to_q8 (kernels/ops/linear_multim.h:24-26).
+ *   viper_hip_qlinear_prequantized  dp4a_smem_gemv{,_residual}
+ *                                   (kernels/ops/dp4a_smem_kernel.h:10-20) and
+ *                                   linear_q4_dp4a_prequantized{,_residual}
+ *                                   (kernels/ops/linear_multim.h:30-41).
+ *   viper_hip_qlinear_partials      no counterpart: the same kernels, also writing
+ *                                   the exact per-group int32 dots for parity tests.
+ *   viper_hip_qlinear_timed         no counterpart: viper_hip_qlinear with events
+ *                                   attached to the GEMV dispatch (benchmarking).
+ *   viper_hip_check_quantizer       no counterpart: device self-check of the
+ *                                   activation quantizer's rounding.
+ *
+ * Formats (qtype values are viper::quant::QType, include/viper/quant.h:19-26):
+ *   Q4_G64 (4)  packed [N][K/2]; k even in the low nibble; nibble = w + 8.
+ *   Q5_G64 (5)  low plane [N][K/2] (nibbles of u = w + 16), then high plane
+ *               [N][K/8]: per 32-weight chunk one u32 holding bit 4 of u for
+ *               weight 8i+2b+p at bit 8b+2i+p.
+ *   Q6_G64 (6)  low plane [N][K/2] (u = w + 32), then high plane [N][K/4]: per
+ *               chunk two u32; word i/2 holds bits 4..5 of u at bit 8b+4(i%2)+2p.
+ *   W8_G32 (8)  [N][K] int8, w in [-127, 127].
+ *   Scales [N][K/G] 16-bit: fp16 (scale_enc 0) or bf16 (scale_enc 1).
+ *   G = 64 for Q4/Q5/Q6, 32 for W8; activations are quantized per row and per
+ *   G-group: s = max(amax/127, 1e-8), q = RNE(x/s) clamped to +-127.
+ *   y[m][n] = bf16_RNE( sum_g ws[n][g] * xs[m][g] * D[m][n][g] [+ residual] ),
+ *   D = exact int32 group dot.
+ *
+ * Alignment: w_packed and x 16 bytes, xq 8 bytes, xs 4 bytes, scales, y and
+ * residual 2 bytes, partials 4 bytes.  Shapes: N, K, M > 0, K % G == 0,
+ * M <= 16.
+ */
+#ifndef VIPER_QLINEAR_H
+#define VIPER_QLINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes: the numbering of viper::StatusCode (include/viper/status.h:12-21). */
+#define VIPER_OK 0
+#define VIPER_UNIMPLEMENTED 1
+#define VIPER_INVALID_ARGUMENT 2
+#define VIPER_DEVICE_ERROR 3 /* CUDA_ERROR in the reference */
+#define VIPER_SHAPE_MISMATCH 4
+#define VIPER_OUT_OF_MEMORY 5
+#define VIPER_INTERNAL 99
+
+/* QType values (include/viper/quant.h:19-26). */
+#define VIPER_QTYPE_BF16 0
+#define VIPER_QTYPE_FP32 1
+#define VIPER_QTYPE_Q4_G64 4
+#define VIPER_QTYPE_Q5_G64 5
+#define VIPER_QTYPE_Q6_G64 6
+#define VIPER_QTYPE_W8_G32 8
+
+#define VIPER_SCALE_FP16 0
+#define VIPER_SCALE_BF16 1
+
+#define VIPER_QLINEAR_MAX_M 16
+#define VIPER_QLINEAR_ABI_VERSION 1
+
+int viper_hip_abi_version(void);
+
+/* Group size of a quantized qtype (64 or 32), 0 for anything else. */
+int viper_hip_group_size(int qtype);
+
+/* Bytes of caller workspace viper_hip_qlinear needs for this shape; 0 when
+ * the activation quantize is fused into the GEMV (M == 1). */
+size_t viper_hip_qlinear_workspace_bytes(int qtype, int N, int K, int M);
+
+/* y[M][N] = linear(w, x) with x[M][K] bf16 quantized per row and group.
+ * residual (may be NULL) is added in fp32 before the bf16 round.  group must
+ * equal the format's group size.  workspace may be NULL when
+ * viper_hip_qlinear_workspace_bytes() is 0. */
+int viper_hip_qlinear(int qtype, const void* w_packed, const void* w_scales, int scale_enc,
+                      int group, int N, int K, const void* x_bf16, int M, void* y_bf16,
+                      const void* residual_bf16, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* xq[M][K] int8 and xs[M][K/group] fp32 from x[M][K] bf16 (group 64 or 32). */
+int viper_hip_quantize_act(int group, const void* x_bf16, int M, int K, void* xq, void* xs,
+                           void* stream);
+
+/* y[M][N] from already quantized activations xq[M][K] (natural order) and
+ * xs[M][K/group]. */
+int viper_hip_qlinear_prequantized(int qtype, const void* w_packed, const void* w_scales,
+                                   int scale_enc, int group, int N, int K, const void* xq,
+                                   const void* xs, int M, void* y_bf16,
+                                   const void* residual_bf16, void* stream);
+
+/* viper_hip_qlinear with two caller-created hipEvent_t attached to the GEMV
+ * dispatch (measurement use: they bracket the kernel's own execution, not
+ * the host launch).  No counterpart in the reference. */
+int viper_hip_qlinear_timed(int qtype, const void* w_packed, const void* w_scales, int scale_enc,
+                            int group, int N, int K, const void* x_bf16, int M, void* y_bf16,
+                            const void* residual_bf16, void* workspace, size_t workspace_bytes,
+                            void* start_event, void* stop_event, void* stream);
+
+/* viper_hip_qlinear, also writing D[M][N][K/group] int32 (test use). */
+int viper_hip_qlinear_partials(int qtype, const void* w_packed, const void* w_scales,
+                               int scale_enc, int group, int N, int K, const void* x_bf16, int M,
+                               void* y_bf16, const void* residual_bf16, void* workspace,
+                               size_t workspace_bytes, int32_t* partials, void* stream);
+
+/* Device self-check of the division-free quantizer step (test use): for
+ * every finite bf16 pair (amax, x) with 0 <= x <= amax and amax's exponent
+ * field in [exp_lo, exp_hi] (0..254), compares the kernels' rounding with an
+ * IEEE divide on the device.  counts[i] (int32, (exp_hi-exp_lo+1)*128
+ * entries) receives the number of disagreements for amax bits
+ * (exp_lo << 7) + i. */
+int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VIPER_QLINEAR_H */

@@ -1,0 +1,85 @@
+"""C-ABI library checks that need no GPU: it loads, exports every entry point
+include/viper_qlinear.h declares, and rejects bad arguments with the
+reference's status codes (include/viper/status.h:12-21) before touching the
+device.  Argument rules follow the reference launchers
+(kernels/ops/linear_multim.cu:152, dp4a_smem_kernel.cu:82, linear.cpp:33-35)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+import viper_amd as va
+from viper_amd import qlinear as ql
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "viper_qlinear.h")
+
+
+def declared():
+    txt = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t)\s+(viper_hip_\w+)\s*\(", txt, re.M)))
+
+
+def test_header_symbols_exported():
+    L = va.lib()
+    names = declared()
+    assert len(names) >= 9
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(ql._SYMBOLS)
+    assert L.viper_hip_abi_version() == 1
+
+
+def test_group_sizes_and_workspace():
+    L = va.lib()
+    assert [L.viper_hip_group_size(q) for q in (4, 5, 6, 8, 0, 1, 7)] == [64, 64, 64, 32, 0, 0, 0]
+    assert va.workspace_bytes(4, 10240, 2560, 1) == 0
+    assert va.workspace_bytes(4, 10240, 2560, 4) == 4 * 2560 + 4 * 40 * 4
+    assert va.workspace_bytes(8, 10, 2560, 3) == 3 * 2560 + ((3 * 80 * 4 + 15) // 16) * 16
+
+
+FAKE = 0x10000  # never dereferenced: every call below fails validation first
+
+
+@pytest.mark.parametrize("args,code", [
+    (dict(qtype=0), 1),             # BF16: not on this path (UNIMPLEMENTED, as linear.cpp:19-24)
+    (dict(qtype=1), 1),
+    (dict(qtype=7), 2),             # bad dtype -> INVALID_ARGUMENT (linear.cpp:33-35)
+    (dict(w=None), 2),
+    (dict(s=None), 2),
+    (dict(x=None), 2),
+    (dict(y=None), 2),
+    (dict(M=17), 2),                # M > 16 (linear_multim.cu:152)
+    (dict(M=0), 2),
+    (dict(N=0), 2),
+    (dict(K=96), 2),                # K % 64 != 0 (dp4a_smem_kernel.cu:82)
+    (dict(group=32), 2),            # group does not match the format
+    (dict(senc=2), 2),
+    (dict(w=FAKE + 8), 2),          # weights not 16-byte aligned
+    (dict(x=FAKE + 4), 2),
+    (dict(M=2), 2),                 # M > 1 needs a workspace
+])
+def test_argument_validation(args, code):
+    a = dict(qtype=4, w=FAKE, s=FAKE, senc=0, group=64, N=64, K=128, x=FAKE, M=1, y=FAKE)
+    a.update(args)
+    rc = va.lib().viper_hip_qlinear(a["qtype"], a["w"], a["s"], a["senc"], a["group"], a["N"], a["K"],
+                                    a["x"], a["M"], a["y"], None, None, 0, None)
+    assert rc == code
+
+
+def test_other_entry_validation():
+    L = va.lib()
+    assert L.viper_hip_quantize_act(48, FAKE, 1, 96, FAKE, FAKE, None) == 2
+    assert L.viper_hip_quantize_act(64, FAKE, 1, 96, FAKE, FAKE, None) == 2
+    assert L.viper_hip_qlinear_prequantized(4, FAKE, FAKE, 0, 64, 8, 64, None, FAKE, 1, FAKE, None, None) == 2
+    assert L.viper_hip_qlinear_partials(4, FAKE, FAKE, 0, 64, 8, 64, FAKE, 1, FAKE, None, None, 0, None, None) == 2
+    assert L.viper_hip_check_quantizer(10, 5, FAKE, None) == 2
+    assert L.viper_hip_check_quantizer(0, 255, FAKE, None) == 2
+
+
+def test_registry_mirror():
+    assert [va.qtype_name(q) for q in (0, 1, 4, 5, 6, 8, 3)] == [
+        "BF16", "FP32", "Q4_G64", "Q5_G64", "Q6_G64", "W8_G32", "UNKNOWN"]
+    assert va.is_lossless(0) and va.is_lossless(1) and not va.is_lossless(4)
+    assert va.packed_bytes(va.QType.Q5_G64, 2, 64) == 2 * 32 + 2 * 8

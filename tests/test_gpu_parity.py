@@ -1,0 +1,215 @@
+"""GPU parity of the gfx950 kernels against the CPU oracle, through the C ABI.
+
+Bar: per-group int32 dots D[m,n,g] bit-exact; int8 activations and fp32 group
+scales bit-exact; bf16 outputs within 1 bf16 ulp of the oracle's bf16 output
+or within 1e-5 * sum|group terms| (the condition-aware bound).  Sizes run from
+one group up to the north-star shape (K=2560, N=10240), which the oracle
+finishes in well under a second.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+import viper_amd as va
+
+pytestmark = pytest.mark.gpu
+
+FORMATS = [O.Q4_G64, O.Q5_G64, O.Q6_G64, O.W8_G32]
+REL_TOL = 1e-5  # relative to sum |group terms|, plus the 1-bf16-ulp clause
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU (run them on the MI355X box)")
+    return torch
+
+
+def dev(torch, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to("cuda")
+
+
+def host(t, dtype):
+    a = t.cpu().numpy()
+    return a.view(dtype) if a.dtype.itemsize == np.dtype(dtype).itemsize else a.astype(dtype)
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def run_case(torch, qtype, N, K, M, seed, scale_enc=O.SCALE_FP16, residual=False, outlier=0.0,
+             check_partials=True):
+    note(f"case qtype={qtype} N={N} K={K} M={M} seed={seed} senc={scale_enc} res={residual}")
+    G = O.group_size(qtype)
+    packed, scales = O.gen_weights(qtype, N, K, seed, scale_enc)
+    x = O.gen_act(M, K, seed + 1, outlier_frac=outlier, outlier_mul=20.0)
+    res = O.gen_act(M, N, seed + 2) if residual else None
+    y_ref, _, absterm = O.qlinear(qtype, packed, scales, scale_enc, N, K, x, residual=res)
+    xq, _ = O.quantize_act(x, G)
+    D_ref = O.group_dots(qtype, packed, N, K, xq)
+
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G,
+                           va.ScaleEnc(scale_enc))
+    xd = dev(torch, x)
+    yd = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    pd = torch.full((M, N, K // G), -7, dtype=torch.int32, device="cuda")
+    rd = None if res is None else dev(torch, res)
+    nws = va.workspace_bytes(qtype, N, K, M)
+    wsd = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda") if nws else None
+    if check_partials:
+        st = va.linear_partials(w, xd, yd, pd, residual=rd, workspace=wsd)
+    else:
+        st = va.linear(w, xd, yd, residual=rd, workspace=wsd)
+    assert st.ok(), st
+    torch.cuda.synchronize()
+    if check_partials:
+        np.testing.assert_array_equal(host(pd, np.int32), D_ref)
+    O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
+    return host(yd, np.uint16)
+
+
+def test_device_quantizer_exhaustive(torch_dev):
+    torch = torch_dev
+    counts = torch.full((255 * 128,), -1, dtype=torch.int32, device="cuda")
+    st = va.check_quantizer(0, 254, counts)
+    assert st.ok(), st
+    torch.cuda.synchronize()
+    c = counts.cpu().numpy()
+    assert (c == 0).all(), np.nonzero(c)[0][:10]
+
+
+@pytest.mark.parametrize("group", [64, 32])
+def test_quantize_act_bitexact(torch_dev, group):
+    torch = torch_dev
+    M, K = 5, 2560
+    x = O.gen_act(M, K, 11, outlier_frac=0.05, outlier_mul=20.0)
+    xf = O.bf16_to_f32(x).copy()
+    xf[0, :group] = 0.0                         # zero group -> scale 1e-8
+    xf[1, :group] = 0.0                         # amax 127 -> scale 1, exact ties
+    xf[1, :6] = [127.0, 2.5, 3.5, -2.5, 0.5, -1.5]
+    xf[2, group:2 * group] = np.linspace(-1e-6, 1e-6, group)
+    x = O.f32_to_bf16(xf)
+    xq_ref, xs_ref = O.quantize_act(x, group)
+    xq = torch.zeros((M, K), dtype=torch.int8, device="cuda")
+    xs = torch.zeros((M, K // group), dtype=torch.float32, device="cuda")
+    st = va.quantize_act(dev(torch, x), group, xq, xs)
+    assert st.ok(), st
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(xq.cpu().numpy(), xq_ref)
+    np.testing.assert_array_equal(xs.cpu().numpy().view(np.uint32), xs_ref.view(np.uint32))
+    assert list(xq_ref[1, :6]) == [127, 2, 4, -2, 0, -2]
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("scale_enc", [O.SCALE_FP16, O.SCALE_BF16])
+@pytest.mark.parametrize("N,K", [(1, 64), (37, 128), (100, 640), (256, 2560), (19, 10240)])
+def test_m1_fused(torch_dev, qtype, scale_enc, N, K):
+    run_case(torch_dev, qtype, N, K, 1, seed=1000 + N + K, scale_enc=scale_enc)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 16])
+def test_multi_row(torch_dev, qtype, M):
+    K = 2048 if M <= 8 else 2560
+    run_case(torch_dev, qtype, 77, K, M, seed=2000 + M, residual=(M % 2 == 0))
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_residual_and_outliers(torch_dev, qtype):
+    run_case(torch_dev, qtype, 130, 2560, 1, seed=31, residual=True, outlier=0.05)
+
+
+def test_north_star_full_size(torch_dev):
+    run_case(torch_dev, O.Q4_G64, 10240, 2560, 1, seed=0x5EED0000)
+
+
+def test_down_shape_full_size(torch_dev):
+    run_case(torch_dev, O.Q4_G64, 2560, 10240, 1, seed=0x5EED0001, residual=True)
+
+
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_format_sweep_full_size(torch_dev, qtype):
+    # config 4: K=2560, N=10240 with 5% x20 outlier channels
+    run_case(torch_dev, qtype, 10240, 2560, 1, seed=0x5EED0004, outlier=0.05, check_partials=False)
+
+
+def test_row_matches_single_row_call(torch_dev):
+    # row m of an M-row call equals an M=1 call on row m, bit for bit
+    torch = torch_dev
+    N, K, M = 300, 2560, 4
+    packed, scales = O.gen_weights(O.Q4_G64, N, K, 5, O.SCALE_FP16)
+    x = O.gen_act(M, K, 6)
+    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K)
+    ws = torch.zeros(va.workspace_bytes(4, N, K, M), dtype=torch.uint8, device="cuda")
+    pm = torch.zeros((M, N, K // 64), dtype=torch.int32, device="cuda")
+    ym = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    assert va.linear_partials(w, dev(torch, x), ym, pm, workspace=ws).ok()
+    for m in range(M):
+        p1 = torch.zeros((1, N, K // 64), dtype=torch.int32, device="cuda")
+        y1 = torch.zeros((1, N), dtype=torch.int16, device="cuda")
+        assert va.linear_partials(w, dev(torch, x[m:m + 1]), y1, p1).ok()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(p1.cpu().numpy()[0], pm.cpu().numpy()[m])
+
+
+def test_prequantized_entry(torch_dev):
+    torch = torch_dev
+    for qtype in FORMATS:
+        G = O.group_size(qtype)
+        N, K, M = 200, 2560, 3
+        packed, scales = O.gen_weights(qtype, N, K, 40 + qtype, O.SCALE_BF16)
+        x = O.gen_act(M, K, 41)
+        xq, xs = O.quantize_act(x, G)
+        res = O.gen_act(M, N, 42)
+        y_ref, _, absterm = O.qlinear_prequant(qtype, packed, scales, O.SCALE_BF16, N, K, xq, xs, residual=res)
+        w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, va.ScaleEnc.BF16)
+        yd = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+        st = va.linear_prequantized(w, dev(torch, xq), dev(torch, xs), yd, residual=dev(torch, res))
+        assert st.ok(), st
+        torch.cuda.synchronize()
+        O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
+
+
+def test_zero_weight_kat(torch_dev):
+    # all-0x88 Q4 bytes are all-zero weights: y is exactly the residual
+    torch = torch_dev
+    N, K = 64, 2560
+    packed = np.full(N * K // 2, 0x88, np.uint8)
+    scales = np.full(N * K // 64, 0x3C00, np.uint16)
+    x = O.gen_act(1, K, 3)
+    res = O.gen_act(1, N, 4)
+    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K)
+    yd = torch.zeros((1, N), dtype=torch.int16, device="cuda")
+    assert va.linear(w, dev(torch, x), yd, residual=dev(torch, res)).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(yd, np.uint16), res)
+
+
+def test_deterministic(torch_dev):
+    a = run_case(torch_dev, O.Q6_G64, 513, 4096, 1, seed=9)
+    b = run_case(torch_dev, O.Q6_G64, 513, 4096, 1, seed=9)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_device_errors_are_codes(torch_dev):
+    torch = torch_dev
+    N, K = 64, 128
+    packed, scales = O.gen_weights(O.Q4_G64, N, K, 1, O.SCALE_FP16)
+    wd, sd = dev(torch, packed), dev(torch, scales)
+    x = dev(torch, O.gen_act(2, K, 1))
+    y = torch.zeros((2, N), dtype=torch.int16, device="cuda")
+    w = va.QuantizedWeight(va.QType.Q4_G64, wd, sd, N, K)
+    assert va.linear(w, x, y).code == va.StatusCode.INVALID_ARGUMENT        # M=2 without workspace
+    small = torch.zeros(16, dtype=torch.uint8, device="cuda")
+    assert va.linear(w, x, y, workspace=small).code == va.StatusCode.INVALID_ARGUMENT
+    wbad = va.QuantizedWeight(va.QType.BF16, wd, sd, N, K)
+    assert va.linear(wbad, x, y).code == va.StatusCode.UNIMPLEMENTED
+    assert va.linear(w, x[:1], y[:1, :N - 1]).code == va.StatusCode.SHAPE_MISMATCH

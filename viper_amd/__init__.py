@@ -1,0 +1,8 @@
+"""MI355X-native quantized linear path of Viper (gfx950 HIP kernels behind a C ABI).
+
+Compute goes through ``viper_amd/lib/libviper_qlinear.so`` (include/viper_qlinear.h);
+there is no CPU fallback.
+"""
+from .qlinear import (GROUP, MAX_M, QType, QuantizedWeight, ScaleEnc, Status, StatusCode,  # noqa: F401
+                      check_quantizer, is_lossless, lib, linear, linear_partials, linear_prequantized,
+                      packed_bytes, qtype_name, quantize_act, workspace_bytes)

@@ -1,0 +1,249 @@
+"""ctypes binding of the gfx950 quantized-linear C ABI (include/viper_qlinear.h).
+
+Torch is plumbing here: tensors provide device memory and the stream; every
+compute call goes through ``libviper_qlinear.so``.  There is no fallback path:
+a missing library raises at load time.
+
+The Python surface mirrors the reference's host API (itzrnvr/viper):
+``QuantizedWeight`` is ``viper::quant::QuantizedWeight`` (include/viper/quant.h:34-41)
+plus the explicit scale encoding, ``QType``/``qtype_name``/``is_lossless`` are the
+closed registry (quant.h:19-29, src/viper/quant.cpp:6-20), and ``linear`` returns a
+``Status`` instead of raising, as ``viper::ops::linear_forward`` does
+(include/viper/ops.h:30-33, src/viper/linear.cpp:16-36).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import os
+from dataclasses import dataclass
+from typing import Optional
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libviper_qlinear.so")
+HOST_LIB_PATH = os.path.join(HERE, "lib", "libviper.so")
+
+
+class StatusCode(enum.IntEnum):
+    """Numbering of viper::StatusCode (include/viper/status.h:12-21)."""
+    OK = 0
+    UNIMPLEMENTED = 1
+    INVALID_ARGUMENT = 2
+    CUDA_ERROR = 3  # device error
+    SHAPE_MISMATCH = 4
+    OUT_OF_MEMORY = 5
+    IO_ERROR = 6
+    INTERNAL = 99
+
+
+@dataclass(frozen=True)
+class Status:
+    code: StatusCode = StatusCode.OK
+    message: str = ""
+
+    def ok(self) -> bool:
+        return self.code == StatusCode.OK
+
+    def __bool__(self) -> bool:
+        return self.ok()
+
+
+class QType(enum.IntEnum):
+    """Closed weight-format registry (include/viper/quant.h:19-26)."""
+    BF16 = 0
+    FP32 = 1
+    Q4_G64 = 4
+    Q5_G64 = 5
+    Q6_G64 = 6
+    W8_G32 = 8
+
+
+class ScaleEnc(enum.IntEnum):
+    FP16 = 0
+    BF16 = 1
+
+
+def qtype_name(q) -> str:
+    """src/viper/quant.cpp:6-16."""
+    try:
+        return QType(int(q)).name
+    except ValueError:
+        return "UNKNOWN"
+
+
+def is_lossless(q) -> bool:
+    """src/viper/quant.cpp:18-20."""
+    return int(q) in (QType.BF16, QType.FP32)
+
+
+GROUP = {QType.Q4_G64: 64, QType.Q5_G64: 64, QType.Q6_G64: 64, QType.W8_G32: 32}
+MAX_M = 16
+
+
+def packed_bytes(qtype, rows, cols) -> int:
+    q = QType(int(qtype))
+    if q == QType.Q4_G64:
+        return rows * cols // 2
+    if q == QType.Q5_G64:
+        return rows * cols // 2 + rows * cols // 8
+    if q == QType.Q6_G64:
+        return rows * cols // 2 + rows * cols // 4
+    if q == QType.W8_G32:
+        return rows * cols
+    raise ValueError(f"not a quantized qtype: {qtype_name(q)}")
+
+
+@dataclass
+class QuantizedWeight:
+    """Device view of one quantized matrix (reference quant.h:34-41).
+
+    ``data`` and ``scales`` are torch tensors on the device (uint8 / int16 or
+    uint16-sized storage); ``rows`` = N output channels, ``cols`` = K inputs.
+    """
+    qtype: QType
+    data: object
+    scales: object
+    rows: int
+    cols: int
+    group_size: int = 64
+    scale_enc: ScaleEnc = ScaleEnc.FP16
+
+
+_lib = None
+
+_SYMBOLS = (
+    "viper_hip_abi_version",
+    "viper_hip_group_size",
+    "viper_hip_qlinear_workspace_bytes",
+    "viper_hip_qlinear",
+    "viper_hip_quantize_act",
+    "viper_hip_qlinear_prequantized",
+    "viper_hip_qlinear_partials",
+    "viper_hip_qlinear_timed",
+    "viper_hip_check_quantizer",
+)
+
+
+def lib():
+    """Load libviper_qlinear.so; raise if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"viper_amd HIP library missing: {LIB_PATH}. Build it with __graft_entry__.build(); "
+            "there is no CPU fallback.")
+    L = C.CDLL(LIB_PATH)
+    vp, i32, sz = C.c_void_p, C.c_int, C.c_size_t
+    L.viper_hip_abi_version.argtypes, L.viper_hip_abi_version.restype = [], i32
+    L.viper_hip_group_size.argtypes, L.viper_hip_group_size.restype = [i32], i32
+    L.viper_hip_qlinear_workspace_bytes.argtypes = [i32, i32, i32, i32]
+    L.viper_hip_qlinear_workspace_bytes.restype = sz
+    L.viper_hip_qlinear.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
+    L.viper_hip_qlinear.restype = i32
+    L.viper_hip_quantize_act.argtypes = [i32, vp, i32, i32, vp, vp, vp]
+    L.viper_hip_quantize_act.restype = i32
+    L.viper_hip_qlinear_prequantized.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp]
+    L.viper_hip_qlinear_prequantized.restype = i32
+    L.viper_hip_qlinear_partials.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp, vp]
+    L.viper_hip_qlinear_partials.restype = i32
+    L.viper_hip_qlinear_timed.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp, vp, vp]
+    L.viper_hip_qlinear_timed.restype = i32
+    L.viper_hip_check_quantizer.argtypes = [i32, i32, vp, vp]
+    L.viper_hip_check_quantizer.restype = i32
+    _lib = L
+    return L
+
+
+def ptr(t) -> Optional[int]:
+    """Device address of a torch tensor (None stays None)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _status(rc: int, what: str) -> Status:
+    if rc == 0:
+        return Status()
+    try:
+        code = StatusCode(rc)
+    except ValueError:
+        code = StatusCode.INTERNAL
+    return Status(code, f"{what}: {code.name}")
+
+
+def workspace_bytes(qtype, N, K, M) -> int:
+    return int(lib().viper_hip_qlinear_workspace_bytes(int(qtype), N, K, M))
+
+
+def qlinear_raw(qtype, w, s, scale_enc, group, N, K, x, M, y, residual=None, workspace=None,
+                workspace_nbytes=0, stream=None) -> int:
+    """Direct call of viper_hip_qlinear with device addresses (ints)."""
+    return lib().viper_hip_qlinear(int(qtype), w, s, int(scale_enc), group, N, K, x, M, y, residual,
+                                   workspace, workspace_nbytes, _stream(stream))
+
+
+def _shape_mk(x, K):
+    if x.dim() == 1:
+        return 1
+    return int(x.numel() // K)
+
+
+def linear(w: QuantizedWeight, x, y, residual=None, workspace=None, stream=None) -> Status:
+    """y[M, N] = x[M, K] (bf16) through the quantized weight w; returns Status."""
+    if is_lossless(w.qtype):
+        return Status(StatusCode.UNIMPLEMENTED, f"linear {qtype_name(w.qtype)}: not on this path")
+    if int(w.qtype) not in GROUP:
+        return Status(StatusCode.INVALID_ARGUMENT, "linear: bad weight qtype")
+    K, N = w.cols, w.rows
+    if x.numel() % K or y.numel() % N:
+        return Status(StatusCode.SHAPE_MISMATCH, "linear: x/y do not match the weight shape")
+    M = _shape_mk(x, K)
+    if y.numel() != M * N:
+        return Status(StatusCode.SHAPE_MISMATCH, "linear: y rows != x rows")
+    if residual is not None and residual.numel() != M * N:
+        return Status(StatusCode.SHAPE_MISMATCH, "linear: residual shape")
+    ws_ptr, ws_n = (None, 0) if workspace is None else (ptr(workspace), workspace.numel() * workspace.element_size())
+    rc = lib().viper_hip_qlinear(int(w.qtype), ptr(w.data), ptr(w.scales), int(w.scale_enc), w.group_size,
+                                 N, K, ptr(x), M, ptr(y), ptr(residual), ws_ptr, ws_n, _stream(stream))
+    return _status(rc, "viper_hip_qlinear")
+
+
+def linear_partials(w: QuantizedWeight, x, y, partials, residual=None, workspace=None, stream=None) -> Status:
+    K, N = w.cols, w.rows
+    M = _shape_mk(x, K)
+    ws_ptr, ws_n = (None, 0) if workspace is None else (ptr(workspace), workspace.numel() * workspace.element_size())
+    rc = lib().viper_hip_qlinear_partials(int(w.qtype), ptr(w.data), ptr(w.scales), int(w.scale_enc),
+                                          w.group_size, N, K, ptr(x), M, ptr(y), ptr(residual), ws_ptr, ws_n,
+                                          ptr(partials), _stream(stream))
+    return _status(rc, "viper_hip_qlinear_partials")
+
+
+def quantize_act(x, group, xq, xs, stream=None) -> Status:
+    K = xq.shape[-1]
+    M = int(xq.numel() // K)
+    rc = lib().viper_hip_quantize_act(group, ptr(x), M, K, ptr(xq), ptr(xs), _stream(stream))
+    return _status(rc, "viper_hip_quantize_act")
+
+
+def linear_prequantized(w: QuantizedWeight, xq, xs, y, residual=None, stream=None) -> Status:
+    K, N = w.cols, w.rows
+    M = int(xq.numel() // K)
+    rc = lib().viper_hip_qlinear_prequantized(int(w.qtype), ptr(w.data), ptr(w.scales), int(w.scale_enc),
+                                              w.group_size, N, K, ptr(xq), ptr(xs), M, ptr(y), ptr(residual),
+                                              _stream(stream))
+    return _status(rc, "viper_hip_qlinear_prequantized")
+
+
+def check_quantizer(exp_lo, exp_hi, counts, stream=None) -> Status:
+    rc = lib().viper_hip_check_quantizer(exp_lo, exp_hi, ptr(counts), _stream(stream))
+    return _status(rc, "viper_hip_check_quantizer")
