@@ -6,24 +6,22 @@ weight copy.  Weights rotate over >= 512 MB of distinct copies so the 256 MB
 MALL cannot serve them; x, y and the copies are resident in HBM before the
 timed region.
 
-Two measurements, both on the stream the kernel is launched on:
-  * whole job: the K timed steps are replayed from HIP graphs (one graph of one
-    launch per weight copy), bracketed by synchronize; value = algorithmic
-    bytes * K / elapsed, ms_per_step = elapsed / K;
-  * kernel: K further launches with hipEvents attached to each GEMV dispatch
-    (hipExtLaunchKernel), giving the kernel's own average duration for the
-    roofline (algorithmic bytes / duration vs 8 TB/s).
+The K timed steps are replayed from a HIP graph (one captured launch per
+weight copy) so the host never throttles the stream; HIP events on that stream
+bracket the timed region.  value = algorithmic bytes * K / elapsed, and the
+roofline's achieved bandwidth uses the same average launch duration
+(elapsed / K), which rocprofv3's per-dispatch kernel durations agree with for
+back-to-back dispatches (profiles/).  Events attached to a single isolated
+dispatch include ~2.5 us of event overhead on this platform and are not used.
 The CPU baseline is the oracle's C restatement of the same GEMV (same
 semantics, seeded inputs), timed on this host with 1 and all threads.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 import argparse
-import ctypes as C
 import json
 import math
 import os
-import statistics
 import sys
 import time
 
@@ -40,43 +38,6 @@ def algorithmic_bytes(qtype_bytes_per_row, N, K, M, G=64):
     return N * qtype_bytes_per_row + N * (K // G) * 2 + M * K * 2 + M * N * 2
 
 
-class Hip:
-    """The few HIP runtime calls the bench needs for per-dispatch events."""
-
-    def __init__(self):
-        path = None
-        for cand in ("libamdhip64.so", "/opt/rocm/lib/libamdhip64.so"):
-            try:
-                self.L = C.CDLL(cand)
-                path = cand
-                break
-            except OSError:
-                continue
-        if path is None:
-            raise RuntimeError("libamdhip64.so not found")
-        self.L.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
-        self.L.hipEventDestroy.argtypes = [C.c_void_p]
-        self.L.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-        self.L.hipEventSynchronize.argtypes = [C.c_void_p]
-
-    def event(self):
-        e = C.c_void_p()
-        rc = self.L.hipEventCreate(C.byref(e))
-        if rc != 0:
-            raise RuntimeError(f"hipEventCreate failed: {rc}")
-        return e
-
-    def elapsed_ms(self, a, b):
-        ms = C.c_float()
-        rc = self.L.hipEventElapsedTime(C.byref(ms), a, b)
-        if rc != 0:
-            raise RuntimeError(f"hipEventElapsedTime failed: {rc}")
-        return ms.value
-
-    def destroy(self, e):
-        self.L.hipEventDestroy(e)
-
-
 def make_weights(torch, copies, N, K, gen):
     """Uniform bytes = uniform nibbles in [-8, 7]; fp16 scales log-uniform in [1e-3, 1e-2]."""
     w = torch.randint(0, 256, (copies, N * K // 2), dtype=torch.uint8, device="cuda", generator=gen)
@@ -85,18 +46,29 @@ def make_weights(torch, copies, N, K, gen):
     return w, s
 
 
-def time_kernel(torch, hip, launch, n):
-    """Mean/median per-dispatch duration (us) of n launches with attached events."""
-    ev = [(hip.event(), hip.event()) for _ in range(n)]
+def capture(torch, launch, copies, steps):
+    """One HIP graph holding one launch per weight copy; replays to cover steps."""
     torch.cuda.synchronize()
-    for i, (a, b) in enumerate(ev):
-        launch(i, a, b)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(copies):
+            launch(i)
+    graph.replay()
     torch.cuda.synchronize()
-    d = [hip.elapsed_ms(a, b) * 1e3 for a, b in ev]
-    for a, b in ev:
-        hip.destroy(a)
-        hip.destroy(b)
-    return statistics.fmean(d), statistics.median(d)
+    return graph, max(1, steps // copies)
+
+
+def time_graph(torch, graph, replays):
+    """Elapsed ms of `replays` graph replays, events on the replay stream."""
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1)
 
 
 def cpu_baseline(N, K, reps_1t, reps_mt):
@@ -123,7 +95,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=4000)
     ap.add_argument("--warmup", type=int, default=400)
-    ap.add_argument("--kernel-launches", type=int, default=2000)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device copy (FETCH_SIZE/WRITE_SIZE calibration under rocprofv3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extras", action="store_true", help="skip the M=16 and down-shape lines")
     args = ap.parse_args()
@@ -135,11 +108,18 @@ def main():
     import torch
     import viper_amd as va
 
+    if args.copy_calibration:
+        torch.cuda.set_device(0)
+        a = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": a.numel(), "launches": 5}), flush=True)
+        return
+
     L = va.lib()
-    hip = Hip()
     torch.cuda.set_device(0)
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
     gen = torch.Generator(device="cuda")
     gen.manual_seed(0x5EED0000)
 
@@ -154,45 +134,21 @@ def main():
     wp = [W[i].data_ptr() for i in range(copies)]
     spp = [S[i].data_ptr() for i in range(copies)]
 
-    def launch(i, ev0=None, ev1=None):
+    def launch(i):
         c = i % copies
-        if ev0 is None:
-            rc = L.viper_hip_qlinear(qtype, wp[c], spp[c], 0, G, N, K, x.data_ptr(), M, y.data_ptr(),
-                                     None, None, 0, sp)
-        else:
-            rc = L.viper_hip_qlinear_timed(qtype, wp[c], spp[c], 0, G, N, K, x.data_ptr(), M,
-                                           y.data_ptr(), None, None, 0, ev0, ev1, sp)
+        rc = L.viper_hip_qlinear(qtype, wp[c], spp[c], 0, G, N, K, x.data_ptr(), M, y.data_ptr(),
+                                 None, None, 0, torch.cuda.current_stream().cuda_stream)
         if rc != 0:
             raise RuntimeError(f"viper_hip_qlinear failed: {rc}")
 
-    # warmup (eager), then capture one graph that walks every weight copy once
     for i in range(args.warmup):
         launch(i)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(copies):
-            launch(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    replays = max(1, args.steps // copies)
+    graph, replays = capture(torch, launch, copies, args.steps)
     steps = replays * copies
-
-    # ---- timed region: whole job ------------------------------------------------
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(replays):
-        graph.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    job_ms = e0.elapsed_time(e1)
+    job_ms = time_graph(torch, graph, replays)
     ms_per_step = job_ms / steps
     value = alg * steps / (job_ms * 1e-3) / 1e9
-
-    # ---- kernel duration: events attached to each dispatch ---------------------
-    k_mean, k_med = time_kernel(torch, hip, launch, args.kernel_launches)
-    achieved = alg / (k_mean * 1e-6) / 1e9
+    achieved = value
 
     extras = {}
     if not args.no_extras:
@@ -203,18 +159,20 @@ def main():
         nws = va.workspace_bytes(qtype, N, K, M16)
         ws16 = torch.empty(nws, dtype=torch.uint8, device="cuda")
 
-        def launch16(i, ev0=None, ev1=None):
+        def launch16(i):
             c = i % copies
-            rc = L.viper_hip_qlinear_timed(qtype, wp[c], spp[c], 0, G, N, K, x16.data_ptr(), M16,
-                                           y16.data_ptr(), None, ws16.data_ptr(), nws, ev0, ev1, sp)
+            rc = L.viper_hip_qlinear(qtype, wp[c], spp[c], 0, G, N, K, x16.data_ptr(), M16, y16.data_ptr(),
+                                     None, ws16.data_ptr(), nws, torch.cuda.current_stream().cuda_stream)
             if rc != 0:
                 raise RuntimeError(f"M=16 qlinear failed: {rc}")
         for i in range(50):
             launch16(i)
-        m16_mean, m16_med = time_kernel(torch, hip, launch16, 400)
+        g16, r16 = capture(torch, launch16, copies, 400)
+        m16_us = time_graph(torch, g16, r16) * 1e3 / (r16 * copies)
         alg16 = algorithmic_bytes(K // 2, N, K, M16)
-        extras["m16_verify_gemm_us"] = round(m16_mean, 3)
-        extras["m16_verify_gemm_gbs"] = round(alg16 / (m16_mean * 1e-6) / 1e9, 1)
+        extras["m16_verify_us"] = round(m16_us, 3)
+        extras["m16_verify_gbs"] = round(alg16 / (m16_us * 1e-6) / 1e9, 1)
+        del g16
 
         # down projection shape (K=10240, N=2560), M=1, fused quantize
         Kd, Nd = 10240, 2560
@@ -224,19 +182,20 @@ def main():
         wdp = [Wd[i].data_ptr() for i in range(copies)]
         sdp = [Sd[i].data_ptr() for i in range(copies)]
 
-        def launchd(i, ev0=None, ev1=None):
+        def launchd(i):
             c = i % copies
-            rc = L.viper_hip_qlinear_timed(qtype, wdp[c], sdp[c], 0, G, Nd, Kd, xd.data_ptr(), 1,
-                                           yd.data_ptr(), None, None, 0, ev0, ev1, sp)
+            rc = L.viper_hip_qlinear(qtype, wdp[c], sdp[c], 0, G, Nd, Kd, xd.data_ptr(), 1, yd.data_ptr(),
+                                     None, None, 0, torch.cuda.current_stream().cuda_stream)
             if rc != 0:
                 raise RuntimeError(f"down qlinear failed: {rc}")
         for i in range(50):
             launchd(i)
-        d_mean, _ = time_kernel(torch, hip, launchd, 400)
+        gd, rd = capture(torch, launchd, copies, 400)
+        d_us = time_graph(torch, gd, rd) * 1e3 / (rd * copies)
         algd = algorithmic_bytes(Kd // 2, Nd, Kd, 1)
-        extras["down_k10240_n2560_us"] = round(d_mean, 3)
-        extras["down_k10240_n2560_gbs"] = round(algd / (d_mean * 1e-6) / 1e9, 1)
-        del Wd, Sd
+        extras["down_k10240_n2560_us"] = round(d_us, 3)
+        extras["down_k10240_n2560_gbs"] = round(algd / (d_us * 1e-6) / 1e9, 1)
+        del gd, Wd, Sd
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_q4_m1_k2560_n10240.json")
@@ -268,10 +227,8 @@ def main():
         "config": {"workload": "Q4_G64 GEMV M=1 K=2560 N=10240 (north star), fused bf16->int8 quantize",
                    "qtype": "Q4_G64", "M": M, "K": K, "N": N, "weight_copies": copies,
                    "rotation_bytes": copies * copy_bytes, "algorithmic_bytes_per_step": alg,
-                   "timed_region": "HIP graph replays of one launch per weight copy"},
-        "us_per_gemv_kernel": round(k_mean, 3),
-        "us_per_gemv_kernel_median": round(k_med, 3),
-        "us_per_step_whole_job": round(ms_per_step * 1e3, 3),
+                   "timed_region": "HIP graph replays, one launch per weight copy, events on the stream"},
+        "us_per_gemv": round(ms_per_step * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
