@@ -1,0 +1,96 @@
+// Host API checks that need no GPU: the closed registry (reference
+// src/viper/quant.cpp:6-20, src/viper/tensor.cpp:8-40) and the Status codes
+// linear() returns for bad arguments before any device work (reference
+// src/viper/linear.cpp:16-36; argument rules as kernels/ops/linear_multim.cu:152).
+#include <cstdio>
+#include <string>
+
+#include "viper/ops.h"
+#include "viper/quant.h"
+#include "viper/tensor.h"
+
+using namespace viper;
+
+static int failures = 0;
+#define EXPECT(cond)                                                            \
+    do {                                                                        \
+        if (!(cond)) {                                                          \
+            std::printf("FAIL %s:%d: %s\n", __FILE__, __LINE__, #cond);         \
+            ++failures;                                                         \
+        }                                                                       \
+    } while (0)
+
+int main() {
+    using quant::QType;
+    EXPECT(quant::qtype_name(QType::BF16) == "BF16");
+    EXPECT(quant::qtype_name(QType::FP32) == "FP32");
+    EXPECT(quant::qtype_name(QType::Q4_G64) == "Q4_G64");
+    EXPECT(quant::qtype_name(QType::Q5_G64) == "Q5_G64");
+    EXPECT(quant::qtype_name(QType::Q6_G64) == "Q6_G64");
+    EXPECT(quant::qtype_name(QType::W8_G32) == "W8_G32");
+    EXPECT(quant::qtype_name(static_cast<QType>(3)) == "UNKNOWN");
+    EXPECT(quant::is_lossless(QType::BF16) && quant::is_lossless(QType::FP32));
+    EXPECT(!quant::is_lossless(QType::Q4_G64) && !quant::is_lossless(QType::W8_G32));
+    EXPECT(static_cast<int>(QType::Q4_G64) == 4 && static_cast<int>(QType::W8_G32) == 8);
+    EXPECT(static_cast<int>(DType::Q4_G64) == 100 && static_cast<int>(DType::W8_G32) == 103);
+    EXPECT(std::string(dtype_name(DType::Q6_G64)) == "Q6_G64");
+    EXPECT(dtype_sizeof(DType::Q4_G64) == 1 && dtype_sizeof(DType::BF16) == 2);
+    EXPECT(quant::group_size(QType::Q5_G64) == 64 && quant::group_size(QType::W8_G32) == 32);
+    EXPECT(quant::packed_bytes(QType::Q4_G64, 10240, 2560) == 13107200);
+    EXPECT(quant::packed_bytes(QType::Q5_G64, 4, 64) == 4 * 32 + 4 * 8);
+    EXPECT(quant::packed_bytes(QType::Q6_G64, 4, 64) == 4 * 32 + 4 * 16);
+    EXPECT(quant::packed_bytes(QType::W8_G32, 4, 64) == 256);
+    EXPECT(quant::packed_bytes(QType::Q4_G64, 4, 96) == 0);
+
+    // argument validation: pointers are fake and never dereferenced
+    void* fake = reinterpret_cast<void*>(0x10000);
+    quant::QuantizedWeight w{QType::Q4_G64, fake, fake, 64, 128, 64, quant::ScaleEnc::FP16};
+    Tensor x(fake, DType::BF16, {128});
+    Tensor y(fake, DType::BF16, {64});
+    auto code = [&](const quant::QuantizedWeight& ww, const Tensor& xx, Tensor& yy) {
+        return ops::linear(ww, xx, yy).code();
+    };
+    quant::QuantizedWeight wb = w;
+    wb.qtype = QType::BF16;
+    EXPECT(code(wb, x, y) == StatusCode::UNIMPLEMENTED);
+    wb.qtype = static_cast<QType>(7);
+    EXPECT(code(wb, x, y) == StatusCode::INVALID_ARGUMENT);
+    wb = w;
+    wb.group_size = 32;
+    EXPECT(code(wb, x, y) == StatusCode::INVALID_ARGUMENT);
+    wb = w;
+    wb.cols = 96;
+    Tensor x96(fake, DType::BF16, {96});
+    EXPECT(code(wb, x96, y) == StatusCode::SHAPE_MISMATCH);
+    wb = w;
+    wb.data = nullptr;
+    EXPECT(code(wb, x, y) == StatusCode::INVALID_ARGUMENT);
+    Tensor xf(fake, DType::FP32, {128});
+    EXPECT(code(w, xf, y) == StatusCode::INVALID_ARGUMENT);
+    Tensor xw(fake, DType::BF16, {100});
+    EXPECT(code(w, xw, y) == StatusCode::SHAPE_MISMATCH);
+    Tensor y2(fake, DType::BF16, {2, 64});
+    EXPECT(code(w, x, y2) == StatusCode::SHAPE_MISMATCH);
+    Tensor x17(fake, DType::BF16, {17, 128});
+    Tensor y17(fake, DType::BF16, {17, 64});
+    EXPECT(code(w, x17, y17) == StatusCode::INVALID_ARGUMENT);
+    Tensor x4(fake, DType::BF16, {4, 128});
+    Tensor y4(fake, DType::BF16, {4, 64});
+    EXPECT(code(w, x4, y4) == StatusCode::INVALID_ARGUMENT);  // no workspace
+    EXPECT(ops::linear_workspace_bytes(w, 1) == 0);
+    EXPECT(ops::linear_workspace_bytes(w, 4) == 4 * 128 + 32);
+    Tensor misaligned(reinterpret_cast<void*>(0x10008), DType::BF16, {128});
+    EXPECT(code(w, misaligned, y) == StatusCode::INVALID_ARGUMENT);
+    Tensor wt(fake, DType::Q4_G64, {64, 128});
+    EXPECT(ops::linear_forward(wt, Tensor(), x, y).code() == StatusCode::INVALID_ARGUMENT);
+    Tensor wbf(fake, DType::BF16, {64, 128});
+    EXPECT(ops::linear_forward(wbf, Tensor(), x, y).code() == StatusCode::UNIMPLEMENTED);
+    Tensor wi(fake, DType::INT32, {64, 128});
+    EXPECT(ops::linear_forward(wi, Tensor(), x, y).code() == StatusCode::INVALID_ARGUMENT);
+    Tensor xq(fake, DType::INT8, {128}), xs(fake, DType::FP32, {2});
+    EXPECT(ops::quantize_activations(x, 48, xq, xs).code() == StatusCode::INVALID_ARGUMENT);
+    EXPECT(ops::quantize_activations(x, 64, xq, y).code() == StatusCode::INVALID_ARGUMENT);
+
+    std::printf("%s (%d failures)\n", failures ? "FAILED" : "PASS", failures);
+    return failures ? 1 : 0;
+}

@@ -1,0 +1,154 @@
+// GPU parity of the C++ host API (viper::ops) against the CPU oracle: every
+// format and scale encoding through linear() at M = 1 (fused quantize) and
+// M = 4 (workspace), quantize_activations() bit-exact, and
+// linear_prequantized() with a residual.  bf16 outputs must be within 1 bf16
+// ulp of the oracle or within 1e-5 * sum|group terms|.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "viper/ops.h"
+#include "viper_oracle.h"
+
+using namespace viper;
+
+static int failures = 0;
+#define CHECK_HIP(x)                                                                        \
+    do {                                                                                    \
+        hipError_t e_ = (x);                                                                \
+        if (e_ != hipSuccess) {                                                             \
+            std::printf("HIP error %s at %s:%d\n", hipGetErrorString(e_), __FILE__, __LINE__); \
+            return 2;                                                                       \
+        }                                                                                   \
+    } while (0)
+
+template <typename T>
+static T* upload(const std::vector<T>& h) {
+    T* d = nullptr;
+    if (hipMalloc(&d, h.size() * sizeof(T) + 16) != hipSuccess) return nullptr;
+    if (hipMemcpy(d, h.data(), h.size() * sizeof(T), hipMemcpyHostToDevice) != hipSuccess) return nullptr;
+    return d;
+}
+
+static double ulp_bf16(uint16_t h) {
+    double f = std::fabs((double)vo_bf16_to_f32(h));
+    double e = std::floor(std::log2(std::fmax(f, std::ldexp(1.0, -126))));
+    return std::ldexp(1.0, (int)e - 7);
+}
+
+static bool close_bf16(const std::vector<uint16_t>& g, const std::vector<uint16_t>& r,
+                       const std::vector<double>& absterm, const char* what) {
+    int bad = 0;
+    for (size_t i = 0; i < g.size(); ++i) {
+        double d = std::fabs((double)vo_bf16_to_f32(g[i]) - (double)vo_bf16_to_f32(r[i]));
+        double tol = std::fmax(std::fmax(ulp_bf16(r[i]), ulp_bf16(g[i])), 1e-5 * absterm[i]);
+        if (!(d <= tol)) {
+            if (bad < 3) std::printf("  %s[%zu]: gpu %g ref %g\n", what, i, vo_bf16_to_f32(g[i]), vo_bf16_to_f32(r[i]));
+            ++bad;
+        }
+    }
+    if (bad) std::printf("FAIL %s: %d of %zu outside tolerance\n", what, bad, g.size());
+    return bad == 0;
+}
+
+static int run_case(int qt, int senc, int N, int K, int M, uint64_t seed) {
+    const int G = vo_group_size(qt);
+    std::vector<uint8_t> packed(vo_packed_bytes(qt, N, K));
+    std::vector<uint16_t> scales((size_t)N * (K / G));
+    vo_gen_weights(qt, N, K, seed, senc, packed.data(), scales.data());
+    std::vector<uint16_t> x((size_t)M * K), res((size_t)M * N);
+    vo_gen_act(M, K, seed + 1, 0.05, 20.0f, x.data());
+    vo_gen_act(M, N, seed + 2, 0.0, 1.0f, res.data());
+    std::vector<uint16_t> yref((size_t)M * N), yref_r((size_t)M * N);
+    std::vector<float> yf((size_t)M * N);
+    std::vector<double> ya((size_t)M * N), ya_r((size_t)M * N);
+    vo_qlinear(qt, packed.data(), scales.data(), senc, N, K, x.data(), M, nullptr, yref.data(), yf.data(), ya.data());
+    vo_qlinear(qt, packed.data(), scales.data(), senc, N, K, x.data(), M, res.data(), yref_r.data(), yf.data(), ya_r.data());
+
+    uint8_t* dw = upload(packed);
+    uint16_t* ds = upload(scales);
+    uint16_t* dx = upload(x);
+    uint16_t* dr = upload(res);
+    uint16_t* dy = nullptr;
+    CHECK_HIP(hipMalloc(&dy, (size_t)M * N * 2));
+    if (!dw || !ds || !dx || !dr) return 2;
+
+    quant::QuantizedWeight w{static_cast<quant::QType>(qt), dw, ds, N, K, G,
+                             static_cast<quant::ScaleEnc>(senc)};
+    Tensor tx = M == 1 ? Tensor(dx, DType::BF16, {K}) : Tensor(dx, DType::BF16, {M, K});
+    Tensor ty = M == 1 ? Tensor(dy, DType::BF16, {N}) : Tensor(dy, DType::BF16, {M, N});
+    Tensor tr = M == 1 ? Tensor(dr, DType::BF16, {N}) : Tensor(dr, DType::BF16, {M, N});
+    const usize nws = ops::linear_workspace_bytes(w, M);
+    void* dws = nullptr;
+    if (nws) CHECK_HIP(hipMalloc(&dws, nws));
+    ops::LinearOptions opt;
+    opt.workspace = dws;
+    opt.workspace_bytes = nws;
+
+    char what[96];
+    std::snprintf(what, sizeof what, "linear q%d senc%d N%d K%d M%d", qt, senc, N, K, M);
+    std::printf("case %s\n", what);
+    std::fflush(stdout);
+    Status st = ops::linear(w, tx, ty, opt);
+    if (!st.ok()) {
+        std::printf("FAIL %s: status %d %.*s\n", what, (int)st.code(), (int)st.message().size(), st.message().data());
+        return 1;
+    }
+    CHECK_HIP(hipDeviceSynchronize());
+    std::vector<uint16_t> yg((size_t)M * N);
+    CHECK_HIP(hipMemcpy(yg.data(), dy, yg.size() * 2, hipMemcpyDeviceToHost));
+    int fails = close_bf16(yg, yref, ya, what) ? 0 : 1;
+
+    // residual through the same call
+    opt.residual = &tr;
+    st = ops::linear(w, tx, ty, opt);
+    if (!st.ok()) return 1;
+    CHECK_HIP(hipDeviceSynchronize());
+    CHECK_HIP(hipMemcpy(yg.data(), dy, yg.size() * 2, hipMemcpyDeviceToHost));
+    fails += close_bf16(yg, yref_r, ya_r, "linear+residual") ? 0 : 1;
+
+    // quantize_activations bit-exact, then linear_prequantized
+    std::vector<int8_t> xq_ref((size_t)M * K);
+    std::vector<float> xs_ref((size_t)M * (K / G));
+    vo_quantize_act(x.data(), M, K, G, xq_ref.data(), xs_ref.data());
+    int8_t* dxq = nullptr;
+    float* dxs = nullptr;
+    CHECK_HIP(hipMalloc(&dxq, xq_ref.size()));
+    CHECK_HIP(hipMalloc(&dxs, xs_ref.size() * 4));
+    Tensor tq(dxq, DType::INT8, {M, K}), ts(dxs, DType::FP32, {M, K / G});
+    st = ops::quantize_activations(tx, G, tq, ts);
+    if (!st.ok()) return 1;
+    CHECK_HIP(hipDeviceSynchronize());
+    std::vector<int8_t> xq_g(xq_ref.size());
+    std::vector<float> xs_g(xs_ref.size());
+    CHECK_HIP(hipMemcpy(xq_g.data(), dxq, xq_g.size(), hipMemcpyDeviceToHost));
+    CHECK_HIP(hipMemcpy(xs_g.data(), dxs, xs_g.size() * 4, hipMemcpyDeviceToHost));
+    if (std::memcmp(xq_g.data(), xq_ref.data(), xq_g.size()) || std::memcmp(xs_g.data(), xs_ref.data(), xs_g.size() * 4)) {
+        std::printf("FAIL quantize_activations not bit-exact\n");
+        ++fails;
+    }
+    ops::LinearOptions po;
+    po.residual = &tr;
+    st = ops::linear_prequantized(w, tq, ts, ty, po);
+    if (!st.ok()) return 1;
+    CHECK_HIP(hipDeviceSynchronize());
+    CHECK_HIP(hipMemcpy(yg.data(), dy, yg.size() * 2, hipMemcpyDeviceToHost));
+    fails += close_bf16(yg, yref_r, ya_r, "linear_prequantized+residual") ? 0 : 1;
+
+    for (void* p : {(void*)dw, (void*)ds, (void*)dx, (void*)dr, (void*)dy, (void*)dxq, (void*)dxs, dws})
+        if (p) (void)hipFree(p);
+    return fails;
+}
+
+int main() {
+    const int qts[] = {VO_Q4_G64, VO_Q5_G64, VO_Q6_G64, VO_W8_G32};
+    for (int qt : qts)
+        for (int senc : {0, 1})
+            for (int M : {1, 4}) failures += run_case(qt, senc, 300, 2560, M, 0x1234u + qt * 7 + senc + M);
+    failures += run_case(VO_Q4_G64, 0, 2560, 10240, 1, 99);
+    std::printf("%s (%d failures)\n", failures ? "FAILED" : "PASS", failures);
+    return failures ? 1 : 0;
+}

@@ -178,6 +178,24 @@ def test_prequantized_entry(torch_dev):
         O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
 
 
+@pytest.mark.parametrize("M", [1, 3])
+def test_residual_in_place(torch_dev, M):
+    # y aliasing the residual, as the reference engine calls its residual GEMV
+    # (include/viper/model_impl.cuh:720,728: y = residual = x_)
+    torch = torch_dev
+    N, K = 2560, 2560
+    packed, scales = O.gen_weights(O.Q4_G64, N, K, 71, O.SCALE_FP16)
+    x = O.gen_act(M, K, 72)
+    res = O.gen_act(M, N, 73)
+    y_ref, _, absterm = O.qlinear(O.Q4_G64, packed, scales, O.SCALE_FP16, N, K, x, residual=res)
+    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K)
+    yd = dev(torch, res)
+    ws = torch.zeros(max(16, va.workspace_bytes(4, N, K, M)), dtype=torch.uint8, device="cuda") if M > 1 else None
+    assert va.linear(w, dev(torch, x), yd, residual=yd, workspace=ws).ok()
+    torch.cuda.synchronize()
+    O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
+
+
 def test_zero_weight_kat(torch_dev):
     # all-0x88 Q4 bytes are all-zero weights: y is exactly the residual
     torch = torch_dev

@@ -332,8 +332,8 @@ __device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, int off) {
 template <int F, int TS, int NTT, int SENC, bool PART, bool EXACT, int DELAY>
 __global__ void __launch_bounds__(NTT)
 qgemv_m1_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws,
-                const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
-                const uint16_t* __restrict__ res, int32_t* __restrict__ part, int N, int K) {
+                const uint16_t* __restrict__ x, uint16_t* y,
+                const uint16_t* res, int32_t* __restrict__ part, int N, int K) {
     using FT = Fmt<F>;
     constexpr int CPL = M1_CPL;
     constexpr int XS = M1_XS;
@@ -496,7 +496,7 @@ template <int F, int MT, int TS>
 __global__ void __launch_bounds__(NT)
 qgemm_pre_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws, int senc,
                  const int8_t* __restrict__ xq, const float* __restrict__ xs,
-                 uint16_t* __restrict__ y, const uint16_t* __restrict__ res,
+                 uint16_t* y, const uint16_t* res,
                  int32_t* __restrict__ part, int N, int K, int M) {
     using FT = Fmt<F>;
     extern __shared__ __align__(16) uint8_t smem[];
