@@ -122,6 +122,40 @@ def test_multi_row(torch_dev, qtype, M):
     run_case(torch_dev, qtype, 77, K, M, seed=2000 + M, residual=(M % 2 == 0))
 
 
+# M = 2..16 run on the i8 matrix cores when K is a multiple of two groups:
+# one load segment per wave (K <= 40 groups per 4 waves), the double-buffered
+# loop (long K), two 16-row tiles per wave (N >= 64 tiles per CU), partial
+# tiles, and K with an odd group count (the v_dot4 path).
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("N,K,M,senc", [
+    (16, 128, 2, O.SCALE_FP16),
+    (45, 2560, 16, O.SCALE_BF16),
+    (50, 10240, 16, O.SCALE_FP16),
+    (33, 6144, 7, O.SCALE_BF16),
+    (16400, 256, 3, O.SCALE_FP16),
+    (29, 192, 4, O.SCALE_FP16),
+])
+def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
+    run_case(torch_dev, qtype, N, K, M, seed=3000 + N + M, scale_enc=senc, residual=(M % 2 == 1))
+
+
+def test_verify_m16_full_size(torch_dev):
+    # config 2: M=16 speculative verify at the north-star shape
+    run_case(torch_dev, O.Q4_G64, 10240, 2560, 16, seed=0x5EED0002)
+
+
+def test_verify_m16_down_full_size(torch_dev):
+    # M=16 at the down-projection shape: 160 KB of int8 activations, more than
+    # one workgroup's LDS, which the matrix-core path never stages
+    run_case(torch_dev, O.Q4_G64, 2560, 10240, 16, seed=0x5EED0003, residual=True)
+
+
+def test_mfma_deterministic(torch_dev):
+    a = run_case(torch_dev, O.Q5_G64, 300, 10240, 9, seed=11)
+    b = run_case(torch_dev, O.Q5_G64, 300, 10240, 9, seed=11)
+    np.testing.assert_array_equal(a, b)
+
+
 @pytest.mark.parametrize("qtype", FORMATS)
 def test_residual_and_outliers(torch_dev, qtype):
     run_case(torch_dev, qtype, 130, 2560, 1, seed=31, residual=True, outlier=0.05)
@@ -160,11 +194,12 @@ def test_row_matches_single_row_call(torch_dev):
         np.testing.assert_array_equal(p1.cpu().numpy()[0], pm.cpu().numpy()[m])
 
 
-def test_prequantized_entry(torch_dev):
+@pytest.mark.parametrize("N,K,M", [(200, 2560, 3), (70, 10240, 16), (40, 192, 2)])
+def test_prequantized_entry(torch_dev, N, K, M):
+    # activations in viper_hip_quantize_act's layout ([M][K] int8, [M][K/G] fp32)
     torch = torch_dev
     for qtype in FORMATS:
         G = O.group_size(qtype)
-        N, K, M = 200, 2560, 3
         packed, scales = O.gen_weights(qtype, N, K, 40 + qtype, O.SCALE_BF16)
         x = O.gen_act(M, K, 41)
         xq, xs = O.quantize_act(x, G)

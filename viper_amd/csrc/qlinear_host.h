@@ -1,0 +1,94 @@
+// Host-side helpers and the launchers each kernel translation unit provides.
+#pragma once
+
+#include <hip/hip_ext.h>
+
+#include "qlinear_dev.h"
+
+namespace vq {
+
+// ------------------------------------------------------------------ host side
+
+inline int status_of(hipError_t e) {
+    if (e == hipSuccess) return VIPER_OK;
+    if (e == hipErrorOutOfMemory) return VIPER_OUT_OF_MEMORY;
+    return VIPER_DEVICE_ERROR;
+}
+
+inline int group_of(int qtype) {
+    switch (qtype) {
+        case VIPER_QTYPE_Q4_G64:
+        case VIPER_QTYPE_Q5_G64:
+        case VIPER_QTYPE_Q6_G64: return 64;
+        case VIPER_QTYPE_W8_G32: return 32;
+        default: return 0;
+    }
+}
+
+inline size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+
+// LDS of the prequantized kernel for M rows
+inline size_t lds_pre(int qtype, int M, int K) {
+    const size_t G = (size_t)group_of(qtype);
+    size_t b = (size_t)M * K + (size_t)M * (K / G) * 4;
+    if (qtype != VIPER_QTYPE_W8_G32) b += (size_t)M * (K / 32) * 4;
+    return b;
+}
+
+inline bool misaligned(const void* p, size_t a) { return ((uintptr_t)p % a) != 0; }
+
+inline int validate_weights(int qtype, const void* w, const void* s, int senc, int group, int N,
+                            int K, int M) {
+    if (qtype == VIPER_QTYPE_BF16 || qtype == VIPER_QTYPE_FP32) return VIPER_UNIMPLEMENTED;
+    const int G = group_of(qtype);
+    if (G == 0) return VIPER_INVALID_ARGUMENT;
+    if (w == nullptr || s == nullptr) return VIPER_INVALID_ARGUMENT;
+    if (senc != VIPER_SCALE_FP16 && senc != VIPER_SCALE_BF16) return VIPER_INVALID_ARGUMENT;
+    if (group != G) return VIPER_INVALID_ARGUMENT;
+    if (N <= 0 || K <= 0 || M <= 0 || M > VIPER_QLINEAR_MAX_M) return VIPER_INVALID_ARGUMENT;
+    if (K % G != 0) return VIPER_INVALID_ARGUMENT;
+    if ((int64_t)M * K > INT32_MAX / 2) return VIPER_INVALID_ARGUMENT;
+    if (misaligned(w, 16) || misaligned(s, 2)) return VIPER_INVALID_ARGUMENT;
+    return VIPER_OK;
+}
+
+inline void launch(const void* fn, unsigned grid, unsigned block, size_t lds, hipStream_t st,
+                   void** args, hipEvent_t ev0, hipEvent_t ev1) {
+    // Events (when given) are attached to this dispatch, so they time the
+    // kernel itself rather than the host-side launch.
+    if (ev0 == nullptr && ev1 == nullptr)
+        (void)hipLaunchKernel(fn, dim3(grid), dim3(block), args, lds, st);
+    else
+        (void)hipExtLaunchKernel(fn, dim3(grid), dim3(block), args, lds, st, ev0, ev1, 0);
+}
+
+inline int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        return 256;
+    return cus;
+}
+
+// ---- launchers (one translation unit each)
+
+// M = 1 with the activation quantize fused (qgemv_m1.hip).
+size_t lds_m1(int qtype, int K);
+int launch_m1(int qtype, const void* w, const void* s, int senc, int N, int K, const void* x, void* y,
+              const void* res, int32_t* part, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
+
+// M <= 16 over prequantized activations, v_dot4 (qgemm_pre.hip).
+int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
+               const void* xs, int M, void* y, const void* res, int32_t* part, hipStream_t st,
+               hipEvent_t ev0, hipEvent_t ev1);
+
+// M = 2..16 on the i8 matrix cores (qgemm_mfma.hip): needs K a multiple of
+// two groups and 4-byte aligned scales.  xnat: activations in the layout of
+// viper_hip_quantize_act, else in the layout quantize_act_kernel<G, true>
+// writes.
+bool mfma_ok(int qtype, int K, int M, const void* s);
+int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
+                const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
+                hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
+
+}  // namespace vq
