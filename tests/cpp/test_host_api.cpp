@@ -78,7 +78,7 @@ int main() {
     Tensor y4(fake, DType::BF16, {4, 64});
     EXPECT(code(w, x4, y4) == StatusCode::INVALID_ARGUMENT);  // no workspace
     EXPECT(ops::linear_workspace_bytes(w, 1) == 0);
-    EXPECT(ops::linear_workspace_bytes(w, 4) == 4 * 128 + 2 * 16 * 4);  // xq, then xs for 16 rows
+    EXPECT(ops::linear_workspace_bytes(w, 4) == 16 * 128 + 2 * 16 * 4);  // xq, xs for 16 rows
     Tensor misaligned(reinterpret_cast<void*>(0x10008), DType::BF16, {128});
     EXPECT(code(w, misaligned, y) == StatusCode::INVALID_ARGUMENT);
     Tensor wt(fake, DType::Q4_G64, {64, 128});

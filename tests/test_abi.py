@@ -35,10 +35,10 @@ def test_group_sizes_and_workspace():
     L = va.lib()
     assert [L.viper_hip_group_size(q) for q in (4, 5, 6, 8, 0, 1, 7)] == [64, 64, 64, 32, 0, 0, 0]
     assert va.workspace_bytes(4, 10240, 2560, 1) == 0
-    # xq [M][K] int8 (16-byte aligned), then xs with room for 16 rows per group
-    assert va.workspace_bytes(4, 10240, 2560, 4) == 4 * 2560 + 40 * 16 * 4
-    assert va.workspace_bytes(8, 10, 2560, 3) == 3 * 2560 + 80 * 16 * 4
-    assert va.workspace_bytes(6, 10, 2496, 3) == ((3 * 2496 + 15) // 16) * 16 + 39 * 16 * 4
+    # int8 activations with room for 16 rows, then fp32 scales for 16 rows per group
+    assert va.workspace_bytes(4, 10240, 2560, 4) == 16 * 2560 + 40 * 16 * 4
+    assert va.workspace_bytes(8, 10, 2560, 3) == 16 * 2560 + 80 * 16 * 4
+    assert va.workspace_bytes(6, 10, 2496, 3) == 16 * 2496 + 39 * 16 * 4
 
 
 FAKE = 0x10000  # never dereferenced: every call below fails validation first

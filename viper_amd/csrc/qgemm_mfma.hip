@@ -41,12 +41,22 @@ namespace vq {
 // double-buffered segments of the looping variant (two sets in registers).
 constexpr int MF_PS_ONE = 5;
 constexpr int MF_PS_LOOP = 3;
+// 16-byte staging loads per thread for the activation scales (SLX) and the
+// weight scales (SLW) of the staged variant.
+constexpr int MF_SLX = 3;
+constexpr int MF_SLW = 2;
 
-// Activation layouts the kernel reads.  XNAT: xq [M][K] int8 in k order and
-// xs [M][K/G] fp32 (the layout of viper_hip_quantize_act).  Otherwise the
-// layout quantize_act_kernel<G, true> writes for this kernel: xq [M][K] with
-// the octets of the nibble formats stored as [even k | odd k], and xs as
-// [K/G][16] fp32 (entries for rows m >= M are never read into an output).
+// Activation layouts.
+//  * natural (XNAT): xq [M][K] int8 in k order, xs [M][K/G] fp32, the layout
+//    of viper_hip_quantize_act and of the prequantized entry point; the kernel
+//    gathers fragments and scales with per-lane loads.
+//  * fragment order (written by quantize_act_kernel<G, true>): for group g,
+//    k-slot kb and row m, the lane's 16 (W8: 8) int8 at
+//    ((g * 4 + kb) * 16 + m) * Q, octets of the nibble formats stored as
+//    [even k | odd k]; one wave instruction reads a group's fragments as one
+//    contiguous 1 KB (512 B).  xs as [K/G][16] fp32.  Both scale arrays are
+//    staged into LDS once per workgroup with contiguous loads.
+// Rows m >= M of either layout are never read into an output.
 
 __device__ __forceinline__ void lane_swap32(uint32_t& a, uint32_t& b) {
     // lanes 32..63 of a <-> lanes 0..31 of b
@@ -76,14 +86,21 @@ __device__ __forceinline__ float scale_f(uint32_t h, int senc) {
 template <int F, int T, int PS>
 struct MfSeg {
     u32x4 a[PS][2];    // activation fragments of groups 2p, 2p+1
-    u32x4 xs[PS][2];   // xs of rows 4*kb + r, groups 2p, 2p+1
+    u32x4 xs[PS][2];   // natural layout: xs of rows 4*kb + r, groups 2p, 2p+1
     u32x4 w[PS][T];    // weight chunk 4p + kb of each tile row
     uint32_t h0[PS][T], h1[PS][T];  // its high-plane words (Q5, Q6)
-    uint32_t s[PS][T];  // weight scales of groups 2p (low half) and 2p+1
+    uint32_t s[PS][T];  // natural layout: weight scales of groups 2p (low half), 2p+1
 };
 
+// LDS of the staged variant: [red W*T*1 KB][xs NG*64][weight scales 16T*NG*2 + 16]
+__host__ __device__ constexpr size_t mf_lds_bytes(bool xnat, int W, int T, int NG) {
+    return (size_t)W * T * 1024 + (xnat ? 0 : (size_t)NG * 64 + (size_t)16 * T * NG * 2 + 16);
+}
+
 // ONE: every wave's pairs fit one segment (ceil(NP / W) <= MF_PS_ONE).
-template <int F, int T, int W, bool ONE, bool XNAT>
+// XNAT: natural activation layout (else fragment order, scales staged in LDS).
+// PART: also store every int32 group dot (test and debug entry point).
+template <int F, int T, int W, bool ONE, bool XNAT, bool PART>
 __global__ void __launch_bounds__(64 * W)
 qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws, int senc,
                   const int8_t* __restrict__ xq, const float* __restrict__ xs,
@@ -95,10 +112,12 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
     constexpr int HB = FT::HIW * 4;   // high-plane bytes per chunk
     constexpr int QB = NIB ? 16 : 8;  // activation bytes per lane per group
     constexpr uint32_t BOFF = (uint32_t)(uint8_t)(-FT::OFF) * 0x01010101u;
-    extern __shared__ __align__(16) float red[];  // [W][T][4][64]
+    extern __shared__ __align__(16) uint8_t smem[];
+    float* red = (float*)smem;  // [W][T][4][64]
 
-    const int lane = (int)threadIdx.x & 63;
-    const int wave = (int)threadIdx.x >> 6;
+    const int tid = (int)threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
     const int nl = lane & 15, kb = lane >> 4;
     const int NG = K / FT::G;
     const int NP = NG / 2;
@@ -110,14 +129,30 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
     const uint32_t rbytes = (uint32_t)CPR * 16;
     const auto wr = buf(w + (size_t)row0 * rbytes, (uint32_t)nrows * rbytes);
     const auto hr = buf(w + (size_t)N * (K / 2) + (size_t)row0 * CPR * HB, (uint32_t)(nrows * CPR * HB));
-    const auto sr = buf(ws + (size_t)row0 * NG, (uint32_t)(nrows * NG) * 2);
-    const auto xr = buf(xq, (uint32_t)(M * K));
-    const auto xsr = buf(xs, XNAT ? (uint32_t)(M * NG) * 4 : (uint32_t)NG * 64);
-    const int qoff = QB * (2 * (kb & 1) + (kb >> 1));
     const bool m_ok = nl < M;
 
-    // Activations and their scales first (cache hits, the first data every
-    // pair needs), then the weight stream; loads retire in issue order.
+    // Staged variant: the workgroup's activation scales and weight-scale rows
+    // are contiguous blocks; their loads go first (they are the first data
+    // every pair needs), then every activation fragment and weight chunk.
+    float* lxs = (float*)(smem + (size_t)W * T * 1024);
+    uint8_t* lws = smem + (size_t)W * T * 1024 + (size_t)NG * 64;
+    const uintptr_t wsa = (uintptr_t)(ws + (size_t)row0 * NG);
+    const int wsd = (int)(wsa & 15);  // the block's offset in its first 16 bytes
+    u32x4 stx[MF_SLX], stw[MF_SLW];
+    if constexpr (!XNAT) {
+        const auto xsr = buf(xs, (uint32_t)NG * 64);
+        const auto sr = buf((const void*)(wsa - wsd), (uint32_t)(wsd + nrows * NG * 2));
+#pragma unroll
+        for (int i = 0; i < MF_SLX; ++i) stx[i] = bload16(xsr, (tid + 64 * W * i) * 16);
+#pragma unroll
+        for (int i = 0; i < MF_SLW; ++i) stw[i] = bload16(sr, (tid + 64 * W * i) * 16);
+    }
+
+    const auto xr = buf(xq, XNAT ? (uint32_t)(M * K) : (uint32_t)NG * 64 * QB);
+    const auto xsr_nat = buf(xs, (uint32_t)(M * NG) * 4);
+    const auto sr_nat = buf(ws + (size_t)row0 * NG, (uint32_t)(nrows * NG) * 2);
+    const int qoff = QB * (2 * (kb & 1) + (kb >> 1));
+
     auto load = [&](MfSeg<F, T, PS>& S, int seg) {
 #pragma unroll
         for (int j = 0; j < PS; ++j) {
@@ -126,7 +161,9 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int g = 2 * p + h;
-                const int ao = (pok && m_ok) ? nl * K + g * FT::G + qoff : OOB;
+                int ao;
+                if constexpr (XNAT) ao = (pok && m_ok) ? nl * K + g * FT::G + qoff : OOB;
+                else ao = (pok && m_ok) ? (g * 64 + lane) * QB : OOB;
                 if constexpr (NIB) {
                     S.a[j][h] = bload16(xr, ao);
                 } else {
@@ -137,24 +174,17 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
                     uint32_t v[4];
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        v[r] = bload4(xsr, (pok && 4 * kb + r < M) ? ((4 * kb + r) * NG + g) * 4 : OOB);
+                        v[r] = bload4(xsr_nat, (pok && 4 * kb + r < M) ? ((4 * kb + r) * NG + g) * 4 : OOB);
                     S.xs[j][h] = u32x4{v[0], v[1], v[2], v[3]};
-                } else {
-                    S.xs[j][h] = bload16(xsr, pok ? (g * 16 + 4 * kb) * 4 : OOB);
                 }
             }
-        }
-#pragma unroll
-        for (int j = 0; j < PS; ++j) {
-            const int p = wave + W * (seg * PS + j);
-            const bool pok = p < NP;
 #pragma unroll
             for (int t = 0; t < T; ++t) {
                 const int nr = 16 * t + nl;
                 const bool ok = pok && nr < nrows;
                 const int c = 4 * p + kb;
                 S.w[j][t] = bload16<AUX_NT>(wr, ok ? nr * (int)rbytes + c * 16 : OOB);
-                S.s[j][t] = bload4(sr, ok ? (nr * NG + 2 * p) * 2 : OOB);
+                if constexpr (XNAT) S.s[j][t] = bload4(sr_nat, ok ? (nr * NG + 2 * p) * 2 : OOB);
                 S.h0[j][t] = 0u;
                 S.h1[j][t] = 0u;
                 if constexpr (FT::HIW == 1) {
@@ -180,6 +210,7 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
             const int p = wave + W * (seg * PS + j);
             if (p < NP) {
                 i32x4 A[2], C0[2];
+                u32x4 xv[2];
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     A[h] = as_i32x4((XNAT && NIB) ? octet_perm(S.a[j][h]) : S.a[j][h]);
@@ -187,6 +218,8 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
                     if constexpr (FT::OFF != 0)
                         C0[h] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                             A[h], i32x4{(int)BOFF, (int)BOFF, (int)BOFF, (int)BOFF}, C0[h], 0, 0, 0);
+                    if constexpr (XNAT) xv[h] = S.xs[j][h];
+                    else xv[h] = *(const u32x4*)(lxs + (2 * p + h) * 16 + 4 * kb);
                 }
 #pragma unroll
                 for (int t = 0; t < T; ++t) {
@@ -211,20 +244,24 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
                             as_i64((uint32_t)A[1].x, (uint32_t)A[1].y), as_i64(wd[2], wd[3]), C0[1], 0, 0, 0);
                     }
                     const int n = row0 + 16 * t + nl;
+                    uint32_t sv;
+                    if constexpr (XNAT) sv = S.s[j][t];
+                    else sv = *(const uint32_t*)(lws + wsd + ((16 * t + nl) * NG + 2 * p) * 2);
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
-                        const float wsf = scale_f(h ? (S.s[j][t] >> 16) : (S.s[j][t] & 0xffffu), senc);
-                        const u32x4 xv = S.xs[j][h];
-                        const float xf[4] = {__uint_as_float(xv.x), __uint_as_float(xv.y),
-                                             __uint_as_float(xv.z), __uint_as_float(xv.w)};
+                        const float wsf = scale_f(h ? (sv >> 16) : (sv & 0xffffu), senc);
+                        const float xf[4] = {__uint_as_float(xv[h].x), __uint_as_float(xv[h].y),
+                                             __uint_as_float(xv[h].z), __uint_as_float(xv[h].w)};
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
                             acc[t][r] = __builtin_fmaf(wsf * xf[r], (float)C[h][r], acc[t][r]);
-                        if (part != nullptr && n < N) {
-                            const int g = 2 * p + h;
+                        if constexpr (PART) {
+                            if (n < N) {
+                                const int g = 2 * p + h;
 #pragma unroll
-                            for (int r = 0; r < 4; ++r)
-                                if (4 * kb + r < M) part[((size_t)(4 * kb + r) * N + n) * NG + g] = C[h][r];
+                                for (int r = 0; r < 4; ++r)
+                                    if (4 * kb + r < M) part[((size_t)(4 * kb + r) * N + n) * NG + g] = C[h][r];
+                            }
                         }
                     }
                 }
@@ -232,13 +269,32 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
         }
     };
 
+    auto stage = [&]() {
+        if constexpr (!XNAT) {
+            const int nws = (wsd + nrows * NG * 2 + 15) / 16;
+#pragma unroll
+            for (int i = 0; i < MF_SLX; ++i) {
+                const int u = tid + 64 * W * i;
+                if (u < NG * 4) *(u32x4*)((uint8_t*)lxs + u * 16) = stx[i];
+            }
+#pragma unroll
+            for (int i = 0; i < MF_SLW; ++i) {
+                const int u = tid + 64 * W * i;
+                if (u < nws) *(u32x4*)(lws + u * 16) = stw[i];
+            }
+            lds_barrier();
+        }
+    };
+
     if constexpr (ONE) {
         MfSeg<F, T, PS> S;
         load(S, 0);
+        stage();
         compute(S, 0);
     } else {
         MfSeg<F, T, PS> S0, S1;
         load(S0, 0);
+        stage();
         for (int seg = 0; seg < nseg; seg += 2) {
             load(S1, seg + 1);  // past the last segment every load is out of range: no traffic
             compute(S0, seg);
@@ -276,18 +332,22 @@ struct MfShape {
     int t, w;
 };
 
-template <int F, bool ONE, bool XNAT>
+template <int F, bool ONE, bool XNAT, bool PART>
 static mf_fn mf_kernel_v(int t, int w) {
 #define VQ_MF(T_, W_) \
-    if (t == T_ && w == W_) return qgemm_mfma_kernel<F, T_, W_, ONE, XNAT>;
+    if (t == T_ && w == W_) return qgemm_mfma_kernel<F, T_, W_, ONE, XNAT, PART>;
     VQ_MF(1, 4) VQ_MF(1, 8) VQ_MF(2, 4) VQ_MF(2, 8)
 #undef VQ_MF
     return nullptr;
 }
+template <int F, bool PART>
+static mf_fn mf_kernel_p(int t, int w, bool one, bool xnat) {
+    if (one) return xnat ? mf_kernel_v<F, true, true, PART>(t, w) : mf_kernel_v<F, true, false, PART>(t, w);
+    return xnat ? mf_kernel_v<F, false, true, PART>(t, w) : mf_kernel_v<F, false, false, PART>(t, w);
+}
 template <int F>
-static mf_fn mf_kernel(int t, int w, bool one, bool xnat) {
-    if (one) return xnat ? mf_kernel_v<F, true, true>(t, w) : mf_kernel_v<F, true, false>(t, w);
-    return xnat ? mf_kernel_v<F, false, true>(t, w) : mf_kernel_v<F, false, false>(t, w);
+static mf_fn mf_kernel(int t, int w, bool one, bool xnat, bool part) {
+    return part ? mf_kernel_p<F, true>(t, w, one, xnat) : mf_kernel_p<F, false>(t, w, one, xnat);
 }
 
 // Tiles of 16 rows per workgroup and waves per workgroup: two tiles per wave
@@ -305,23 +365,40 @@ bool mfma_ok(int qtype, int K, int M, const void* s) {
     return M >= 2 && G != 0 && K % (2 * G) == 0 && !misaligned(s, 4);
 }
 
+// The staged variant holds the workgroup's scales in LDS and loads them with
+// MF_SLX + MF_SLW 16-byte loads per thread.
+static bool staged_fits(int NG, MfShape sh) {
+    const int nthr = 64 * sh.w;
+    return NG * 4 <= MF_SLX * nthr && (16 * sh.t * NG * 2 + 16 + 15) / 16 <= MF_SLW * nthr &&
+           mf_lds_bytes(false, sh.w, sh.t, NG) <= (size_t)LDS_MAX;
+}
+
+bool mfma_staged(int qtype, int N, int K) {
+    const int G = group_of(qtype);
+    if (G == 0) return false;
+    const int NG = K / G;
+    return staged_fits(NG, mf_shape(N, NG / 2, device_cus()));
+}
+
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
                 hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     if (!mfma_ok(qtype, K, M, s)) return VIPER_INTERNAL;
-    const int NP = K / group_of(qtype) / 2;
+    const int NG = K / group_of(qtype);
+    const int NP = NG / 2;
     const MfShape sh = mf_shape(N, NP, device_cus());
+    if (!xnat && !staged_fits(NG, sh)) return VIPER_INTERNAL;
     const bool one = (NP + sh.w - 1) / sh.w <= MF_PS_ONE;
     mf_fn fn;
     switch (qtype) {
-        case VIPER_QTYPE_Q4_G64: fn = mf_kernel<4>(sh.t, sh.w, one, xnat); break;
-        case VIPER_QTYPE_Q5_G64: fn = mf_kernel<5>(sh.t, sh.w, one, xnat); break;
-        case VIPER_QTYPE_Q6_G64: fn = mf_kernel<6>(sh.t, sh.w, one, xnat); break;
-        default: fn = mf_kernel<8>(sh.t, sh.w, one, xnat); break;
+        case VIPER_QTYPE_Q4_G64: fn = mf_kernel<4>(sh.t, sh.w, one, xnat, part != nullptr); break;
+        case VIPER_QTYPE_Q5_G64: fn = mf_kernel<5>(sh.t, sh.w, one, xnat, part != nullptr); break;
+        case VIPER_QTYPE_Q6_G64: fn = mf_kernel<6>(sh.t, sh.w, one, xnat, part != nullptr); break;
+        default: fn = mf_kernel<8>(sh.t, sh.w, one, xnat, part != nullptr); break;
     }
     if (fn == nullptr) return VIPER_INTERNAL;
     const unsigned grid = (unsigned)((N + 16 * sh.t - 1) / (16 * sh.t));
-    const size_t lds = (size_t)sh.w * sh.t * 4 * 64 * sizeof(float);
+    const size_t lds = mf_lds_bytes(xnat, sh.w, sh.t, NG);
     const uint8_t* a0 = (const uint8_t*)w;
     const uint16_t* a1 = (const uint16_t*)s;
     const int8_t* a3 = (const int8_t*)xq;

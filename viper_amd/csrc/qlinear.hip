@@ -39,9 +39,9 @@ namespace vq {
 
 // ------------------------------------------------ standalone activation quantize
 
-// MF: the layout qgemm_mfma_kernel reads (octets of 64-groups stored as
-// [even k | odd k], xs transposed to [K/G][16]); else xq [M][K] in k order and
-// xs [M][K/G].
+// MF: the fragment order qgemm_mfma_kernel reads (octets of 64-groups stored
+// as [even k | odd k], xs transposed to [K/G][16]); else xq [M][K] in k order
+// and xs [M][K/G].
 template <int G, bool MF>
 __global__ void __launch_bounds__(NT)
 quantize_act_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ xq,
@@ -54,14 +54,21 @@ quantize_act_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ xq,
     float s;
     quantize_octet<G, MF && G == 64>(v, d0, d1, s);
     if (ok) {
-        *(u32x2*)(xq + (size_t)o * 8) = u32x2{d0, d1};
-        if ((o & (G / 8 - 1)) == 0) {
-            if constexpr (MF) {
-                const int opr = K / 8;
-                xs[((o % opr) / (G / 8)) * 16 + o / opr] = s;
-            } else {
-                xs[(size_t)o * 8 / G] = s;
-            }
+        if constexpr (MF) {
+            // group g, k-slot kb of the octet's quarter, row m (matrix-core
+            // fragment order: quarter qi of a group sits in k-slot
+            // kb = bit-swap(qi), Q bytes per fragment)
+            constexpr int Q = G == 64 ? 16 : 8;
+            const int opr = K / 8;
+            const int m = o / opr, og = o % opr;
+            const int g = og / (G / 8), k0 = (og % (G / 8)) * 8;
+            const int qi = k0 / Q;
+            const int kb = ((qi & 1) << 1) | (qi >> 1);
+            *(u32x2*)(xq + ((size_t)(g * 4 + kb) * 16 + m) * Q + k0 % Q) = u32x2{d0, d1};
+            if ((o & (G / 8 - 1)) == 0) xs[g * 16 + m] = s;
+        } else {
+            *(u32x2*)(xq + (size_t)o * 8) = u32x2{d0, d1};
+            if ((o & (G / 8 - 1)) == 0) xs[(size_t)o * 8 / G] = s;
         }
     }
 }
@@ -118,8 +125,9 @@ static size_t workspace_need(int qtype, int K, int M) {
     const int G = group_of(qtype);
     if (G == 0 || M <= 0 || K <= 0) return 0;
     if (fused_ok(qtype, M, K)) return 0;
-    // xq [M][K], then xs: [M][K/G] or (matrix-core path) [K/G][16] fp32
-    return align16((size_t)M * K) + (size_t)(K / G) * 16 * 4;
+    // xq ([M][K], or fragment order with room for 16 rows), then xs ([M][K/G],
+    // or [K/G][16]) fp32
+    return align16((size_t)16 * K) + (size_t)(K / G) * 16 * 4;
 }
 
 static int qlinear_common(int qtype, const void* w, const void* s, int senc, int group, int N,
@@ -136,12 +144,13 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     const size_t need = workspace_need(qtype, K, M);
     if (wsp == nullptr || wsp_bytes < need || misaligned(wsp, 16)) return VIPER_INVALID_ARGUMENT;
     const bool mf = mfma_ok(qtype, K, M, s);
+    const bool staged = mf && mfma_staged(qtype, N, K);
     if (!mf && lds_pre(qtype, M, K) > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
     uint8_t* xq = (uint8_t*)wsp;
-    float* xs = (float*)(xq + align16((size_t)M * K));
-    rc = launch_quantize(group, x, M, K, xq, xs, mf, st);
+    float* xs = (float*)(xq + align16((size_t)16 * K));
+    rc = launch_quantize(group, x, M, K, xq, xs, staged, st);
     if (rc != VIPER_OK) return rc;
-    if (mf) return launch_mfma(qtype, w, s, senc, N, K, xq, xs, false, M, y, res, part, st, ev0, ev1);
+    if (mf) return launch_mfma(qtype, w, s, senc, N, K, xq, xs, !staged, M, y, res, part, st, ev0, ev1);
     return launch_pre(qtype, w, s, senc, N, K, xq, xs, M, y, res, part, st, ev0, ev1);
 }
 

@@ -84,9 +84,10 @@ int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K, 
 
 // M = 2..16 on the i8 matrix cores (qgemm_mfma.hip): needs K a multiple of
 // two groups and 4-byte aligned scales.  xnat: activations in the layout of
-// viper_hip_quantize_act, else in the layout quantize_act_kernel<G, true>
-// writes.
+// viper_hip_quantize_act, else in the fragment order quantize_act_kernel<G,
+// true> writes, which the shape must support (mfma_staged).
 bool mfma_ok(int qtype, int K, int M, const void* s);
+bool mfma_staged(int qtype, int N, int K);
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
                 hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
