@@ -25,6 +25,13 @@
  *                                   (kernels/ops/dp4a_smem_kernel.h:10-20) and
  *                                   linear_q4_dp4a_prequantized{,_residual}
  *                                   (kernels/ops/linear_multim.h:30-41).
+ *   viper_hip_qlinear_fused2_prequantized
+ *                                   dp4a_smem_gemv_fused2 (kernels/ops/dp4a_smem_kernel.cu:141-152,
+ *                                   declared kernels/ops/dp4a_smem_kernel.h:22-27):
+ *                                   two matrices of one shape (k and v, gate and up,
+ *                                   include/viper/model_impl.cuh:652,725) on one
+ *                                   quantized activation in one launch.
+ *   viper_hip_qlinear_fused2        the same from bf16 x (quantize fused at M = 1).
  *   viper_hip_qlinear_partials      no counterpart: the same kernels, also writing
  *                                   the exact per-group int32 dots for parity tests.
  *   viper_hip_qlinear_timed         no counterpart: viper_hip_qlinear with events
@@ -81,7 +88,7 @@ extern "C" {
 #define VIPER_SCALE_BF16 1
 
 #define VIPER_QLINEAR_MAX_M 16
-#define VIPER_QLINEAR_ABI_VERSION 1
+#define VIPER_QLINEAR_ABI_VERSION 2
 
 int viper_hip_abi_version(void);
 
@@ -111,6 +118,22 @@ int viper_hip_qlinear_prequantized(int qtype, const void* w_packed, const void* 
                                    int scale_enc, int group, int N, int K, const void* xq,
                                    const void* xs, int M, void* y_bf16,
                                    const void* residual_bf16, void* stream);
+
+/* y0 = linear(w0, x) and y1 = linear(w1, x) for two weight matrices of the
+ * same qtype, scale encoding and shape, in one launch; no residual.  The
+ * workspace is that of viper_hip_qlinear for (qtype, N, K, M). */
+int viper_hip_qlinear_fused2(int qtype, const void* w0_packed, const void* w0_scales,
+                             const void* w1_packed, const void* w1_scales, int scale_enc, int group,
+                             int N, int K, const void* x_bf16, int M, void* y0_bf16, void* y1_bf16,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* viper_hip_qlinear_fused2 from already quantized activations (as
+ * viper_hip_qlinear_prequantized). */
+int viper_hip_qlinear_fused2_prequantized(int qtype, const void* w0_packed, const void* w0_scales,
+                                          const void* w1_packed, const void* w1_scales,
+                                          int scale_enc, int group, int N, int K, const void* xq,
+                                          const void* xs, int M, void* y0_bf16, void* y1_bf16,
+                                          void* stream);
 
 /* viper_hip_qlinear with two caller-created hipEvent_t attached to the GEMV
  * dispatch (measurement use: they bracket the kernel's own execution, not

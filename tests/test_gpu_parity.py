@@ -213,6 +213,71 @@ def test_prequantized_entry(torch_dev, N, K, M):
         O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
 
 
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("N,K", [(2560, 2560), (61, 10240)])
+def test_prequantized_m1(torch_dev, qtype, N, K):
+    # M = 1 from int8 activations: the M = 1 kernel's prequantized prologue
+    torch = torch_dev
+    G = O.group_size(qtype)
+    packed, scales = O.gen_weights(qtype, N, K, 50 + qtype, O.SCALE_FP16)
+    xq, xs = O.quantize_act(O.gen_act(1, K, 51, outlier_frac=0.05, outlier_mul=20.0), G)
+    res = O.gen_act(1, N, 52)
+    y_ref, _, absterm = O.qlinear_prequant(qtype, packed, scales, O.SCALE_FP16, N, K, xq, xs, residual=res)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G)
+    yd = torch.zeros((1, N), dtype=torch.int16, device="cuda")
+    assert va.linear_prequantized(w, dev(torch, xq), dev(torch, xs), yd, residual=dev(torch, res)).ok()
+    torch.cuda.synchronize()
+    O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
+
+
+# Two matrices of one shape on one activation in one launch (the reference's
+# fused2 for k/v and gate/up): M = 1 (fused quantize), M > 1 (matrix cores),
+# K with an odd group count (two v_dot4 launches).
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("N,K,M", [(300, 2560, 1), (70, 2560, 16), (33, 192, 3)])
+@pytest.mark.parametrize("prequantized", [False, True])
+def test_fused2(torch_dev, qtype, N, K, M, prequantized):
+    torch = torch_dev
+    G = O.group_size(qtype)
+    note(f"fused2 qtype={qtype} N={N} K={K} M={M} pre={prequantized}")
+    p0, s0 = O.gen_weights(qtype, N, K, 60 + qtype, O.SCALE_BF16)
+    p1, s1 = O.gen_weights(qtype, N, K, 70 + qtype, O.SCALE_BF16)
+    x = O.gen_act(M, K, 61)
+    xq, xs = O.quantize_act(x, G)
+    refs = [O.qlinear_prequant(qtype, p, sc, O.SCALE_BF16, N, K, xq, xs) for p, sc in ((p0, s0), (p1, s1))]
+    w0 = va.QuantizedWeight(va.QType(qtype), dev(torch, p0), dev(torch, s0), N, K, G, va.ScaleEnc.BF16)
+    w1 = va.QuantizedWeight(va.QType(qtype), dev(torch, p1), dev(torch, s1), N, K, G, va.ScaleEnc.BF16)
+    y0 = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    y1 = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    if prequantized:
+        st = va.linear_fused2_prequantized(w0, w1, dev(torch, xq), dev(torch, xs), y0, y1)
+    else:
+        nws = va.workspace_bytes(qtype, N, K, M)
+        ws = torch.zeros(max(16, nws), dtype=torch.uint8, device="cuda") if nws else None
+        st = va.linear_fused2(w0, w1, dev(torch, x), y0, y1, workspace=ws)
+    assert st.ok(), st
+    torch.cuda.synchronize()
+    for yd, (y_ref, _, absterm) in zip((y0, y1), refs):
+        O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
+
+
+def test_fused2_matches_two_calls(torch_dev):
+    # bit-identical to two single-matrix calls
+    torch = torch_dev
+    N, K, M = 512, 2560, 1
+    mats = [O.gen_weights(O.Q4_G64, N, K, s, O.SCALE_FP16) for s in (81, 82)]
+    ws = [va.QuantizedWeight(va.QType.Q4_G64, dev(torch, p), dev(torch, sc), N, K) for p, sc in mats]
+    x = dev(torch, O.gen_act(M, K, 83))
+    ya = [torch.zeros((M, N), dtype=torch.int16, device="cuda") for _ in range(2)]
+    yb = [torch.zeros((M, N), dtype=torch.int16, device="cuda") for _ in range(2)]
+    assert va.linear_fused2(ws[0], ws[1], x, ya[0], ya[1]).ok()
+    for w, y in zip(ws, yb):
+        assert va.linear(w, x, y).ok()
+    torch.cuda.synchronize()
+    for a, b in zip(ya, yb):
+        np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy())
+
+
 @pytest.mark.parametrize("M", [1, 3])
 def test_residual_in_place(torch_dev, M):
     # y aliasing the residual, as the reference engine calls its residual GEMV

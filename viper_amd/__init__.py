@@ -4,5 +4,6 @@ Compute goes through ``viper_amd/lib/libviper_qlinear.so`` (include/viper_qlinea
 there is no CPU fallback.
 """
 from .qlinear import (GROUP, MAX_M, QType, QuantizedWeight, ScaleEnc, Status, StatusCode,  # noqa: F401
-                      check_quantizer, is_lossless, lib, linear, linear_partials, linear_prequantized,
-                      packed_bytes, qtype_name, quantize_act, workspace_bytes)
+                      check_quantizer, is_lossless, lib, linear, linear_fused2, linear_fused2_prequantized,
+                      linear_partials, linear_prequantized, packed_bytes, qtype_name, quantize_act,
+                      workspace_bytes)

@@ -31,7 +31,9 @@
 // Work split.  A workgroup owns T tiles of 16 weight rows and W waves; wave v
 // takes group pairs p = v, v + W, v + 2W, ... (adjacent waves read adjacent
 // 64-byte pieces of every row), and the W partial sums are added in wave
-// order through LDS, so results do not depend on timing.
+// order through LDS, so results do not depend on timing.  Two matrices
+// of one shape may share a launch (the reference's fused2): workgroups
+// [0, nb0) work on (w, ws, y), the rest on (w1, ws1, y1).
 
 #include "qlinear_host.h"
 
@@ -105,7 +107,8 @@ __global__ void __launch_bounds__(64 * W)
 qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws, int senc,
                   const int8_t* __restrict__ xq, const float* __restrict__ xs,
                   uint16_t* y, const uint16_t* res, int32_t* __restrict__ part,
-                  int N, int K, int M) {
+                  int N, int K, int M, const uint8_t* __restrict__ w1,
+                  const uint16_t* __restrict__ ws1, uint16_t* y1, int nb0) {
     using FT = Fmt<F>;
     constexpr int PS = ONE ? MF_PS_ONE : MF_PS_LOOP;
     constexpr bool NIB = F != 8;
@@ -124,7 +127,14 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
     const int CPR = K / FT::CK;
     const int cnt = (NP + W - 1) / W;
     const int nseg = ONE ? 1 : (cnt + PS - 1) / PS;
-    const int row0 = (int)blockIdx.x * 16 * T;
+    int bid = (int)blockIdx.x;
+    if (bid >= nb0) {  // second matrix of a fused pair
+        bid -= nb0;
+        w = w1;
+        ws = ws1;
+        y = y1;
+    }
+    const int row0 = bid * 16 * T;
     const int nrows = min(16 * T, N - row0);
     const uint32_t rbytes = (uint32_t)CPR * 16;
     const auto wr = buf(w + (size_t)row0 * rbytes, (uint32_t)nrows * rbytes);
@@ -326,7 +336,8 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
 // ------------------------------------------------------------------ host side
 
 typedef void (*mf_fn)(const uint8_t*, const uint16_t*, int, const int8_t*, const float*, uint16_t*,
-                      const uint16_t*, int32_t*, int, int, int);
+                      const uint16_t*, int32_t*, int, int, int, const uint8_t*, const uint16_t*,
+                      uint16_t*, int);
 
 struct MfShape {
     int t, w;
@@ -382,7 +393,8 @@ bool mfma_staged(int qtype, int N, int K) {
 
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
-                hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+                const void* w1, const void* s1, void* y1, hipStream_t st, hipEvent_t ev0,
+                hipEvent_t ev1) {
     if (!mfma_ok(qtype, K, M, s)) return VIPER_INTERNAL;
     const int NG = K / group_of(qtype);
     const int NP = NG / 2;
@@ -397,7 +409,8 @@ int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K,
         default: fn = mf_kernel<8>(sh.t, sh.w, one, xnat, part != nullptr); break;
     }
     if (fn == nullptr) return VIPER_INTERNAL;
-    const unsigned grid = (unsigned)((N + 16 * sh.t - 1) / (16 * sh.t));
+    int nb0 = (N + 16 * sh.t - 1) / (16 * sh.t);
+    const unsigned grid = (unsigned)(w1 != nullptr ? 2 * nb0 : nb0);
     const size_t lds = mf_lds_bytes(xnat, sh.w, sh.t, NG);
     const uint8_t* a0 = (const uint8_t*)w;
     const uint16_t* a1 = (const uint16_t*)s;
@@ -405,7 +418,10 @@ int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K,
     const float* a4 = (const float*)xs;
     uint16_t* a5 = (uint16_t*)y;
     const uint16_t* a6 = (const uint16_t*)res;
-    void* args[] = {&a0, &a1, &senc, &a3, &a4, &a5, &a6, &part, &N, &K, &M};
+    const uint8_t* b0 = (const uint8_t*)w1;
+    const uint16_t* b1 = (const uint16_t*)s1;
+    uint16_t* b2 = (uint16_t*)y1;
+    void* args[] = {&a0, &a1, &senc, &a3, &a4, &a5, &a6, &part, &N, &K, &M, &b0, &b1, &b2, &nb0};
     launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args, ev0, ev1);
     return status_of(hipGetLastError());
 }

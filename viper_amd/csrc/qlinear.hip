@@ -130,28 +130,75 @@ static size_t workspace_need(int qtype, int K, int M) {
     return align16((size_t)16 * K) + (size_t)(K / G) * 16 * 4;
 }
 
+// Optional second matrix of the same shape applied to the same activation in
+// the same launch (the reference's fused2: k and v, gate and up).
+struct Second {
+    const void* w = nullptr;
+    const void* s = nullptr;
+    void* y = nullptr;
+};
+
+static int validate_second(const Second& b, int qtype, int senc, int group, int N, int K, int M,
+                           const void* res, const int32_t* part) {
+    if (b.w == nullptr && b.s == nullptr && b.y == nullptr) return VIPER_OK;
+    if (b.y == nullptr || res != nullptr || part != nullptr) return VIPER_INVALID_ARGUMENT;
+    if (misaligned(b.y, 2)) return VIPER_INVALID_ARGUMENT;
+    return validate_weights(qtype, b.w, b.s, senc, group, N, K, M);
+}
+
 static int qlinear_common(int qtype, const void* w, const void* s, int senc, int group, int N,
                           int K, const void* x, int M, void* y, const void* res, void* wsp,
                           size_t wsp_bytes, int32_t* part, void* stream,
-                          hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr) {
+                          hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr, Second b = Second()) {
     int rc = validate_weights(qtype, w, s, senc, group, N, K, M);
     if (rc != VIPER_OK) return rc;
     if (x == nullptr || y == nullptr) return VIPER_INVALID_ARGUMENT;
     if (misaligned(x, 16) || misaligned(y, 2) || misaligned(res, 2) || misaligned(part, 4))
         return VIPER_INVALID_ARGUMENT;
+    rc = validate_second(b, qtype, senc, group, N, K, M, res, part);
+    if (rc != VIPER_OK) return rc;
     hipStream_t st = (hipStream_t)stream;
-    if (fused_ok(qtype, M, K)) return launch_m1(qtype, w, s, senc, N, K, x, y, res, part, st, ev0, ev1);
+    if (fused_ok(qtype, M, K))
+        return launch_m1(qtype, w, s, senc, N, K, x, nullptr, y, res, part, b.w, b.s, b.y, st, ev0, ev1);
     const size_t need = workspace_need(qtype, K, M);
     if (wsp == nullptr || wsp_bytes < need || misaligned(wsp, 16)) return VIPER_INVALID_ARGUMENT;
-    const bool mf = mfma_ok(qtype, K, M, s);
+    const bool mf = mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s));
     const bool staged = mf && mfma_staged(qtype, N, K);
     if (!mf && lds_pre(qtype, M, K) > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
     uint8_t* xq = (uint8_t*)wsp;
     float* xs = (float*)(xq + align16((size_t)16 * K));
     rc = launch_quantize(group, x, M, K, xq, xs, staged, st);
     if (rc != VIPER_OK) return rc;
-    if (mf) return launch_mfma(qtype, w, s, senc, N, K, xq, xs, !staged, M, y, res, part, st, ev0, ev1);
-    return launch_pre(qtype, w, s, senc, N, K, xq, xs, M, y, res, part, st, ev0, ev1);
+    if (mf)
+        return launch_mfma(qtype, w, s, senc, N, K, xq, xs, !staged, M, y, res, part, b.w, b.s, b.y,
+                           st, ev0, ev1);
+    rc = launch_pre(qtype, w, s, senc, N, K, xq, xs, M, y, res, part, st, ev0, ev1);
+    if (rc == VIPER_OK && b.w != nullptr)
+        rc = launch_pre(qtype, b.w, b.s, senc, N, K, xq, xs, M, b.y, nullptr, nullptr, st, nullptr, nullptr);
+    return rc;
+}
+
+static int prequant_common(int qtype, const void* w, const void* s, int senc, int group, int N,
+                           int K, const void* xq, const void* xs, int M, void* y, const void* res,
+                           void* stream, Second b = Second()) {
+    int rc = validate_weights(qtype, w, s, senc, group, N, K, M);
+    if (rc != VIPER_OK) return rc;
+    if (xq == nullptr || xs == nullptr || y == nullptr) return VIPER_INVALID_ARGUMENT;
+    if (misaligned(xq, 8) || misaligned(xs, 4) || misaligned(y, 2) || misaligned(res, 2))
+        return VIPER_INVALID_ARGUMENT;
+    rc = validate_second(b, qtype, senc, group, N, K, M, res, nullptr);
+    if (rc != VIPER_OK) return rc;
+    hipStream_t st = (hipStream_t)stream;
+    if (fused_ok(qtype, M, K))
+        return launch_m1(qtype, w, s, senc, N, K, xq, (const float*)xs, y, res, nullptr, b.w, b.s, b.y,
+                         st, nullptr, nullptr);
+    if (mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s)))
+        return launch_mfma(qtype, w, s, senc, N, K, xq, xs, true, M, y, res, nullptr, b.w, b.s, b.y, st,
+                           nullptr, nullptr);
+    rc = launch_pre(qtype, w, s, senc, N, K, xq, xs, M, y, res, nullptr, st, nullptr, nullptr);
+    if (rc == VIPER_OK && b.w != nullptr)
+        rc = launch_pre(qtype, b.w, b.s, senc, N, K, xq, xs, M, b.y, nullptr, nullptr, st, nullptr, nullptr);
+    return rc;
 }
 
 }  // namespace vq
@@ -212,17 +259,30 @@ extern "C" int viper_hip_qlinear_prequantized(int qtype, const void* w_packed,
                                               int N, int K, const void* xq, const void* xs, int M,
                                               void* y_bf16, const void* residual_bf16,
                                               void* stream) {
-    int rc = vq::validate_weights(qtype, w_packed, w_scales, scale_enc, group, N, K, M);
-    if (rc != VIPER_OK) return rc;
-    if (xq == nullptr || xs == nullptr || y_bf16 == nullptr) return VIPER_INVALID_ARGUMENT;
-    if (vq::misaligned(xq, 8) || vq::misaligned(xs, 4) || vq::misaligned(y_bf16, 2) ||
-        vq::misaligned(residual_bf16, 2))
-        return VIPER_INVALID_ARGUMENT;
-    if (vq::mfma_ok(qtype, K, M, w_scales))
-        return vq::launch_mfma(qtype, w_packed, w_scales, scale_enc, N, K, xq, xs, true, M, y_bf16,
-                               residual_bf16, nullptr, (hipStream_t)stream, nullptr, nullptr);
-    return vq::launch_pre(qtype, w_packed, w_scales, scale_enc, N, K, xq, xs, M, y_bf16,
-                          residual_bf16, nullptr, (hipStream_t)stream, nullptr, nullptr);
+    return vq::prequant_common(qtype, w_packed, w_scales, scale_enc, group, N, K, xq, xs, M, y_bf16,
+                               residual_bf16, stream);
+}
+
+extern "C" int viper_hip_qlinear_fused2(int qtype, const void* w0_packed, const void* w0_scales,
+                                        const void* w1_packed, const void* w1_scales, int scale_enc,
+                                        int group, int N, int K, const void* x_bf16, int M,
+                                        void* y0_bf16, void* y1_bf16, void* workspace,
+                                        size_t workspace_bytes, void* stream) {
+    if (w1_packed == nullptr || w1_scales == nullptr || y1_bf16 == nullptr) return VIPER_INVALID_ARGUMENT;
+    return vq::qlinear_common(qtype, w0_packed, w0_scales, scale_enc, group, N, K, x_bf16, M, y0_bf16,
+                              nullptr, workspace, workspace_bytes, nullptr, stream, nullptr, nullptr,
+                              vq::Second{w1_packed, w1_scales, y1_bf16});
+}
+
+extern "C" int viper_hip_qlinear_fused2_prequantized(int qtype, const void* w0_packed,
+                                                     const void* w0_scales, const void* w1_packed,
+                                                     const void* w1_scales, int scale_enc, int group,
+                                                     int N, int K, const void* xq, const void* xs,
+                                                     int M, void* y0_bf16, void* y1_bf16,
+                                                     void* stream) {
+    if (w1_packed == nullptr || w1_scales == nullptr || y1_bf16 == nullptr) return VIPER_INVALID_ARGUMENT;
+    return vq::prequant_common(qtype, w0_packed, w0_scales, scale_enc, group, N, K, xq, xs, M, y0_bf16,
+                               nullptr, stream, vq::Second{w1_packed, w1_scales, y1_bf16});
 }
 
 extern "C" int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream) {

@@ -72,10 +72,13 @@ inline int device_cus() {
 
 // ---- launchers (one translation unit each)
 
-// M = 1 with the activation quantize fused (qgemv_m1.hip).
+// M = 1 (qgemv_m1.hip): x bf16 with the quantize fused (xs == nullptr), or
+// x int8 + xs fp32 already quantized; w1/s1/y1 non-null: a second matrix of
+// the same shape in the same launch.
 size_t lds_m1(int qtype, int K);
-int launch_m1(int qtype, const void* w, const void* s, int senc, int N, int K, const void* x, void* y,
-              const void* res, int32_t* part, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
+int launch_m1(int qtype, const void* w, const void* s, int senc, int N, int K, const void* x,
+              const float* xs, void* y, const void* res, int32_t* part, const void* w1,
+              const void* s1, void* y1, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
 
 // M <= 16 over prequantized activations, v_dot4 (qgemm_pre.hip).
 int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
@@ -90,6 +93,7 @@ bool mfma_ok(int qtype, int K, int M, const void* s);
 bool mfma_staged(int qtype, int N, int K);
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
-                hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
+                const void* w1, const void* s1, void* y1, hipStream_t st, hipEvent_t ev0,
+                hipEvent_t ev1);
 
 }  // namespace vq

@@ -121,6 +121,8 @@ _SYMBOLS = (
     "viper_hip_qlinear_partials",
     "viper_hip_qlinear_timed",
     "viper_hip_check_quantizer",
+    "viper_hip_qlinear_fused2",
+    "viper_hip_qlinear_fused2_prequantized",
 )
 
 
@@ -151,6 +153,11 @@ def lib():
     L.viper_hip_qlinear_timed.restype = i32
     L.viper_hip_check_quantizer.argtypes = [i32, i32, vp, vp]
     L.viper_hip_check_quantizer.restype = i32
+    L.viper_hip_qlinear_fused2.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
+    L.viper_hip_qlinear_fused2.restype = i32
+    L.viper_hip_qlinear_fused2_prequantized.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, i32,
+                                                        vp, vp, vp]
+    L.viper_hip_qlinear_fused2_prequantized.restype = i32
     _lib = L
     return L
 
@@ -242,6 +249,35 @@ def linear_prequantized(w: QuantizedWeight, xq, xs, y, residual=None, stream=Non
                                               w.group_size, N, K, ptr(xq), ptr(xs), M, ptr(y), ptr(residual),
                                               _stream(stream))
     return _status(rc, "viper_hip_qlinear_prequantized")
+
+
+def _same_kind(w0: QuantizedWeight, w1: QuantizedWeight) -> bool:
+    return (w0.qtype, w0.rows, w0.cols, w0.group_size, w0.scale_enc) == \
+        (w1.qtype, w1.rows, w1.cols, w1.group_size, w1.scale_enc)
+
+
+def linear_fused2(w0: QuantizedWeight, w1: QuantizedWeight, x, y0, y1, workspace=None, stream=None) -> Status:
+    """y0 = x w0 and y1 = x w1 in one launch (two matrices of one shape)."""
+    if not _same_kind(w0, w1):
+        return Status(StatusCode.SHAPE_MISMATCH, "linear_fused2: the two weights differ in kind or shape")
+    K, N = w0.cols, w0.rows
+    M = _shape_mk(x, K)
+    ws_ptr, ws_n = (None, 0) if workspace is None else (ptr(workspace), workspace.numel() * workspace.element_size())
+    rc = lib().viper_hip_qlinear_fused2(int(w0.qtype), ptr(w0.data), ptr(w0.scales), ptr(w1.data), ptr(w1.scales),
+                                        int(w0.scale_enc), w0.group_size, N, K, ptr(x), M, ptr(y0), ptr(y1),
+                                        ws_ptr, ws_n, _stream(stream))
+    return _status(rc, "viper_hip_qlinear_fused2")
+
+
+def linear_fused2_prequantized(w0: QuantizedWeight, w1: QuantizedWeight, xq, xs, y0, y1, stream=None) -> Status:
+    if not _same_kind(w0, w1):
+        return Status(StatusCode.SHAPE_MISMATCH, "linear_fused2: the two weights differ in kind or shape")
+    K, N = w0.cols, w0.rows
+    M = int(xq.numel() // K)
+    rc = lib().viper_hip_qlinear_fused2_prequantized(int(w0.qtype), ptr(w0.data), ptr(w0.scales), ptr(w1.data),
+                                                     ptr(w1.scales), int(w0.scale_enc), w0.group_size, N, K,
+                                                     ptr(xq), ptr(xs), M, ptr(y0), ptr(y1), _stream(stream))
+    return _status(rc, "viper_hip_qlinear_fused2_prequantized")
 
 
 def check_quantizer(exp_lo, exp_hi, counts, stream=None) -> Status:
