@@ -32,6 +32,9 @@
  *                                   include/viper/model_impl.cuh:652,725) on one
  *                                   quantized activation in one launch.
  *   viper_hip_qlinear_fused2        the same from bf16 x (quantize fused at M = 1).
+ *   viper_hip_rmsnorm_quantize      rmsnorm_quantize_bf16 (kernels/ops/rmsnorm_quantize.cu:107-123,
+ *                                   declared kernels/ops/rmsnorm_kernel.h), per row.
+ *   viper_hip_swiglu_quantize       swiglu_quantize_bf16 (kernels/ops/swiglu_quantize.cu:81-96).
  *   viper_hip_qlinear_partials      no counterpart: the same kernels, also writing
  *                                   the exact per-group int32 dots for parity tests.
  *   viper_hip_qlinear_timed         no counterpart: viper_hip_qlinear with events
@@ -134,6 +137,18 @@ int viper_hip_qlinear_fused2_prequantized(int qtype, const void* w0_packed, cons
                                           int scale_enc, int group, int N, int K, const void* xq,
                                           const void* xs, int M, void* y0_bf16, void* y1_bf16,
                                           void* stream);
+
+/* Producer-side activation quantize, per row m < M of H (or I) elements:
+ *   rmsnorm: v = bf16_RNE((x * rsqrt(sum(x^2)/H + eps)) * gamma),
+ *   swiglu:  v = bf16_RNE(gate / (1 + exp(-gate)) * up),
+ * then xq[M][H] int8 and xs[M][H/group] fp32 from v exactly as
+ * viper_hip_quantize_act.  out_bf16 (may be NULL) receives v; for swiglu it
+ * may alias gate (the reference's engine passes gate as the output).  x,
+ * gamma, gate, up and out 16-byte aligned; group 64 or 32. */
+int viper_hip_rmsnorm_quantize(const void* x_bf16, const void* gamma_bf16, float eps, int M, int H,
+                               int group, void* out_bf16, void* xq, void* xs, void* stream);
+int viper_hip_swiglu_quantize(const void* gate_bf16, const void* up_bf16, int M, int I, int group,
+                              void* out_bf16, void* xq, void* xs, void* stream);
 
 /* viper_hip_qlinear with two caller-created hipEvent_t attached to the GEMV
  * dispatch (measurement use: they bracket the kernel's own execution, not

@@ -53,6 +53,8 @@ def lib():
         L.vo_quantize_weights.argtypes = [i32, vp, i32, i32, i32, vp, vp]
         L.vo_quantize_weights.restype = i32
         L.vo_quantize_act.argtypes, L.vo_quantize_act.restype = [vp, i32, i32, i32, vp, vp], i32
+        L.vo_rmsnorm_bf16.argtypes, L.vo_rmsnorm_bf16.restype = [vp, vp, C.c_float, i32, i32, vp], i32
+        L.vo_swiglu_bf16.argtypes, L.vo_swiglu_bf16.restype = [vp, vp, i32, i32, vp], i32
         L.vo_group_dots.argtypes, L.vo_group_dots.restype = [i32, vp, i32, i32, vp, i32, vp], i32
         L.vo_qlinear_prequant.argtypes = [i32, vp, vp, i32, i32, i32, vp, vp, i32, vp, vp, vp, vp]
         L.vo_qlinear_prequant.restype = i32
@@ -154,6 +156,24 @@ def quantize_act(x_bf16, group):
     xs = np.zeros((M, K // group), dtype=np.float32)
     _check(lib().vo_quantize_act(_p(x_bf16), M, K, group, _p(xq), _p(xs)), "quantize_act")
     return xq, xs
+
+
+def rmsnorm_bf16(x_bf16, gamma_bf16, eps):
+    x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    M, H = x_bf16.shape
+    gamma = np.ascontiguousarray(gamma_bf16, dtype=np.uint16)
+    out = np.zeros((M, H), dtype=np.uint16)
+    _check(lib().vo_rmsnorm_bf16(_p(x_bf16), _p(gamma), C.c_float(eps), M, H, _p(out)), "rmsnorm_bf16")
+    return out
+
+
+def swiglu_bf16(gate_bf16, up_bf16):
+    gate = np.ascontiguousarray(gate_bf16, dtype=np.uint16)
+    up = np.ascontiguousarray(up_bf16, dtype=np.uint16)
+    M, I = gate.shape
+    out = np.zeros((M, I), dtype=np.uint16)
+    _check(lib().vo_swiglu_bf16(_p(gate), _p(up), M, I, _p(out)), "swiglu_bf16")
+    return out
 
 
 def group_dots(qtype, packed, N, K, xq):

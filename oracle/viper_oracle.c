@@ -367,6 +367,39 @@ int vo_quantize_act(const uint16_t* x, int M, int K, int group, int8_t* xq, floa
 }
 
 /* ------------------------------------------------------------------ */
+/* producers of the activation: rmsnorm and swiglu (before the quantize) */
+/* ------------------------------------------------------------------ */
+
+int vo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma, float eps, int M, int H, uint16_t* out) {
+    if (M <= 0 || H <= 0) return -1;
+    for (int m = 0; m < M; ++m) {
+        const uint16_t* xr = x + (size_t)m * H;
+        double ss = 0.0;
+        for (int i = 0; i < H; ++i) {
+            const double v = vo_bf16_to_f32(xr[i]);
+            ss += v * v;
+        }
+        const float t = (float)ss / (float)H + eps;
+        const float inv = (float)(1.0 / sqrt((double)t));
+        for (int i = 0; i < H; ++i) {
+            const float v = (vo_bf16_to_f32(xr[i]) * inv) * vo_bf16_to_f32(gamma[i]);
+            out[(size_t)m * H + i] = vo_f32_to_bf16(v);
+        }
+    }
+    return 0;
+}
+
+int vo_swiglu_bf16(const uint16_t* gate, const uint16_t* up, int M, int I, uint16_t* out) {
+    if (M <= 0 || I <= 0) return -1;
+    for (size_t i = 0; i < (size_t)M * I; ++i) {
+        const float g = vo_bf16_to_f32(gate[i]), u = vo_bf16_to_f32(up[i]);
+        const float v = g / (1.0f + expf(-g)) * u;
+        out[i] = vo_f32_to_bf16(v);
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* exact group dots                                                    */
 /* ------------------------------------------------------------------ */
 

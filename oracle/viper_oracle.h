@@ -15,6 +15,17 @@
  *                         swiglu_quantize.cu:45-78, linear_multim.cu:21-61:
  *                         per-row, per-group amax; scale = max(amax/127, 1e-8);
  *                         q = RNE(x / scale) with an IEEE divide; clamp +-127.
+ *   vo_rmsnorm_bf16       kernels/ops/rmsnorm_quantize.cu:37-73 (phases 1-3):
+ *                         inv = 1/sqrt(ss/H + eps) with ss = sum x^2, then
+ *                         bf16_RNE((x * inv) * gamma) in fp32.  ss is summed in
+ *                         double and rounded to fp32 once, and the square root
+ *                         is exact; the reference sums in fp32 in a thread
+ *                         order and uses rsqrtf, so outputs agree to 1 bf16 ulp.
+ *   vo_swiglu_bf16        kernels/ops/swiglu_quantize.cu:35-41 (phase 1):
+ *                         bf16_RNE(g / (1 + exp(-g)) * u) in fp32 with the libm
+ *                         exp (the reference uses __expf; 1 bf16 ulp).
+ *                         The quantize step after both is vo_quantize_act
+ *                         (rmsnorm_quantize.cu:75-104, swiglu_quantize.cu:45-78).
  *   vo_group_dots         the exact int32 group sum that dp4a_q4_kernel.cu:116-150
  *                         forms and dp4a_smem_kernel.cu:49-58 / linear_multim.cu:
  *                         92-112 split into 8-element dp4a partials.
@@ -91,6 +102,12 @@ int vo_quantize_weights(int qtype, const uint16_t* w_bf16, int N, int K, int sca
 
 /* ---- activation quantize: x[M][K] bf16 -> xq[M][K] int8, xs[M][K/G] fp32 ---- */
 int vo_quantize_act(const uint16_t* x, int M, int K, int group, int8_t* xq, float* xs);
+
+/* out[M][H] = rmsnorm(x) * gamma (bf16), per row; eps as the reference's cfg.rms_eps. */
+int vo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma, float eps, int M, int H, uint16_t* out);
+
+/* out[M][I] = silu(gate) * up (bf16). */
+int vo_swiglu_bf16(const uint16_t* gate, const uint16_t* up, int M, int I, uint16_t* out);
 
 /* ---- exact per-group int32 dots: D[m][n][g] ---- */
 int vo_group_dots(int qtype, const uint8_t* packed, int N, int K, const int8_t* xq, int M,

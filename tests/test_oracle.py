@@ -309,3 +309,57 @@ def test_generator_deterministic_and_in_range():
     xo = O.bf16_to_f32(O.gen_act(64, 1024, 1, outlier_frac=0.05, outlier_mul=20.0))
     frac = float((np.abs(xo - x) > 0).any(axis=0).mean())
     assert 0.03 < frac < 0.07
+
+
+# ---- producers of the activation (rmsnorm, swiglu) before the quantize
+
+def _bf16(a):
+    return O.f32_to_bf16(np.asarray(a, dtype=np.float32))
+
+
+def test_rmsnorm_closed_form_constant_row():
+    # x = c everywhere, gamma = 1: every output is bf16(c / sqrt(c^2 + eps))
+    H, eps = 2560, 1e-6
+    for c in (0.5, -3.0, 1e-3, 7.25):
+        x = np.tile(_bf16([c]), (1, H))
+        out = O.rmsnorm_bf16(x, np.tile(_bf16([1.0]), H), eps)
+        cf = float(O.bf16_to_f32(_bf16([c]))[0])
+        want = _bf16([cf / np.sqrt(cf * cf + eps)])[0]
+        assert (out == want).all(), (c, out[0, 0], want)
+
+
+def test_rmsnorm_invariants_and_float64():
+    rng = np.random.default_rng(3)
+    M, H, eps = 3, 2560, 1e-5
+    x = _bf16(rng.standard_normal((M, H)))
+    gamma = _bf16(1.0 + 0.1 * rng.standard_normal(H))
+    out = O.rmsnorm_bf16(x, gamma, eps)
+    # scale invariance: x -> 4x with eps -> 16 eps scales ss/H + eps by 16 and
+    # inv by 1/4, all exactly (powers of two), so every output is unchanged
+    x4 = _bf16(O.bf16_to_f32(x) * 4.0)
+    assert (O.rmsnorm_bf16(x4, gamma, eps * 16.0) == out).all()
+    # gamma linearity: 2*gamma doubles every output exactly
+    g2 = _bf16(O.bf16_to_f32(gamma) * 2.0)
+    np.testing.assert_array_equal(O.bf16_to_f32(O.rmsnorm_bf16(x, g2, eps)), 2.0 * O.bf16_to_f32(out))
+    # float64 restatement, within one bf16 ulp
+    xf = O.bf16_to_f32(x).astype(np.float64)
+    ref = xf / np.sqrt((xf * xf).mean(axis=1, keepdims=True) + eps) * O.bf16_to_f32(gamma)
+    assert (np.abs(O.bf16_to_f32(out) - ref) <= O.bf16_ulp(out)).all()
+
+
+def test_swiglu_known_values_and_float64():
+    g = _bf16([0.0, 20.0, -20.0, 1.0, -1.0, 3.5])
+    u = _bf16([5.0, 1.0, 1.0, 2.0, 2.0, -1.0])
+    out = O.bf16_to_f32(O.swiglu_bf16(g[None, :], u[None, :]))[0]
+    assert out[0] == 0.0                      # silu(0) = 0
+    assert out[1] == 20.0                     # silu(20) = 20 to within bf16
+    assert -1e-6 < out[2] < 0.0               # silu(-20) = -20 e^-20
+    # silu(g) - silu(-g) = g
+    assert abs((out[3] - out[4]) / 2.0 - 1.0) <= 2 * 2.0 ** -8
+    rng = np.random.default_rng(4)
+    G = _bf16(3.0 * rng.standard_normal((2, 4096)))
+    U = _bf16(rng.standard_normal((2, 4096)))
+    got = O.swiglu_bf16(G, U)
+    gf, uf = O.bf16_to_f32(G).astype(np.float64), O.bf16_to_f32(U).astype(np.float64)
+    ref = gf / (1.0 + np.exp(-gf)) * uf
+    assert (np.abs(O.bf16_to_f32(got) - ref) <= O.bf16_ulp(got)).all()

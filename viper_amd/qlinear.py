@@ -123,6 +123,8 @@ _SYMBOLS = (
     "viper_hip_check_quantizer",
     "viper_hip_qlinear_fused2",
     "viper_hip_qlinear_fused2_prequantized",
+    "viper_hip_rmsnorm_quantize",
+    "viper_hip_swiglu_quantize",
 )
 
 
@@ -158,6 +160,10 @@ def lib():
     L.viper_hip_qlinear_fused2_prequantized.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, i32,
                                                         vp, vp, vp]
     L.viper_hip_qlinear_fused2_prequantized.restype = i32
+    L.viper_hip_rmsnorm_quantize.argtypes = [vp, vp, C.c_float, i32, i32, i32, vp, vp, vp, vp]
+    L.viper_hip_rmsnorm_quantize.restype = i32
+    L.viper_hip_swiglu_quantize.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, vp]
+    L.viper_hip_swiglu_quantize.restype = i32
     _lib = L
     return L
 
@@ -278,6 +284,24 @@ def linear_fused2_prequantized(w0: QuantizedWeight, w1: QuantizedWeight, xq, xs,
                                                      ptr(w1.scales), int(w0.scale_enc), w0.group_size, N, K,
                                                      ptr(xq), ptr(xs), M, ptr(y0), ptr(y1), _stream(stream))
     return _status(rc, "viper_hip_qlinear_fused2_prequantized")
+
+
+def rmsnorm_quantize(x, gamma, eps, group, xq, xs, out=None, stream=None) -> Status:
+    """xq/xs (and out, bf16) from rmsnorm(x) * gamma, per row of x [M, H]."""
+    H = gamma.numel()
+    M = int(x.numel() // H)
+    rc = lib().viper_hip_rmsnorm_quantize(ptr(x), ptr(gamma), float(eps), M, H, group, ptr(out), ptr(xq),
+                                          ptr(xs), _stream(stream))
+    return _status(rc, "viper_hip_rmsnorm_quantize")
+
+
+def swiglu_quantize(gate, up, group, xq, xs, out=None, stream=None) -> Status:
+    """xq/xs (and out, bf16; may be gate itself) from silu(gate) * up, rows of [M, I]."""
+    I = gate.shape[-1]
+    M = int(gate.numel() // I)
+    rc = lib().viper_hip_swiglu_quantize(ptr(gate), ptr(up), M, I, group, ptr(out), ptr(xq), ptr(xs),
+                                         _stream(stream))
+    return _status(rc, "viper_hip_swiglu_quantize")
 
 
 def check_quantizer(exp_lo, exp_hi, counts, stream=None) -> Status:
