@@ -197,6 +197,46 @@ def main():
         extras["down_k10240_n2560_gbs"] = round(algd / (d_us * 1e-6) / 1e9, 1)
         del gd, Wd, Sd
 
+        # config 1: gate+up (one fused2 launch, K=2560, N=2x10240) -> swiglu +
+        # quantize -> down (K=10240, N=2560) + residual; one step = 3 launches
+        H, I = 2560, 10240
+        step_bytes = 3 * (N * K // 2 + N * (K // G) * 2)
+        mcopies = max(2, -(-ROTATE_BYTES // step_bytes) + 1)
+        Wg, Sg = make_weights(torch, mcopies, I, H, gen)
+        Wu, Su = make_weights(torch, mcopies, I, H, gen)
+        Wdn, Sdn = make_weights(torch, mcopies, H, I, gen)
+        xm = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
+        rm = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
+        gm = torch.empty((1, I), dtype=torch.bfloat16, device="cuda")
+        um = torch.empty((1, I), dtype=torch.bfloat16, device="cuda")
+        ym = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
+        xqm = torch.empty((1, I), dtype=torch.int8, device="cuda")
+        xsm = torch.empty((1, I // G), dtype=torch.float32, device="cuda")
+
+        def launch_mlp(i):
+            c = i % mcopies
+            st = torch.cuda.current_stream().cuda_stream
+            rc = L.viper_hip_qlinear_fused2(qtype, Wg[c].data_ptr(), Sg[c].data_ptr(), Wu[c].data_ptr(),
+                                            Su[c].data_ptr(), 0, G, I, H, xm.data_ptr(), 1, gm.data_ptr(),
+                                            um.data_ptr(), None, 0, st)
+            rc = rc or L.viper_hip_swiglu_quantize(gm.data_ptr(), um.data_ptr(), 1, I, G, gm.data_ptr(),
+                                                   xqm.data_ptr(), xsm.data_ptr(), st)
+            rc = rc or L.viper_hip_qlinear_prequantized(qtype, Wdn[c].data_ptr(), Sdn[c].data_ptr(), 0, G, H, I,
+                                                        xqm.data_ptr(), xsm.data_ptr(), 1, ym.data_ptr(),
+                                                        rm.data_ptr(), st)
+            if rc != 0:
+                raise RuntimeError(f"MLP step failed: {rc}")
+        for i in range(20):
+            launch_mlp(i)
+        gm1, rm1 = capture(torch, launch_mlp, mcopies, 200)
+        mlp_us = time_graph(torch, gm1, rm1) * 1e3 / (rm1 * mcopies)
+        # weights + scales of the three matrices, x and the residual in, gate/up
+        # out and back in, int8 activation + scales out and back in, y out
+        mlp_bytes = (step_bytes + H * 2 * 2 + 2 * I * 2 * 2 + (I + I // G * 4) * 2 + H * 2)
+        extras["mlp_config1_us"] = round(mlp_us, 3)
+        extras["mlp_config1_gbs"] = round(mlp_bytes / (mlp_us * 1e-6) / 1e9, 1)
+        del gm1, Wg, Sg, Wu, Su, Wdn, Sdn
+
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_q4_m1_k2560_n10240.json")
     if os.path.exists(tpath):

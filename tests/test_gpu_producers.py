@@ -98,3 +98,44 @@ def test_producer_errors_are_codes(torch_dev):
     assert va.swiglu_quantize(x, x, 16, xq, xs).code == va.StatusCode.INVALID_ARGUMENT
     assert va.rmsnorm_quantize(x, g, 1e-6, 32, xq, xs).ok()
     torch.cuda.synchronize()
+
+
+def test_mlp_pipeline(torch_dev):
+    # config 1 at full size: gate+up (fused2, K=2560, N=2x10240) -> swiglu +
+    # quantize -> down (K=10240, N=2560) + residual, each stage checked
+    # against the oracle fed with the device's previous stage
+    torch = torch_dev
+    H, I = 2560, 10240
+    G = 64
+    pg, sg = O.gen_weights(O.Q4_G64, I, H, 0x5EED0001, O.SCALE_FP16)
+    pu, su = O.gen_weights(O.Q4_G64, I, H, 0x5EED0011, O.SCALE_FP16)
+    pd, sd = O.gen_weights(O.Q4_G64, H, I, 0x5EED0021, O.SCALE_FP16)
+    x = O.gen_act(1, H, 0x5EED0031)
+    res = O.gen_act(1, H, 0x5EED0041)
+    wg = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, pg), dev(torch, sg), I, H)
+    wu = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, pu), dev(torch, su), I, H)
+    wd = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, pd), dev(torch, sd), H, I)
+    g = torch.zeros((1, I), dtype=torch.int16, device="cuda")
+    u = torch.zeros((1, I), dtype=torch.int16, device="cuda")
+    xq = torch.zeros((1, I), dtype=torch.int8, device="cuda")
+    xs = torch.zeros((1, I // G), dtype=torch.float32, device="cuda")
+    y = torch.zeros((1, H), dtype=torch.int16, device="cuda")
+    assert va.linear_fused2(wg, wu, dev(torch, x), g, u).ok()
+    assert va.swiglu_quantize(g, u, G, xq, xs, out=g).ok()       # in place, as the engine
+    assert va.linear_prequantized(wd, xq, xs, y, residual=dev(torch, res)).ok()
+    torch.cuda.synchronize()
+    # stage 1 (g is overwritten in place: compare u, and g through a second call)
+    u_ref, _, u_abs = O.qlinear(O.Q4_G64, pu, su, O.SCALE_FP16, I, H, x)
+    O.assert_bf16_close(host_u16(u), u_ref, u_abs, rel=1e-5)
+    g2 = torch.zeros((1, I), dtype=torch.int16, device="cuda")
+    assert va.linear(wg, dev(torch, x), g2).ok()
+    torch.cuda.synchronize()
+    g_ref, _, g_abs = O.qlinear(O.Q4_G64, pg, sg, O.SCALE_FP16, I, H, x)
+    O.assert_bf16_close(host_u16(g2), g_ref, g_abs, rel=1e-5)
+    # stage 2 from the device's g, u
+    h_ref = O.swiglu_bf16(host_u16(g2), host_u16(u))
+    check_producer_output(host_u16(g), h_ref, xq.cpu().numpy(), xs.cpu().numpy(), G)
+    # stage 3 from the device's xq, xs
+    y_ref, _, y_abs = O.qlinear_prequant(O.Q4_G64, pd, sd, O.SCALE_FP16, H, I, xq.cpu().numpy(),
+                                         xs.cpu().numpy(), residual=res)
+    O.assert_bf16_close(host_u16(y), y_ref, y_abs, rel=1e-5)
