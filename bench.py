@@ -237,6 +237,38 @@ def main():
         extras["mlp_config1_gbs"] = round(mlp_bytes / (mlp_us * 1e-6) / 1e9, 1)
         del gm1, Wg, Sg, Wu, Su, Wdn, Sdn
 
+        # LM head (config 3's head): bf16 GEMV K=2560, N=166144 (850 MB, larger
+        # than the MALL, so one copy streams from HBM every call) + greedy argmax
+        Nv = 166144
+        Wh = (0.02 * torch.randn((Nv, K), device="cuda", generator=gen)).to(torch.bfloat16)
+        xh = torch.randn((1, K), device="cuda", generator=gen).to(torch.bfloat16)
+        yh = torch.empty((1, Nv), dtype=torch.bfloat16, device="cuda")
+        th = torch.empty(1, dtype=torch.int32, device="cuda")
+
+        def launch_head(i):
+            st = torch.cuda.current_stream().cuda_stream
+            rc = L.viper_hip_linear_bf16(Wh.data_ptr(), xh.data_ptr(), yh.data_ptr(), 1, Nv, K, st)
+            if rc != 0:
+                raise RuntimeError(f"LM head failed: {rc}")
+
+        def launch_greedy(i):
+            rc = L.viper_hip_sampling_greedy(yh.data_ptr(), th.data_ptr(), 1, Nv,
+                                             torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"greedy failed: {rc}")
+        for i in range(5):
+            launch_head(i)
+            launch_greedy(i)
+        gh, rh = capture(torch, launch_head, 10, 50)
+        head_us = time_graph(torch, gh, rh) * 1e3 / (rh * 10)
+        gg, rg = capture(torch, launch_greedy, 10, 200)
+        greedy_us = time_graph(torch, gg, rg) * 1e3 / (rg * 10)
+        head_bytes = Nv * K * 2 + K * 2 + Nv * 2
+        extras["lm_head_us"] = round(head_us, 3)
+        extras["lm_head_gbs"] = round(head_bytes / (head_us * 1e-6) / 1e9, 1)
+        extras["greedy_argmax_us"] = round(greedy_us, 3)
+        del gh, gg, Wh
+
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_q4_m1_k2560_n10240.json")
     if os.path.exists(tpath):

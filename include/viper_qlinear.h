@@ -35,6 +35,10 @@
  *   viper_hip_rmsnorm_quantize      rmsnorm_quantize_bf16 (kernels/ops/rmsnorm_quantize.cu:107-123,
  *                                   declared kernels/ops/rmsnorm_kernel.h), per row.
  *   viper_hip_swiglu_quantize       swiglu_quantize_bf16 (kernels/ops/swiglu_quantize.cu:81-96).
+ *   viper_hip_linear_bf16           linear_bf16 (kernels/ops/linear_bf16_kernel.cu:57-70,
+ *                                   declared kernels/ops/linear_bf16_kernel.h): the bf16 LM
+ *                                   head GEMV (src/viper/model.cpp:300-304).
+ *   viper_hip_sampling_greedy       sampling_greedy_bf16 (kernels/ops/sampling_kernel.cu:66-80).
  *   viper_hip_qlinear_partials      no counterpart: the same kernels, also writing
  *                                   the exact per-group int32 dots for parity tests.
  *   viper_hip_qlinear_timed         no counterpart: viper_hip_qlinear with events
@@ -149,6 +153,16 @@ int viper_hip_rmsnorm_quantize(const void* x_bf16, const void* gamma_bf16, float
                                int group, void* out_bf16, void* xq, void* xs, void* stream);
 int viper_hip_swiglu_quantize(const void* gate_bf16, const void* up_bf16, int M, int I, int group,
                               void* out_bf16, void* xq, void* xs, void* stream);
+
+/* LM head: y[M][N] = bf16_RNE(x[M][K] w[N][K]^T), w and x bf16, fp32
+ * accumulation.  M <= 16, K % 8 == 0, M*K*2 <= 64 KiB; w and x 16-byte
+ * aligned. */
+int viper_hip_linear_bf16(const void* w_bf16, const void* x_bf16, void* y_bf16, int M, int N, int K,
+                          void* stream);
+
+/* out_token[b] = the smallest index of the largest logits[b][V] (bf16); NaN
+ * never wins; a row with nothing above -inf gives 0. */
+int viper_hip_sampling_greedy(const void* logits_bf16, int32_t* out_token, int B, int V, void* stream);
 
 /* viper_hip_qlinear with two caller-created hipEvent_t attached to the GEMV
  * dispatch (measurement use: they bracket the kernel's own execution, not

@@ -55,6 +55,8 @@ def lib():
         L.vo_quantize_act.argtypes, L.vo_quantize_act.restype = [vp, i32, i32, i32, vp, vp], i32
         L.vo_rmsnorm_bf16.argtypes, L.vo_rmsnorm_bf16.restype = [vp, vp, C.c_float, i32, i32, vp], i32
         L.vo_swiglu_bf16.argtypes, L.vo_swiglu_bf16.restype = [vp, vp, i32, i32, vp], i32
+        L.vo_linear_bf16.argtypes, L.vo_linear_bf16.restype = [vp, vp, i32, i32, i32, vp, vp, vp], i32
+        L.vo_argmax_bf16.argtypes, L.vo_argmax_bf16.restype = [vp, i32, i32, vp], i32
         L.vo_group_dots.argtypes, L.vo_group_dots.restype = [i32, vp, i32, i32, vp, i32, vp], i32
         L.vo_qlinear_prequant.argtypes = [i32, vp, vp, i32, i32, i32, vp, vp, i32, vp, vp, vp, vp]
         L.vo_qlinear_prequant.restype = i32
@@ -173,6 +175,27 @@ def swiglu_bf16(gate_bf16, up_bf16):
     M, I = gate.shape
     out = np.zeros((M, I), dtype=np.uint16)
     _check(lib().vo_swiglu_bf16(_p(gate), _p(up), M, I, _p(out)), "swiglu_bf16")
+    return out
+
+
+def linear_bf16(w_bf16, x_bf16):
+    """(y_bf16 [M,N], y_f32, absterm) of x [M,K] times w [N,K]^T, all bf16 in."""
+    w = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+    x = np.ascontiguousarray(x_bf16, dtype=np.uint16)
+    N, K = w.shape
+    M = x.shape[0]
+    y = np.zeros((M, N), dtype=np.uint16)
+    yf = np.zeros((M, N), dtype=np.float32)
+    ya = np.zeros((M, N), dtype=np.float64)
+    _check(lib().vo_linear_bf16(_p(w), _p(x), M, N, K, _p(y), _p(yf), _p(ya)), "linear_bf16")
+    return y, yf, ya
+
+
+def argmax_bf16(logits_bf16):
+    lg = np.ascontiguousarray(logits_bf16, dtype=np.uint16)
+    B, V = lg.shape
+    out = np.zeros(B, dtype=np.int32)
+    _check(lib().vo_argmax_bf16(_p(lg), B, V, _p(out)), "argmax_bf16")
     return out
 
 

@@ -400,6 +400,52 @@ int vo_swiglu_bf16(const uint16_t* gate, const uint16_t* up, int M, int I, uint1
 }
 
 /* ------------------------------------------------------------------ */
+/* bf16 GEMV (LM head) and greedy argmax                               */
+/* ------------------------------------------------------------------ */
+
+int vo_linear_bf16(const uint16_t* w, const uint16_t* x, int M, int N, int K, uint16_t* y,
+                   float* y_f32, double* absterm) {
+    if (M <= 0 || N <= 0 || K <= 0) return -1;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int n = 0; n < N; ++n) {
+        const uint16_t* wr = w + (size_t)n * K;
+        for (int m = 0; m < M; ++m) {
+            const uint16_t* xr = x + (size_t)m * K;
+            double s = 0.0, a = 0.0;
+            for (int k = 0; k < K; ++k) {
+                const double p = (double)vo_bf16_to_f32(wr[k]) * (double)vo_bf16_to_f32(xr[k]);
+                s += p;
+                a += fabs(p);
+            }
+            const size_t o = (size_t)m * N + n;
+            y[o] = vo_f32_to_bf16((float)s);
+            if (y_f32) y_f32[o] = (float)s;
+            if (absterm) absterm[o] = a;
+        }
+    }
+    return 0;
+}
+
+int vo_argmax_bf16(const uint16_t* logits, int B, int V, int32_t* out) {
+    if (B <= 0 || V <= 0) return -1;
+    for (int b = 0; b < B; ++b) {
+        float best = -INFINITY;
+        int32_t idx = 0;
+        for (int v = 0; v < V; ++v) {
+            const float f = vo_bf16_to_f32(logits[(size_t)b * V + v]);
+            if (f > best) {  /* strict: the first occurrence wins, NaN never */
+                best = f;
+                idx = v;
+            }
+        }
+        out[b] = idx;
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
 /* exact group dots                                                    */
 /* ------------------------------------------------------------------ */
 

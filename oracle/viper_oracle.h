@@ -26,6 +26,13 @@
  *                         exp (the reference uses __expf; 1 bf16 ulp).
  *                         The quantize step after both is vo_quantize_act
  *                         (rmsnorm_quantize.cu:75-104, swiglu_quantize.cu:45-78).
+ *   vo_linear_bf16        kernels/ops/linear_bf16_kernel.cu:15-54: y[m][n] =
+ *                         bf16_RNE(sum_k f32(w[n][k]) * f32(x[m][k])); summed in
+ *                         double here (the reference's fp32 order is its own),
+ *                         with sum |w x| returned for the tolerance.
+ *   vo_argmax_bf16        kernels/ops/sampling_kernel.cu:11-63: per row, the
+ *                         smallest index of the largest f32(logit); NaN never
+ *                         wins; a row with no value above -inf gives 0.
  *   vo_group_dots         the exact int32 group sum that dp4a_q4_kernel.cu:116-150
  *                         forms and dp4a_smem_kernel.cu:49-58 / linear_multim.cu:
  *                         92-112 split into 8-element dp4a partials.
@@ -105,6 +112,14 @@ int vo_quantize_act(const uint16_t* x, int M, int K, int group, int8_t* xq, floa
 
 /* out[M][H] = rmsnorm(x) * gamma (bf16), per row; eps as the reference's cfg.rms_eps. */
 int vo_rmsnorm_bf16(const uint16_t* x, const uint16_t* gamma, float eps, int M, int H, uint16_t* out);
+
+/* y[M][N] (bf16) = x[M][K] w[N][K]^T, both bf16; y_f32 and absterm (may be NULL)
+ * receive the unrounded sum and sum |w x|. */
+int vo_linear_bf16(const uint16_t* w, const uint16_t* x, int M, int N, int K, uint16_t* y,
+                   float* y_f32, double* absterm);
+
+/* out[b] = greedy token of logits[b][V] (bf16). */
+int vo_argmax_bf16(const uint16_t* logits, int B, int V, int32_t* out);
 
 /* out[M][I] = silu(gate) * up (bf16). */
 int vo_swiglu_bf16(const uint16_t* gate, const uint16_t* up, int M, int I, uint16_t* out);

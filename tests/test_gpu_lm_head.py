@@ -1,0 +1,111 @@
+"""GPU parity of the LM head (bf16 GEMV) and greedy sampling against the CPU
+oracle, through the C ABI.
+
+Bar: logits within 1 bf16 ulp of the oracle's, or within 1e-5 * sum|w x|
+(the reference's fp32 summation order is its own); the greedy token exactly
+the oracle's argmax of the device's logits, and of the oracle's logits.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import viper_amd as va
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU (run them on the MI355X box)")
+    return torch
+
+
+def dev(torch, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to("cuda")
+
+
+def host_u16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def bf16(a):
+    return O.f32_to_bf16(np.asarray(a, dtype=np.float32))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4097, 2560), (3, 100, 1000), (1, 50, 64), (16, 33, 2048), (3, 70, 10240)])
+def test_linear_bf16(torch_dev, M, N, K):
+    torch = torch_dev
+    print(f"linear_bf16 M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(N + K + M)
+    w = bf16(0.05 * rng.standard_normal((N, K)))
+    x = O.gen_act(M, K, 900 + K)
+    y_ref, _, absterm = O.linear_bf16(w, x)
+    y = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    assert va.linear_bf16(dev(torch, w), dev(torch, x), y).ok()
+    torch.cuda.synchronize()
+    O.assert_bf16_close(host_u16(y), y_ref, absterm, rel=1e-5)
+
+
+def test_linear_bf16_limits_are_codes(torch_dev):
+    torch = torch_dev
+    w = torch.zeros((8, 10240), dtype=torch.int16, device="cuda")
+    x = torch.zeros((5, 10240), dtype=torch.int16, device="cuda")   # 100 KiB of activations: over the LDS limit
+    y = torch.zeros((5, 8), dtype=torch.int16, device="cuda")
+    assert va.linear_bf16(w, x, y).code == va.StatusCode.INVALID_ARGUMENT
+    x = torch.zeros((1, 10236), dtype=torch.int16, device="cuda")   # K % 8 != 0
+    assert va.linear_bf16(torch.zeros((8, 10236), dtype=torch.int16, device="cuda"), x, y[:1]).code == \
+        va.StatusCode.INVALID_ARGUMENT
+
+
+def test_lm_head_full_size_greedy(torch_dev):
+    # config 3's head: K=2560, N=166144 (850 MB of bf16 weights), M=1
+    torch = torch_dev
+    N, K = 166144, 2560
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x5EED0003)
+    wd = (0.02 * torch.randn((N, K), device="cuda", generator=g)).to(torch.bfloat16)
+    x = O.gen_act(1, K, 0x5EED0013)
+    y = torch.zeros((1, N), dtype=torch.int16, device="cuda")
+    tok = torch.full((1,), -1, dtype=torch.int32, device="cuda")
+    assert va.linear_bf16(wd, dev(torch, x), y).ok()
+    assert va.sampling_greedy(y, tok).ok()
+    torch.cuda.synchronize()
+    w = wd.view(torch.int16).cpu().numpy().view(np.uint16)
+    y_ref, _, absterm = O.linear_bf16(w, x)
+    yg = host_u16(y)
+    O.assert_bf16_close(yg, y_ref, absterm, rel=1e-5)
+    assert int(tok.item()) == int(O.argmax_bf16(yg)[0])
+    assert int(tok.item()) == int(O.argmax_bf16(y_ref)[0])
+
+
+def test_sampling_greedy_known_answers(torch_dev):
+    torch = torch_dev
+    rows = np.stack([
+        bf16([1.0, 3.0, 3.0, 2.0, -1.0, 0.0, 0.0, 0.0]),
+        bf16([np.nan, 0.5, np.nan, 0.25, 0.5, 0.0, -0.0, 0.1]),
+        bf16([-np.inf] * 8),
+        bf16([-np.inf, -5.0, np.inf, np.inf, 0.0, 0.0, 0.0, 0.0]),
+        bf16([-2.0, -1.0, -3.0, -1.0, -7.0, -9.0, -9.0, -9.0]),
+    ])
+    out = torch.zeros(5, dtype=torch.int32, device="cuda")
+    assert va.sampling_greedy(dev(torch, rows), out).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), [1, 1, 0, 2, 1])
+
+
+@pytest.mark.parametrize("B,V", [(3, 166144), (2, 1001), (4, 7)])
+def test_sampling_greedy_random(torch_dev, B, V):
+    torch = torch_dev
+    rng = np.random.default_rng(V)
+    lg = bf16(rng.standard_normal((B, V)))
+    lg[0, V // 3] = lg[0, V // 2] = bf16([9.0])[0]   # a tie across lanes: the smaller index
+    out = torch.zeros(B, dtype=torch.int32, device="cuda")
+    assert va.sampling_greedy(dev(torch, lg), out).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), O.argmax_bf16(lg))
+    assert out.cpu().numpy()[0] == V // 3

@@ -363,3 +363,38 @@ def test_swiglu_known_values_and_float64():
     gf, uf = O.bf16_to_f32(G).astype(np.float64), O.bf16_to_f32(U).astype(np.float64)
     ref = gf / (1.0 + np.exp(-gf)) * uf
     assert (np.abs(O.bf16_to_f32(got) - ref) <= O.bf16_ulp(got)).all()
+
+
+# ---- bf16 GEMV (LM head) and greedy argmax
+
+def test_linear_bf16_known_answers_and_float64():
+    rng = np.random.default_rng(5)
+    K = 2560
+    x = _bf16(rng.standard_normal((2, K)))
+    # unit rows pick one input each: y = x[k] exactly
+    w = np.zeros((4, K), dtype=np.uint16)
+    for n, k in enumerate((0, 7, 1000, K - 1)):
+        w[n, k] = _bf16([1.0])[0]
+    y, _, _ = O.linear_bf16(w, x)
+    np.testing.assert_array_equal(y, x[:, [0, 7, 1000, K - 1]])
+    # random: within the bf16 rounding of the float64 product
+    W = _bf16(0.05 * rng.standard_normal((300, K)))
+    y, yf, ya = O.linear_bf16(W, x)
+    ref = O.bf16_to_f32(x).astype(np.float64) @ O.bf16_to_f32(W).astype(np.float64).T
+    assert (np.abs(yf - ref) <= 1e-6 * ya + 1e-30).all()
+    np.testing.assert_array_equal(y, O.f32_to_bf16(yf))
+
+
+def test_argmax_ties_nan_inf():
+    f = lambda v: _bf16(v)
+    rows = np.stack([
+        f([1.0, 3.0, 3.0, 2.0, -1.0]),              # tie: first index
+        f([np.nan, 0.5, np.nan, 0.25, 0.5]),        # NaN never wins
+        f([-np.inf] * 5),                           # nothing above -inf: 0
+        f([-np.inf, -5.0, np.inf, np.inf, 0.0]),    # +inf, first occurrence
+        f([-2.0, -1.0, -3.0, -1.0, -7.0]),
+    ])
+    np.testing.assert_array_equal(O.argmax_bf16(rows), [1, 1, 0, 2, 1])
+    rng = np.random.default_rng(6)
+    big = _bf16(rng.standard_normal((3, 166144)))
+    np.testing.assert_array_equal(O.argmax_bf16(big), np.argmax(O.bf16_to_f32(big), axis=1))

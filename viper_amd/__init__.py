@@ -6,4 +6,4 @@ there is no CPU fallback.
 from .qlinear import (GROUP, MAX_M, QType, QuantizedWeight, ScaleEnc, Status, StatusCode,  # noqa: F401
                       check_quantizer, is_lossless, lib, linear, linear_fused2, linear_fused2_prequantized,
                       linear_partials, linear_prequantized, packed_bytes, qtype_name, quantize_act,
-                      rmsnorm_quantize, swiglu_quantize, workspace_bytes)
+                      linear_bf16, rmsnorm_quantize, sampling_greedy, swiglu_quantize, workspace_bytes)

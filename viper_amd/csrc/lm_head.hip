@@ -1,0 +1,226 @@
+// LM head: bf16 GEMV (the reference's linear_bf16,
+// kernels/ops/linear_bf16_kernel.cu:15-70) and greedy argmax
+// (sampling_greedy_bf16, kernels/ops/sampling_kernel.cu:11-80).
+//
+// GEMV: y[m][n] = bf16_RNE(sum_k w[n][k] * x[m][k]) with fp32 accumulation.
+// The matrix (vocab x hidden, e.g. 166144 x 2560 = 850 MB) is streamed once
+// from HBM: a team of TS lanes owns a row and each lane issues its 16-byte
+// chunks of the row at once (non-temporal loads), after the activation loads
+// (loads retire in issue order, so x is staged into LDS while the weights
+// are in flight).  Each 16-byte chunk is 8 bf16 and costs 4 v_dot2_f32_bf16
+// per activation row; teams are reduced with DPP in a fixed order.
+//
+// Argmax: one workgroup per logits row scans 16-byte octets; a lane keeps the
+// first index of its largest value (strict >, so NaN never wins and ties keep
+// the smaller index); lanes and waves combine by (value, then smaller index).
+
+#include "qlinear_host.h"
+
+namespace vq {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a), __builtin_bit_cast(bf16x2, b), c,
+                                           false);
+}
+
+constexpr int LH_CPL = 10;  // 16-byte chunk slots per lane per row segment
+constexpr int LH_XS = 4;    // activation octets per thread loaded before the weights
+
+template <int TS, int NTT, int MT, bool EXACT>
+__global__ void __launch_bounds__(NTT)
+gemv_bf16_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                 int M, int N, int K) {
+    constexpr int ROWS = NTT / TS;
+    extern __shared__ __align__(16) u32x4 lx[];  // [M][K/8]
+    const int tid = (int)threadIdx.x;
+    const int l = tid % TS;
+    const int rr = tid / TS;
+    const int row0 = (int)blockIdx.x * ROWS;
+    const int row = row0 + rr;
+    const int nrows = min(ROWS, N - row0);
+    const bool row_ok = rr < nrows;
+    const int CPR = K / 8;
+    const int nx = M * CPR;
+
+    // 1. activation octets, then the weight chunks of the first segment
+    const auto xr = buf(x, (uint32_t)nx * 16);
+    u32x4 xv[LH_XS];
+#pragma unroll
+    for (int i = 0; i < LH_XS; ++i) xv[i] = bload16(xr, (tid + NTT * i) * 16);
+    const uint32_t rbytes = (uint32_t)K * 2;
+    const auto wr = buf(w + (size_t)row0 * K, (uint32_t)nrows * rbytes);
+    const int segw = TS * LH_CPL;
+    const int nseg = EXACT ? 1 : (CPR + segw - 1) / segw;
+    u32x4 wv[LH_CPL];
+    auto load_seg = [&](int seg) {
+#pragma unroll
+        for (int j = 0; j < LH_CPL; ++j) {
+            const int c = seg * segw + j * TS + l;
+            const bool in = EXACT || c < CPR;
+            wv[j] = bload16<AUX_NT>(wr, in ? rr * (int)rbytes + c * 16 : OOB);
+        }
+    };
+    load_seg(0);
+
+    // 2. stage x into LDS
+#pragma unroll
+    for (int i = 0; i < LH_XS; ++i)
+        if (tid + NTT * i < nx) lx[tid + NTT * i] = xv[i];
+    for (int i = tid + NTT * LH_XS; i < nx; i += NTT) lx[i] = bload16(xr, i * 16);
+    lds_barrier();
+
+    // 3. dots
+    float acc[MT];
+#pragma unroll
+    for (int m = 0; m < MT; ++m) acc[m] = 0.0f;
+    for (int seg = 0; seg < nseg; ++seg) {
+        if (seg) load_seg(seg);
+#pragma unroll
+        for (int j = 0; j < LH_CPL; ++j) {
+            const int c = seg * segw + j * TS + l;
+            const bool ok = EXACT || c < CPR;
+            const int cc = EXACT ? c : min(c, CPR - 1);
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                if (m < M) {
+                    const u32x4 a = lx[m * CPR + cc];
+                    float t = acc[m];
+                    t = dot2_bf16(wv[j].x, a.x, t);
+                    t = dot2_bf16(wv[j].y, a.y, t);
+                    t = dot2_bf16(wv[j].z, a.z, t);
+                    t = dot2_bf16(wv[j].w, a.w, t);
+                    acc[m] = ok ? t : acc[m];  // a lane past the row adds nothing (not even 0 * inf)
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MT; ++m) {
+        if (m < M) {
+            const float v = team_sum<TS>(acc[m]);
+            if (l == 0 && row_ok) y[(size_t)m * N + row] = f2bf(v);
+        }
+    }
+}
+
+// (value, index) order of the greedy pick: larger value, then smaller index
+__device__ __forceinline__ void better(float& v, int& i, float ov, int oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+constexpr int AM_NT = 1024;
+
+__global__ void __launch_bounds__(AM_NT)
+argmax_bf16_kernel(const uint16_t* __restrict__ logits, int32_t* __restrict__ out, int V) {
+    __shared__ float sv[AM_NT / 64];
+    __shared__ int si[AM_NT / 64];
+    const int b = (int)blockIdx.x;
+    const int tid = (int)threadIdx.x;
+    const uint16_t* row = logits + (size_t)b * V;
+    float best = -__builtin_inff();
+    int idx = 0;
+    // octets first (16-byte loads when the row is 16-byte aligned), then the tail
+    const bool vec = ((((uintptr_t)row) & 15) == 0);
+    const int noct = vec ? V / 8 : 0;
+    for (int o = tid; o < noct; o += AM_NT) {
+        const u32x4 q = *(const u32x4*)(row + (size_t)o * 8);
+        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const float f = bf16f((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+            if (f > best) {
+                best = f;
+                idx = o * 8 + j;
+            }
+        }
+    }
+    for (int v = noct * 8 + tid; v < V; v += AM_NT) {
+        const float f = bf16f(row[v]);
+        if (f > best) {
+            best = f;
+            idx = v;
+        }
+    }
+    // The per-lane scans above visit indices in increasing order per lane but
+    // interleaved across lanes, so equal maxima resolve in the combine below.
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        better(best, idx, ov, oi);
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = best;
+        si[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < AM_NT / 64; ++i) better(best, idx, sv[i], si[i]);
+        out[b] = idx;
+    }
+}
+
+// ---- host
+
+typedef void (*lh_fn)(const uint16_t*, const uint16_t*, uint16_t*, int, int, int);
+
+template <int TS, bool EXACT>
+static lh_fn lh_pick_mt(int mt) {
+    switch (mt) {
+        case 1: return gemv_bf16_kernel<TS, 256, 1, EXACT>;
+        case 4: return gemv_bf16_kernel<TS, 256, 4, EXACT>;
+        default: return gemv_bf16_kernel<TS, 256, 16, EXACT>;
+    }
+}
+template <int TS>
+static lh_fn lh_pick(int mt, bool exact) {
+    return exact ? lh_pick_mt<TS, true>(mt) : lh_pick_mt<TS, false>(mt);
+}
+
+}  // namespace vq
+
+extern "C" int viper_hip_linear_bf16(const void* w_bf16, const void* x_bf16, void* y_bf16, int M, int N,
+                                     int K, void* stream) {
+    if (w_bf16 == nullptr || x_bf16 == nullptr || y_bf16 == nullptr) return VIPER_INVALID_ARGUMENT;
+    if (M <= 0 || N <= 0 || K <= 0 || M > VIPER_QLINEAR_MAX_M || K % 8 != 0) return VIPER_INVALID_ARGUMENT;
+    if (vq::misaligned(w_bf16, 16) || vq::misaligned(x_bf16, 16) || vq::misaligned(y_bf16, 2))
+        return VIPER_INVALID_ARGUMENT;
+    const size_t lds = (size_t)M * K * 2;
+    if (lds > (size_t)vq::LDS_MAX || (size_t)K * 2 * 256 > (size_t)INT32_MAX) return VIPER_INVALID_ARGUMENT;
+    const int cpr = K / 8;
+    int ts = 8;
+    while (ts < 64 && ts * vq::LH_CPL < cpr) ts *= 2;
+    const bool exact = cpr == ts * vq::LH_CPL;
+    const int mt = M == 1 ? 1 : M <= 4 ? 4 : 16;
+    vq::lh_fn fn;
+    switch (ts) {
+        case 8: fn = vq::lh_pick<8>(mt, exact); break;
+        case 16: fn = vq::lh_pick<16>(mt, exact); break;
+        case 32: fn = vq::lh_pick<32>(mt, exact); break;
+        default: fn = vq::lh_pick<64>(mt, exact); break;
+    }
+    const int rows = 256 / ts;
+    const unsigned grid = (unsigned)((N + rows - 1) / rows);
+    const uint16_t* a0 = (const uint16_t*)w_bf16;
+    const uint16_t* a1 = (const uint16_t*)x_bf16;
+    uint16_t* a2 = (uint16_t*)y_bf16;
+    void* args[] = {&a0, &a1, &a2, &M, &N, &K};
+    (void)hipLaunchKernel((const void*)fn, dim3(grid), dim3(256), args, lds, (hipStream_t)stream);
+    return vq::status_of(hipGetLastError());
+}
+
+extern "C" int viper_hip_sampling_greedy(const void* logits_bf16, int32_t* out_token, int B, int V,
+                                         void* stream) {
+    if (logits_bf16 == nullptr || out_token == nullptr || B <= 0 || V <= 0) return VIPER_INVALID_ARGUMENT;
+    if (vq::misaligned(logits_bf16, 2) || vq::misaligned(out_token, 4)) return VIPER_INVALID_ARGUMENT;
+    const uint16_t* a0 = (const uint16_t*)logits_bf16;
+    void* args[] = {&a0, &out_token, &V};
+    (void)hipLaunchKernel((const void*)vq::argmax_bf16_kernel, dim3((unsigned)B), dim3(vq::AM_NT), args, 0,
+                          (hipStream_t)stream);
+    return vq::status_of(hipGetLastError());
+}

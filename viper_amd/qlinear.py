@@ -125,6 +125,8 @@ _SYMBOLS = (
     "viper_hip_qlinear_fused2_prequantized",
     "viper_hip_rmsnorm_quantize",
     "viper_hip_swiglu_quantize",
+    "viper_hip_linear_bf16",
+    "viper_hip_sampling_greedy",
 )
 
 
@@ -164,6 +166,10 @@ def lib():
     L.viper_hip_rmsnorm_quantize.restype = i32
     L.viper_hip_swiglu_quantize.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, vp]
     L.viper_hip_swiglu_quantize.restype = i32
+    L.viper_hip_linear_bf16.argtypes = [vp, vp, vp, i32, i32, i32, vp]
+    L.viper_hip_linear_bf16.restype = i32
+    L.viper_hip_sampling_greedy.argtypes = [vp, vp, i32, i32, vp]
+    L.viper_hip_sampling_greedy.restype = i32
     _lib = L
     return L
 
@@ -302,6 +308,22 @@ def swiglu_quantize(gate, up, group, xq, xs, out=None, stream=None) -> Status:
     rc = lib().viper_hip_swiglu_quantize(ptr(gate), ptr(up), M, I, group, ptr(out), ptr(xq), ptr(xs),
                                          _stream(stream))
     return _status(rc, "viper_hip_swiglu_quantize")
+
+
+def linear_bf16(w, x, y, stream=None) -> Status:
+    """y[M, N] = x[M, K] w[N, K]^T, all bf16 (the LM head)."""
+    N, K = w.shape
+    M = int(x.numel() // K)
+    rc = lib().viper_hip_linear_bf16(ptr(w), ptr(x), ptr(y), M, N, K, _stream(stream))
+    return _status(rc, "viper_hip_linear_bf16")
+
+
+def sampling_greedy(logits, out_token, stream=None) -> Status:
+    """out_token[b] = argmax of logits[b, :] (bf16), smallest index on ties."""
+    V = logits.shape[-1]
+    B = int(logits.numel() // V)
+    rc = lib().viper_hip_sampling_greedy(ptr(logits), ptr(out_token), B, V, _stream(stream))
+    return _status(rc, "viper_hip_sampling_greedy")
 
 
 def check_quantizer(exp_lo, exp_hi, counts, stream=None) -> Status:
