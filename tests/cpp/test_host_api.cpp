@@ -4,7 +4,10 @@
 // src/viper/linear.cpp:16-36; argument rules as kernels/ops/linear_multim.cu:152).
 #include <cstdio>
 #include <string>
+#include <unistd.h>
 
+#include "artifact_writer.h"
+#include "viper/artifact.h"
 #include "viper/ops.h"
 #include "viper/quant.h"
 #include "viper/tensor.h"
@@ -90,6 +93,64 @@ int main() {
     Tensor xq(fake, DType::INT8, {128}), xs(fake, DType::FP32, {2});
     EXPECT(ops::quantize_activations(x, 48, xq, xs).code() == StatusCode::INVALID_ARGUMENT);
     EXPECT(ops::quantize_activations(x, 64, xq, y).code() == StatusCode::INVALID_ARGUMENT);
+
+    // .viper v1 artifact: index, offsets and every rejection path
+    {
+        namespace A = artifact;
+        ArtifactDims d;
+        std::vector<uint8_t> f = write_artifact(d, hash_fill);
+        A::Index idx;
+        EXPECT(A::parse(f.data(), f.size(), &idx).ok());
+        EXPECT(idx.header.version == 1 && idx.header.n_layers == 2 && idx.header.hidden == 128 &&
+               idx.header.vocab == 300);
+        EXPECT(idx.layers.size() == 2 && idx.norms.size() == 2);
+        EXPECT(idx.layers[1][A::DOWN].rows == 128 && idx.layers[1][A::DOWN].cols == 256);
+        EXPECT(idx.layers[0][A::K].rows == 64 && idx.layers[0][A::O].cols == 128);
+        EXPECT(idx.layers[0][A::Q].packed.offset == A::kHeaderBytes + 8);
+        std::vector<uint8_t> want;
+        hash_fill("up_proj.scales", 1, 256 * 2 * 2, want);
+        const A::Blob& b = idx.layers[1][A::UP].scales;
+        EXPECT(b.size == want.size() && std::memcmp(f.data() + b.offset, want.data(), want.size()) == 0);
+        hash_fill("post_attention_layernorm", 0, 256, want);
+        EXPECT(std::memcmp(f.data() + idx.norms[0][1].offset, want.data(), 256) == 0);
+        hash_fill("lm_head", -1, 300 * 64, want);
+        EXPECT(std::memcmp(f.data() + idx.lm_head.packed.offset, want.data(), want.size()) == 0);
+
+        std::vector<uint8_t> g = f;
+        g[2] = 'x';
+        EXPECT(A::parse(g.data(), g.size(), &idx).code() == StatusCode::INVALID_ARGUMENT);
+        g = write_artifact(d, hash_fill, 2);
+        EXPECT(A::parse(g.data(), g.size(), &idx).code() == StatusCode::INVALID_ARGUMENT);
+        EXPECT(A::parse(f.data(), f.size() - 1, &idx).code() == StatusCode::IO_ERROR);
+        EXPECT(A::parse(f.data(), 40, &idx).code() == StatusCode::IO_ERROR);
+        g = f;
+        g.push_back(0);
+        EXPECT(A::parse(g.data(), g.size(), &idx).code() == StatusCode::IO_ERROR);
+        // one section a byte short (of the right total length): its size field disagrees
+        auto short_fill = [](const std::string& name, int layer, size_t bytes, std::vector<uint8_t>& out) {
+            hash_fill(name, layer, bytes, out);
+            if (name == "k_proj.scales" && layer == 1) out.pop_back();
+        };
+        g = write_artifact(d, short_fill);
+        EXPECT(A::parse(g.data(), g.size(), &idx).code() == StatusCode::INVALID_ARGUMENT);
+        ArtifactDims odd = d;
+        odd.hidden = 96;  // not a multiple of the 64-group
+        g = write_artifact(odd, hash_fill);
+        EXPECT(A::parse(g.data(), g.size(), &idx).code() == StatusCode::INVALID_ARGUMENT);
+
+        char path[] = "/tmp/viper_artifact_XXXXXX";
+        const int fd = mkstemp(path);
+        EXPECT(fd >= 0 && write(fd, f.data(), f.size()) == (ssize_t)f.size());
+        close(fd);
+        {
+            A::MappedFile mf;
+            EXPECT(mf.open(path).ok() && mf.size() == f.size());
+            EXPECT(A::parse(mf.data(), mf.size(), &idx).ok());
+        }
+        unlink(path);
+        A::MappedFile missing;
+        EXPECT(missing.open("/nonexistent/model.viper").code() == StatusCode::IO_ERROR);
+    }
 
     std::printf("%s (%d failures)\n", failures ? "FAILED" : "PASS", failures);
     return failures ? 1 : 0;

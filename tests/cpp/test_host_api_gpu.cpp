@@ -10,6 +10,8 @@
 #include <cstring>
 #include <vector>
 
+#include "artifact_writer.h"
+#include "viper/artifact.h"
 #include "viper/ops.h"
 #include "viper_oracle.h"
 
@@ -143,7 +145,104 @@ static int run_case(int qt, int senc, int N, int K, int M, uint64_t seed) {
     return fails;
 }
 
+// A synthetic .viper artifact with real Q4 data (oracle weights with bf16
+// scales) is parsed and uploaded; linears run from the uploaded views and
+// the bf16 sections read back byte for byte.
+static int artifact_case() {
+    namespace A = artifact;
+    std::printf("case artifact upload\n");
+    std::fflush(stdout);
+    ArtifactDims d;
+    auto fill = [&](const std::string& name, int layer, size_t bytes, std::vector<uint8_t>& out) {
+        const bool scales = name.size() > 7 && name.compare(name.size() - 7, 7, ".scales") == 0;
+        const std::string base = scales ? name.substr(0, name.size() - 7) : name;
+        const bool linear = base != "embed" && base != "final_norm" && base != "input_layernorm" &&
+                            base != "post_attention_layernorm";
+        if (!linear) {
+            hash_fill(name, layer, bytes, out);
+            for (size_t i = 1; i < bytes; i += 2) out[i] &= 0x3f;  // finite bf16 bit patterns
+            return;
+        }
+        // rows x cols from the byte counts: packed = rows*cols/2, scales = rows*(cols/64)*2
+        int rows, cols;
+        if (base == "q_proj") rows = 128, cols = 128;
+        else if (base == "k_proj" || base == "v_proj") rows = 64, cols = 128;
+        else if (base == "o_proj") rows = 128, cols = 128;
+        else if (base == "gate_proj" || base == "up_proj") rows = 256, cols = 128;
+        else if (base == "down_proj") rows = 128, cols = 256;
+        else rows = 300, cols = 128;  // lm_head
+        std::vector<uint8_t> packed((size_t)rows * cols / 2);
+        std::vector<uint16_t> sc((size_t)rows * (cols / 64));
+        const uint64_t seed = 0xA0000 + (uint64_t)(layer + 1) * 16 + (uint64_t)(base.size() * 131 + base[0]);
+        vo_gen_weights(VO_Q4_G64, rows, cols, seed, VO_SCALE_BF16, packed.data(), sc.data());
+        if (scales) out.assign((const uint8_t*)sc.data(), (const uint8_t*)sc.data() + sc.size() * 2);
+        else out = packed;
+        if (out.size() != bytes) std::printf("FAIL artifact writer size %s\n", name.c_str());
+    };
+    std::vector<uint8_t> f = write_artifact(d, fill);
+    A::Index idx;
+    Status st = A::parse(f.data(), f.size(), &idx);
+    if (!st.ok()) {
+        std::printf("FAIL artifact parse\n");
+        return 1;
+    }
+    A::DeviceModel dm;
+    st = A::upload(f.data(), idx, &dm);
+    if (!st.ok()) {
+        std::printf("FAIL artifact upload: %.*s\n", (int)st.message().size(), st.message().data());
+        return 1;
+    }
+    int fails = 0;
+    // every view 256-byte aligned
+    for (auto& layer : dm.layers)
+        for (auto& w : layer)
+            if (((uintptr_t)w.data & 255) || ((uintptr_t)w.scales & 255)) ++fails;
+    // linears from the uploaded views
+    struct Pick {
+        quant::QuantizedWeight w;
+        const A::LinearBlob* b;
+    };
+    const Pick picks[] = {{dm.layers[0][A::Q], &idx.layers[0][A::Q]},
+                          {dm.layers[1][A::DOWN], &idx.layers[1][A::DOWN]},
+                          {dm.lm_head, &idx.lm_head}};
+    for (const Pick& pk : picks) {
+        const int N = pk.w.rows, K = pk.w.cols;
+        std::vector<uint16_t> x(K), yref(N);
+        std::vector<float> yf(N);
+        std::vector<double> ya(N);
+        vo_gen_act(1, K, 77 + N, 0.0, 1.0f, x.data());
+        vo_qlinear(VO_Q4_G64, f.data() + pk.b->packed.offset, (const uint16_t*)(f.data() + pk.b->scales.offset),
+                   VO_SCALE_BF16, N, K, x.data(), 1, nullptr, yref.data(), yf.data(), ya.data());
+        uint16_t* dx = upload(x);
+        uint16_t* dy = nullptr;
+        CHECK_HIP(hipMalloc(&dy, (size_t)N * 2));
+        Tensor tx(dx, DType::BF16, {K}), ty(dy, DType::BF16, {N});
+        st = ops::linear(pk.w, tx, ty);
+        if (!st.ok()) return 1;
+        CHECK_HIP(hipDeviceSynchronize());
+        std::vector<uint16_t> yg(N);
+        CHECK_HIP(hipMemcpy(yg.data(), dy, (size_t)N * 2, hipMemcpyDeviceToHost));
+        fails += close_bf16(yg, yref, ya, "artifact linear") ? 0 : 1;
+        (void)hipFree(dx);
+        (void)hipFree(dy);
+    }
+    // bf16 sections round trip
+    auto same = [&](const void* dptr, const A::Blob& b) {
+        std::vector<uint8_t> h(b.size);
+        if (hipMemcpy(h.data(), dptr, b.size, hipMemcpyDeviceToHost) != hipSuccess) return false;
+        return std::memcmp(h.data(), f.data() + b.offset, b.size) == 0;
+    };
+    if (!same(dm.embed, idx.embed) || !same(dm.final_norm, idx.final_norm) ||
+        !same(dm.norms[1][0], idx.norms[1][0]) || !same(dm.norms[0][1], idx.norms[0][1])) {
+        std::printf("FAIL artifact bf16 sections\n");
+        ++fails;
+    }
+    if (!A::release(&dm).ok() || dm.arena != nullptr) ++fails;
+    return fails;
+}
+
 int main() {
+    failures += artifact_case();
     const int qts[] = {VO_Q4_G64, VO_Q5_G64, VO_Q6_G64, VO_W8_G32};
     for (int qt : qts)
         for (int senc : {0, 1})
