@@ -269,6 +269,24 @@ def main():
         extras["greedy_argmax_us"] = round(greedy_us, 3)
         del gh, gg, Wh
 
+        # config 3: 22 weight sets x 2 passes (44 slots) of the linear path +
+        # final norm + bf16 LM head + greedy token, one step = one graph replay
+        from viper_amd.stack import Stack
+        stk = Stack(torch)
+        stk.step()
+        torch.cuda.synchronize()
+        g3 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g3):
+            stk.step()
+        g3.replay()
+        torch.cuda.synchronize()
+        s3_ms = time_graph(torch, g3, 10) / 10
+        s3_bytes = stk.weight_bytes_per_step() + 4_595_712 + 337_408
+        extras["config3_step_us"] = round(s3_ms * 1e3, 1)
+        extras["config3_step_gbs"] = round(s3_bytes / (s3_ms * 1e-3) / 1e9, 1)
+        extras["config3_launches_per_step"] = 9 * stk.layers * stk.passes + 3
+        del g3, stk
+
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_q4_m1_k2560_n10240.json")
     if os.path.exists(tpath):

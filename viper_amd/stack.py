@@ -1,0 +1,108 @@
+"""Config-3 decode step of the quantized linear path, driven through the C ABI.
+
+A stack of `layers` weight sets applied `passes` times (the reference's
+looped 22-layer model: 44 slots, each weight set read twice), then the final
+norm, the bf16 LM head and the greedy token.  Per slot, the linear-path
+launches of the reference engine's decode step
+(include/viper/model_impl.cuh:650-728), attention itself excluded (it is not
+on this path; its output is a fixed activation):
+
+    rmsnorm_quantize(x, input_ln)  -> q GEMV, fused2(k, v)
+    quantize(attn)                 -> o GEMV + residual (in place on x)
+    rmsnorm_quantize(x, post_ln)   -> fused2(gate, up)
+    swiglu_quantize(gate, up)      -> down GEMV + residual (in place on x)
+
+Device buffers are torch tensors (allocation only); every launch is a C ABI
+call on the current stream, so a whole step can be captured in a HIP graph.
+"""
+import math
+
+from . import qlinear as _q
+
+Q4 = int(_q.QType.Q4_G64)
+
+
+class Stack:
+    def __init__(self, torch, hidden=2560, inter=10240, n_heads=20, n_kv_heads=4, head_dim=128,
+                 layers=22, passes=2, vocab=166144, seed=0x5EED0003, eps=1e-6):
+        self.torch = torch
+        self.H, self.I = hidden, inter
+        self.nQ, self.nKV = n_heads * head_dim, n_kv_heads * head_dim
+        self.layers, self.passes, self.V, self.eps = layers, passes, vocab, eps
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        self.gen = g
+        H, I, nQ, nKV = self.H, self.I, self.nQ, self.nKV
+        shapes = [(nQ, H), (nKV, H), (nKV, H), (H, nQ), (I, H), (I, H), (H, I)]
+        self.w = []   # per layer: 7 (packed, scales) pairs
+        for _ in range(layers):
+            lw = []
+            for (n, k) in shapes:
+                packed = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device="cuda", generator=g)
+                u = torch.rand((n * (k // 64),), device="cuda", generator=g)
+                scales = torch.exp(math.log(1e-3) + u * math.log(10.0)).to(torch.float16)
+                lw.append((packed, scales, n, k))
+            self.w.append(lw)
+        bf = torch.bfloat16
+        self.ln = [(1.0 + 0.05 * torch.randn((H,), device="cuda", generator=g)).to(bf) for _ in range(2 * layers)]
+        self.final_ln = (1.0 + 0.05 * torch.randn((H,), device="cuda", generator=g)).to(bf)
+        self.head = (0.02 * torch.randn((vocab, H), device="cuda", generator=g)).to(bf)
+        self.x0 = torch.randn((1, H), device="cuda", generator=g).to(bf)
+        self.attn = torch.randn((1, nQ), device="cuda", generator=g).to(bf)
+        self.x = torch.empty((1, H), dtype=bf, device="cuda")
+        self.q = torch.empty((1, nQ), dtype=bf, device="cuda")
+        self.k = torch.empty((1, nKV), dtype=bf, device="cuda")
+        self.v = torch.empty((1, nKV), dtype=bf, device="cuda")
+        self.gt = torch.empty((1, I), dtype=bf, device="cuda")
+        self.ut = torch.empty((1, I), dtype=bf, device="cuda")
+        self.xn = torch.empty((1, H), dtype=bf, device="cuda")
+        kmax = max(H, I, nQ)
+        self.xq = torch.empty((kmax,), dtype=torch.int8, device="cuda")
+        self.xs = torch.empty((kmax // 64,), dtype=torch.float32, device="cuda")
+        self.logits = torch.empty((1, vocab), dtype=bf, device="cuda")
+        self.token = torch.empty((1,), dtype=torch.int32, device="cuda")
+        L = _q.lib()
+        self.L = L
+
+    def weight_bytes_per_step(self):
+        per_layer = sum(p.numel() + s.numel() * 2 for (p, s, _, _) in self.w[0])
+        return per_layer * self.layers * self.passes + self.head.numel() * 2
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {rc}")
+
+    def step(self):
+        """One decode step of the linear path, reference launch sequence."""
+        torch, L = self.torch, self.L
+        st = torch.cuda.current_stream().cuda_stream
+        H, I, nQ, nKV = self.H, self.I, self.nQ, self.nKV
+        p = lambda t: t.data_ptr()
+        x = self.x
+        x.copy_(self.x0)
+        for loop in range(self.passes):
+            for l in range(self.layers):
+                wq, wk, wv, wo, wg, wu, wd = self.w[l]
+                self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(self.ln[2 * l]), self.eps, 1, H, 64, p(self.xn),
+                                                      p(self.xq), p(self.xs), st), "rmsnorm_quantize")
+                self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wq[0]), p(wq[1]), 0, 64, nQ, H, p(self.xq),
+                                                          p(self.xs), 1, p(self.q), None, st), "q")
+                self._ok(L.viper_hip_qlinear_fused2_prequantized(Q4, p(wk[0]), p(wk[1]), p(wv[0]), p(wv[1]), 0, 64,
+                                                                 nKV, H, p(self.xq), p(self.xs), 1, p(self.k),
+                                                                 p(self.v), st), "kv")
+                self._ok(L.viper_hip_quantize_act(64, p(self.attn), 1, nQ, p(self.xq), p(self.xs), st), "quantize")
+                self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wo[0]), p(wo[1]), 0, 64, H, nQ, p(self.xq),
+                                                          p(self.xs), 1, p(x), p(x), st), "o")
+                self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(self.ln[2 * l + 1]), self.eps, 1, H, 64, p(self.xn),
+                                                      p(self.xq), p(self.xs), st), "rmsnorm_quantize")
+                self._ok(L.viper_hip_qlinear_fused2_prequantized(Q4, p(wg[0]), p(wg[1]), p(wu[0]), p(wu[1]), 0, 64,
+                                                                 I, H, p(self.xq), p(self.xs), 1, p(self.gt),
+                                                                 p(self.ut), st), "gate_up")
+                self._ok(L.viper_hip_swiglu_quantize(p(self.gt), p(self.ut), 1, I, 64, p(self.gt), p(self.xq),
+                                                     p(self.xs), st), "swiglu_quantize")
+                self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wd[0]), p(wd[1]), 0, 64, H, I, p(self.xq),
+                                                          p(self.xs), 1, p(x), p(x), st), "down")
+        self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(self.final_ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
+                                              p(self.xs), st), "final norm")
+        self._ok(L.viper_hip_linear_bf16(p(self.head), p(self.xn), p(self.logits), 1, self.V, H, st), "lm_head")
+        self._ok(L.viper_hip_sampling_greedy(p(self.logits), p(self.token), 1, self.V, st), "greedy")
