@@ -32,6 +32,11 @@
  *                                   include/viper/model_impl.cuh:652,725) on one
  *                                   quantized activation in one launch.
  *   viper_hip_qlinear_fused2        the same from bf16 x (quantize fused at M = 1).
+ *   viper_hip_qlinear_m1            no single counterpart: one launch for what the engine
+ *                                   does in two to four (include/viper/model_impl.cuh:650-652,
+ *                                   719-720, 724-725, 727-728): the producer (rmsnorm+quantize,
+ *                                   swiglu+quantize, quantize) folded into the GEMV prologue,
+ *                                   and up to three matrices (q, k, v / gate, up) per launch.
  *   viper_hip_rmsnorm_quantize      rmsnorm_quantize_bf16 (kernels/ops/rmsnorm_quantize.cu:107-123,
  *                                   declared kernels/ops/rmsnorm_kernel.h), per row.
  *   viper_hip_swiglu_quantize       swiglu_quantize_bf16 (kernels/ops/swiglu_quantize.cu:81-96).
@@ -141,6 +146,27 @@ int viper_hip_qlinear_fused2_prequantized(int qtype, const void* w0_packed, cons
                                           int scale_enc, int group, int N, int K, const void* xq,
                                           const void* xs, int M, void* y0_bf16, void* y1_bf16,
                                           void* stream);
+
+/* Prologues of viper_hip_qlinear_m1 (what a and b hold). */
+#define VIPER_PROLOGUE_BF16 0    /* a: x bf16 [K], quantized in the kernel */
+#define VIPER_PROLOGUE_INT8 1    /* a: xq int8 [K], b: xs fp32 [K/group] (8- and 4-byte aligned) */
+#define VIPER_PROLOGUE_RMSNORM 2 /* a: x bf16 [K], b: gamma bf16 [K]; v = bf16((x * rsqrt(sum x^2 / K + eps)) * gamma) */
+#define VIPER_PROLOGUE_SWIGLU 3  /* a: gate bf16 [K], b: up bf16 [K]; v = bf16(gate / (1 + exp(-gate)) * up) */
+
+/* M = 1: y_i[N_i] = linear(w_i, v) for n_out = 1..3 matrices of one qtype,
+ * scale encoding and K (each with its own N_i), where v is the activation
+ * row the prologue produces and quantizes (exactly as viper_hip_rmsnorm_quantize
+ * / viper_hip_swiglu_quantize / viper_hip_quantize_act would), all in one
+ * launch.  w_packed, w_scales, N and y_bf16 are host arrays of n_out entries.
+ * residual (may be NULL, may alias y_bf16[0]) is added to output 0.
+ * norm_out (RMSNORM only, may be NULL) receives the bf16 row v.  The
+ * RMSNORM and SWIGLU prologues need K <= 20480 (Q4/Q5/Q6; the whole row is
+ * held after one load round); a, b and norm_out 16-byte aligned unless
+ * stated. */
+int viper_hip_qlinear_m1(int qtype, int scale_enc, int group, int K, int prologue, const void* a, const void* b,
+                         float eps, void* norm_out, int n_out, const void* const* w_packed,
+                         const void* const* w_scales, const int* N, void* const* y_bf16,
+                         const void* residual_bf16, void* stream);
 
 /* Producer-side activation quantize, per row m < M of H (or I) elements:
  *   rmsnorm: v = bf16_RNE((x * rsqrt(sum(x^2)/H + eps)) * gamma),

@@ -1,0 +1,149 @@
+"""GPU parity of viper_hip_qlinear_m1: producers folded into the M = 1 GEMV
+prologue and up to three matrices per launch.
+
+The folded prologues run the same arithmetic as the standalone producer
+kernels, so at the engine's shapes (K = 2560 rmsnorm with 320 threads on both
+sides, swiglu element-wise) the outputs must equal the two-launch chain bit
+for bit; elsewhere they are checked against the oracle chain fed with the
+kernel's own normalized row (norm_out), to the usual bar.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import viper_amd as va
+
+pytestmark = pytest.mark.gpu
+P = va.Prologue
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU (run them on the MI355X box)")
+    return torch
+
+
+def dev(torch, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to("cuda")
+
+
+def u16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def weights(torch, qtype, N, K, seed, senc=O.SCALE_FP16):
+    G = O.group_size(qtype)
+    p, s = O.gen_weights(qtype, N, K, seed, senc)
+    return va.QuantizedWeight(va.QType(qtype), dev(torch, p), dev(torch, s), N, K, G, va.ScaleEnc(senc)), p, s
+
+
+def bf16(a):
+    return O.f32_to_bf16(np.asarray(a, dtype=np.float32))
+
+
+def test_rmsnorm_qkv_equals_two_launches(torch_dev):
+    # engine shape: q (2560), k and v (512) from rmsnorm(x) in one launch
+    torch = torch_dev
+    K, eps = 2560, 1e-6
+    ws = [weights(torch, O.Q4_G64, n, K, 500 + i)[0] for i, n in enumerate((2560, 512, 512))]
+    x = dev(torch, O.gen_act(1, K, 510, outlier_frac=0.02))
+    rng = np.random.default_rng(511)
+    gamma = dev(torch, bf16(1.0 + 0.1 * rng.standard_normal(K)))
+    ys = [torch.zeros((1, w.rows), dtype=torch.int16, device="cuda") for w in ws]
+    norm = torch.zeros((1, K), dtype=torch.int16, device="cuda")
+    assert va.linear_m1(ws, P.RMSNORM, x, gamma, ys, eps=eps, norm_out=norm).ok()
+    # two-launch chain
+    xq = torch.zeros((1, K), dtype=torch.int8, device="cuda")
+    xs = torch.zeros((1, K // 64), dtype=torch.float32, device="cuda")
+    norm2 = torch.zeros_like(norm)
+    assert va.rmsnorm_quantize(x, gamma, eps, 64, xq, xs, out=norm2).ok()
+    refs = [torch.zeros_like(y) for y in ys]
+    for w, r in zip(ws, refs):
+        assert va.linear_prequantized(w, xq, xs, r).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(norm), u16(norm2))
+    for y, r in zip(ys, refs):
+        np.testing.assert_array_equal(u16(y), u16(r))
+
+
+def test_swiglu_down_residual_equals_two_launches(torch_dev):
+    # engine shape: down (K=10240, N=2560) from silu(gate) * up, residual in place
+    torch = torch_dev
+    K, N = 10240, 2560
+    w = weights(torch, O.Q4_G64, N, K, 520)[0]
+    rng = np.random.default_rng(521)
+    g = dev(torch, bf16(3.0 * rng.standard_normal((1, K))))
+    u = dev(torch, bf16(rng.standard_normal((1, K))))
+    res = O.gen_act(1, N, 522)
+    y = dev(torch, res)
+    assert va.linear_m1([w], P.SWIGLU, g, u, [y], residual=y).ok()
+    xq = torch.zeros((1, K), dtype=torch.int8, device="cuda")
+    xs = torch.zeros((1, K // 64), dtype=torch.float32, device="cuda")
+    assert va.swiglu_quantize(g, u, 64, xq, xs).ok()
+    r = dev(torch, res)
+    assert va.linear_prequantized(w, xq, xs, r, residual=r).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(y), u16(r))
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_G64, O.Q5_G64, O.Q6_G64, O.W8_G32])
+def test_rmsnorm_prologue_against_oracle(torch_dev, qtype):
+    torch = torch_dev
+    K, eps = 4096, 1e-5
+    trip = [weights(torch, qtype, n, K, 530 + n, O.SCALE_BF16) for n in (300, 64)]
+    ws = [t[0] for t in trip]
+    x = O.gen_act(1, K, 531, outlier_frac=0.05)
+    rng = np.random.default_rng(532)
+    gamma = bf16(1.0 + 0.1 * rng.standard_normal(K))
+    ys = [torch.zeros((1, w.rows), dtype=torch.int16, device="cuda") for w in ws]
+    norm = torch.zeros((1, K), dtype=torch.int16, device="cuda")
+    assert va.linear_m1(ws, P.RMSNORM, dev(torch, x), dev(torch, gamma), ys, eps=eps, norm_out=norm).ok()
+    torch.cuda.synchronize()
+    nv = u16(norm)
+    ref = O.rmsnorm_bf16(x, gamma, eps)
+    assert (np.abs(O.bf16_to_f32(nv).astype(np.float64) - O.bf16_to_f32(ref)) <= O.bf16_ulp(ref)).all()
+    xq, xs = O.quantize_act(nv, O.group_size(qtype))
+    for (w, p, s), y in zip(trip, ys):
+        y_ref, _, absterm = O.qlinear_prequant(qtype, p, s, O.SCALE_BF16, w.rows, K, xq, xs)
+        O.assert_bf16_close(u16(y), y_ref, absterm, rel=1e-5)
+
+
+@pytest.mark.parametrize("prologue", [P.BF16, P.INT8])
+def test_three_matrices_equal_single_calls(torch_dev, prologue):
+    torch = torch_dev
+    K = 2560
+    ws = [weights(torch, O.Q6_G64, n, K, 540 + n)[0] for n in (1000, 77, 256)]
+    x = O.gen_act(1, K, 541)
+    xq, xs = O.quantize_act(x, 64)
+    a, b = (dev(torch, x), None) if prologue == P.BF16 else (dev(torch, xq), dev(torch, xs))
+    ys = [torch.zeros((1, w.rows), dtype=torch.int16, device="cuda") for w in ws]
+    res = dev(torch, O.gen_act(1, 1000, 542))
+    assert va.linear_m1(ws, prologue, a, b, ys, residual=res).ok()
+    refs = [torch.zeros_like(y) for y in ys]
+    for i, (w, r) in enumerate(zip(ws, refs)):
+        rr = res if i == 0 else None
+        if prologue == P.BF16:
+            assert va.linear(w, a, r, residual=rr).ok()
+        else:
+            assert va.linear_prequantized(w, a, b, r, residual=rr).ok()
+    torch.cuda.synchronize()
+    for y, r in zip(ys, refs):
+        np.testing.assert_array_equal(u16(y), u16(r))
+
+
+def test_m1_errors_are_codes(torch_dev):
+    torch = torch_dev
+    w = weights(torch, O.Q4_G64, 64, 24576, 550)[0]
+    x = torch.zeros((1, 24576), dtype=torch.int16, device="cuda")
+    y = torch.zeros((1, 64), dtype=torch.int16, device="cuda")
+    # the folded prologues hold at most 20480 elements
+    assert va.linear_m1([w], P.SWIGLU, x, x, [y]).code == va.StatusCode.INVALID_ARGUMENT
+    assert va.linear_m1([w], P.BF16, x, None, [y]).ok()
+    assert va.linear_m1([w] * 4, P.BF16, x, None, [y] * 4).code == va.StatusCode.INVALID_ARGUMENT
+    assert va.linear_m1([w], P.BF16, x, None, [y], norm_out=x).code == va.StatusCode.INVALID_ARGUMENT
+    torch.cuda.synchronize()

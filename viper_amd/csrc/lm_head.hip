@@ -30,7 +30,7 @@ constexpr int LH_XS = 4;    // activation octets per thread loaded before the we
 
 template <int TS, int NTT, int MT, bool EXACT>
 __global__ void __launch_bounds__(NTT)
-gemv_bf16_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+gemv_bf16_kernel(const uint16_t* __restrict__ w, const uint16_t* x, uint16_t* __restrict__ y,
                  int M, int N, int K) {
     constexpr int ROWS = NTT / TS;
     extern __shared__ __align__(16) u32x4 lx[];  // [M][K/8]
@@ -49,6 +49,7 @@ gemv_bf16_kernel(const uint16_t* __restrict__ w, const uint16_t* __restrict__ x,
     u32x4 xv[LH_XS];
 #pragma unroll
     for (int i = 0; i < LH_XS; ++i) xv[i] = bload16(xr, (tid + NTT * i) * 16);
+    issue_fence();
     const uint32_t rbytes = (uint32_t)K * 2;
     const auto wr = buf(w + (size_t)row0 * K, (uint32_t)nrows * rbytes);
     const int segw = TS * LH_CPL;

@@ -105,7 +105,7 @@ __host__ __device__ constexpr size_t mf_lds_bytes(bool xnat, int W, int T, int N
 template <int F, int T, int W, bool ONE, bool XNAT, bool PART>
 __global__ void __launch_bounds__(64 * W)
 qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws, int senc,
-                  const int8_t* __restrict__ xq, const float* __restrict__ xs,
+                  const int8_t* xq, const float* xs,
                   uint16_t* y, const uint16_t* res, int32_t* __restrict__ part,
                   int N, int K, int M, const uint8_t* __restrict__ w1,
                   const uint16_t* __restrict__ ws1, uint16_t* y1, int nb0) {

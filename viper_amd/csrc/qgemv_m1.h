@@ -8,12 +8,23 @@ namespace vq {
 
 // ------------------------------------------------------- M = 1, fused quantize
 //
-// The activation arrives as bf16 and is quantized in the prologue, or (PRE)
-// arrives already quantized (int8 in k order + fp32 group scales, the
-// layout of viper_hip_quantize_act) and is only rearranged into LDS.
+// Prologues (PRO): the activation row that every workgroup stages into LDS
+// arrives as
+//   PRO_BF16     bf16 x, quantized here;
+//   PRO_INT8     int8 xq (k order) + fp32 group scales xs (the layout of
+//                viper_hip_quantize_act), only rearranged;
+//   PRO_RMSNORM  bf16 x and gamma: v = bf16((x * rsqrt(sum x^2 / K + eps)) *
+//                gamma), then quantized (the reference's rmsnorm_quantize,
+//                kernels/ops/rmsnorm_quantize.cu:37-104, folded into the GEMV:
+//                every workgroup recomputes the row's sum of squares);
+//   PRO_SWIGLU   bf16 gate and up: v = bf16(g / (1 + exp(-g)) * u), then
+//                quantized (swiglu_quantize.cu:35-78 folded in).
+// The two folded prologues need the whole row in one load round
+// (K / 8 <= M1_XS * NTT octets).
 //
-// Two matrices of one shape may share a launch (the reference's fused2):
-// workgroups [0, nb0) work on (w, ws, y), the rest on (w1, ws1, y1).
+// Up to three matrices with the same K may share a launch (q/k/v, gate/up):
+// workgroups [0, e0) work on matrix 0, [e0, e1) on matrix 1, the rest on
+// matrix 2.  The residual and the partials belong to matrix 0.
 //
 // A team of TS lanes streams one output row: in each load instruction lane l
 // reads 16-byte chunk c = base + l of the row, so every instruction reads
@@ -28,9 +39,25 @@ constexpr int M1_CPL = 10;  // chunk slots per lane per row segment
 constexpr int M1_XS = 4;    // activation octets per thread loaded before the weights
 constexpr int M1_DELAY = 4; // weight-issue delay, s_sleep units
 
+// Matrices of one launch (passed by value in the kernel arguments).
+struct M1Mats {
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const uint8_t* w2;
+    const uint16_t* s0;
+    const uint16_t* s1;
+    const uint16_t* s2;
+    uint16_t* y0;
+    uint16_t* y1;
+    uint16_t* y2;
+    int n0, n1, n2;
+    int e0, e1;  // workgroup ends of matrices 0 and 1
+};
+
+// LDS: xq [K], per-chunk records, 16 floats of cross-wave sums
 template <int F>
 __host__ __device__ constexpr size_t m1_lds_bytes(int K) {
-    return (size_t)K + (size_t)(K / Fmt<F>::CK) * 8;
+    return (size_t)K + (size_t)(K / Fmt<F>::CK) * 8 + 64;
 }
 
 // EXACT: every lane's chunks of every slot lie inside its row (the row has
@@ -39,14 +66,16 @@ __host__ __device__ constexpr size_t m1_lds_bytes(int K) {
 // the weight loads.  The activation is a few KB read by every workgroup; a
 // short head start lets its requests through the memory pipeline before the
 // weight stream saturates it, which moves every workgroup's barrier earlier.
-template <int F, int TS, int NTT, int SENC, bool PART, bool EXACT, bool PRE, int DELAY>
+// xa: PRO_INT8 the group scales, PRO_RMSNORM gamma, PRO_SWIGLU up.
+// xout (PRO_RMSNORM, may be null): the bf16 normalized row, written by the
+// first workgroup.
+template <int F, int TS, int NTT, int SENC, bool PART, bool EXACT, int PRO, int DELAY>
 __global__ void __launch_bounds__(NTT)
-qgemv_m1_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws,
-                const void* __restrict__ x, const float* __restrict__ xsc, uint16_t* y,
-                const uint16_t* res, int32_t* __restrict__ part, int N, int K,
-                const uint8_t* __restrict__ w1, const uint16_t* __restrict__ ws1, uint16_t* y1,
-                int nb0) {
+qgemv_m1_kernel(const void* x, const void* xa, int K, float eps,
+                uint16_t* __restrict__ xout, const uint16_t* res, int32_t* __restrict__ part, M1Mats mats) {
     using FT = Fmt<F>;
+    constexpr bool PRE = PRO == PRO_INT8;
+    constexpr bool TWO = PRO == PRO_RMSNORM || PRO == PRO_SWIGLU;  // two bf16 inputs
     constexpr int CPL = M1_CPL;
     constexpr int XS = M1_XS;
     constexpr int ROWS = NTT / TS;
@@ -57,17 +86,19 @@ qgemv_m1_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws,
     const int NGR = K / FT::G;       // groups per row
     int8_t* lxq = (int8_t*)smem;
     u32x2* lcs = (u32x2*)(smem + K);
+    float* lred = (float*)(smem + K + (size_t)CPR * 8);
 
     const int tid = (int)threadIdx.x;
     const int l = tid % TS;
     const int rr = tid / TS;  // row within the workgroup
     int bid = (int)blockIdx.x;
-    if (bid >= nb0) {  // second matrix of a fused pair
-        bid -= nb0;
-        w = w1;
-        ws = ws1;
-        y = y1;
-    }
+    const int z = bid < mats.e0 ? 0 : bid < mats.e1 ? 1 : 2;
+    bid -= z == 0 ? 0 : z == 1 ? mats.e0 : mats.e1;
+    const uint8_t* w = z == 0 ? mats.w0 : z == 1 ? mats.w1 : mats.w2;
+    const uint16_t* ws = z == 0 ? mats.s0 : z == 1 ? mats.s1 : mats.s2;
+    uint16_t* y = z == 0 ? mats.y0 : z == 1 ? mats.y1 : mats.y2;
+    const int N = z == 0 ? mats.n0 : z == 1 ? mats.n1 : mats.n2;
+    if (z != 0) res = nullptr;
     const int row0 = bid * ROWS;
     const int row = row0 + rr;
     const int nrows = min(ROWS, N - row0);
@@ -78,7 +109,7 @@ qgemv_m1_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws,
     const int noct = K / 8;
     constexpr int OPG = FT::G / 8;   // octets per group
     const auto xr = buf(x, (uint32_t)K * (PRE ? 1 : 2));
-    const auto xsr = buf(xsc, PRE ? (uint32_t)(K / FT::G) * 4 : 0u);
+    const auto xsr = buf(xa, PRE ? (uint32_t)(K / FT::G) * 4 : TWO ? (uint32_t)K * 2 : 0u);
     // bf16 octet, or {int8 octet, int8 octet, group scale of a chunk's first octet}
     auto load_x = [&](int o) -> u32x4 {
         if constexpr (PRE) {
@@ -89,9 +120,14 @@ qgemv_m1_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws,
             return bload16(xr, o * 16);
         }
     };
-    u32x4 xv[XS];
+    u32x4 xv[XS], av[XS];
 #pragma unroll
     for (int i = 0; i < XS; ++i) xv[i] = load_x(tid + NTT * i);
+    if constexpr (TWO) {
+#pragma unroll
+        for (int i = 0; i < XS; ++i) av[i] = bload16(xsr, (tid + NTT * i) * 16);
+    }
+    issue_fence();
     const auto sr = buf(ws + (size_t)row0 * NGR, (uint32_t)(nrows * NGR) * 2);
     const bool lead = (l & 1) == 0;  // the even lane of a chunk pair owns the group
 
@@ -130,6 +166,50 @@ qgemv_m1_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws,
     //    octet as (ql nibbles, qh nibbles); Q5/Q6 as [k even | k odd] int8;
     //    W8 in k order.
     const int xiters = (noct + NTT - 1) / NTT;
+    // PRO_RMSNORM: the row's sum of squares (per-thread fma chain over its
+    // octets in order, DPP within the wave, wave sums in wave order)
+    float inv = 0.0f;
+    if constexpr (PRO == PRO_RMSNORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < XS; ++i) {
+            if (tid + NTT * i < noct) {
+                const u32x4 v = xv[i];
+                const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float f = bf16f((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                    ss = __builtin_fmaf(f, f, ss);
+                }
+            }
+        }
+        ss = team_sum<64>(ss);
+        if ((tid & 63) == 0) lred[tid >> 6] = ss;
+        lds_barrier();
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NTT / 64; ++i) t += lred[i];
+        inv = __builtin_amdgcn_rsqf(t / (float)K + eps);
+    }
+    // PRO_RMSNORM / PRO_SWIGLU: the bf16 row element-wise from two inputs
+    auto produce = [&](const u32x4& v, const u32x4& a) -> u32x4 {
+        const uint32_t vw[4] = {v.x, v.y, v.z, v.w}, aw[4] = {a.x, a.y, a.z, a.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float f0 = bf16f(vw[j] & 0xffffu), f1 = bf16f(vw[j] >> 16);
+            const float g0 = bf16f(aw[j] & 0xffffu), g1 = bf16f(aw[j] >> 16);
+            if constexpr (PRO == PRO_RMSNORM) {
+                f0 = (f0 * inv) * g0;
+                f1 = (f1 * inv) * g1;
+            } else {
+                f0 = f0 / (1.0f + __expf(-f0)) * g0;
+                f1 = f1 / (1.0f + __expf(-f1)) * g1;
+            }
+            o[j] = (uint32_t)f2bf(f0) | ((uint32_t)f2bf(f1) << 16);
+        }
+        return u32x4{o[0], o[1], o[2], o[3]};
+    };
     auto quant_store = [&](int o, const u32x4& v) {
         uint32_t d0, d1;
         float s;
@@ -160,10 +240,23 @@ qgemv_m1_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws,
     };
     const int wave0 = tid & ~63;  // waves with no octet skip the quantize
 #pragma unroll
-    for (int i = 0; i < XS; ++i)
-        if (i < xiters && wave0 + NTT * i < noct) quant_store(tid + NTT * i, xv[i]);
-    for (int i = XS; i < xiters; ++i)
-        if (wave0 + NTT * i < noct) quant_store(tid + NTT * i, load_x(tid + NTT * i));
+    for (int i = 0; i < XS; ++i) {
+        if (i < xiters && wave0 + NTT * i < noct) {
+            if constexpr (TWO) {
+                const int o = tid + NTT * i;
+                const u32x4 v = produce(xv[i], av[i]);
+                if (PRO == PRO_RMSNORM && xout != nullptr && blockIdx.x == 0 && o < noct)
+                    *(u32x4*)(xout + (size_t)o * 8) = v;
+                quant_store(o, v);
+            } else {
+                quant_store(tid + NTT * i, xv[i]);
+            }
+        }
+    }
+    if constexpr (!TWO) {
+        for (int i = XS; i < xiters; ++i)
+            if (wave0 + NTT * i < noct) quant_store(tid + NTT * i, load_x(tid + NTT * i));
+    }
 
     lds_barrier();
 
@@ -197,44 +290,48 @@ qgemv_m1_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws,
     }
 }
 
-typedef void (*m1_fn)(const uint8_t*, const uint16_t*, const void*, const float*, uint16_t*,
-                      const uint16_t*, int32_t*, int, int, const uint8_t*, const uint16_t*, uint16_t*,
-                      int);
+typedef void (*m1_fn)(const void*, const void*, int, float, uint16_t*, const uint16_t*, int32_t*, M1Mats);
 
 // Launch shapes instantiated for every format: (team size, workgroup size).
 constexpr int M1_SHAPES[][2] = {{8, 320}, {16, 256}, {16, 640}, {32, 320}, {32, 640}, {64, 640}};
 
-template <int F, int SENC, bool PART, bool EXACT, bool PRE>
+template <int F, int SENC, bool PART, bool EXACT, int PRO>
 m1_fn m1_kernel_v(int ts, int ntt) {
 #define VQ_M1(TS_, NTT_) \
-    if (ts == TS_ && ntt == NTT_) return qgemv_m1_kernel<F, TS_, NTT_, SENC, PART, EXACT, PRE, M1_DELAY>;
+    if (ts == TS_ && ntt == NTT_) return qgemv_m1_kernel<F, TS_, NTT_, SENC, PART, EXACT, PRO, M1_DELAY>;
     VQ_M1(8, 320) VQ_M1(16, 256) VQ_M1(16, 640) VQ_M1(32, 320) VQ_M1(32, 640) VQ_M1(64, 640)
 #undef VQ_M1
     return nullptr;
 }
 
-// Kernel for format F (defined in that format's translation unit).
-template <int F>
-m1_fn m1_pick(int ts, int ntt, int senc, bool part, bool exact, bool pre);
+template <int F, int PRO>
+m1_fn m1_pick_pro(int ts, int ntt, int senc, bool part, bool exact) {
+    if (exact) {
+        if (senc) return part ? m1_kernel_v<F, 1, true, true, PRO>(ts, ntt) : m1_kernel_v<F, 1, false, true, PRO>(ts, ntt);
+        return part ? m1_kernel_v<F, 0, true, true, PRO>(ts, ntt) : m1_kernel_v<F, 0, false, true, PRO>(ts, ntt);
+    }
+    if (senc) return part ? m1_kernel_v<F, 1, true, false, PRO>(ts, ntt) : m1_kernel_v<F, 1, false, false, PRO>(ts, ntt);
+    return part ? m1_kernel_v<F, 0, true, false, PRO>(ts, ntt) : m1_kernel_v<F, 0, false, false, PRO>(ts, ntt);
+}
 
-#define VQ_M1_PICK(F)                                                                              \
-    template <bool PRE>                                                                            \
-    static m1_fn m1_pick_e(int ts, int ntt, int senc, bool part, bool exact) {                     \
-        if (exact) {                                                                               \
-            if (senc) return part ? m1_kernel_v<F, 1, true, true, PRE>(ts, ntt)                    \
-                                  : m1_kernel_v<F, 1, false, true, PRE>(ts, ntt);                  \
-            return part ? m1_kernel_v<F, 0, true, true, PRE>(ts, ntt)                              \
-                        : m1_kernel_v<F, 0, false, true, PRE>(ts, ntt);                            \
-        }                                                                                          \
-        if (senc) return part ? m1_kernel_v<F, 1, true, false, PRE>(ts, ntt)                       \
-                              : m1_kernel_v<F, 1, false, false, PRE>(ts, ntt);                     \
-        return part ? m1_kernel_v<F, 0, true, false, PRE>(ts, ntt)                                 \
-                    : m1_kernel_v<F, 0, false, false, PRE>(ts, ntt);                               \
-    }                                                                                              \
-    template <>                                                                                    \
-    m1_fn m1_pick<F>(int ts, int ntt, int senc, bool part, bool exact, bool pre) {                 \
-        return pre ? m1_pick_e<true>(ts, ntt, senc, part, exact)                                   \
-                   : m1_pick_e<false>(ts, ntt, senc, part, exact);                                 \
+// Kernels of format F with the quantize / int8 prologues and with the folded
+// rmsnorm / swiglu prologues (each defined in its own translation unit).
+template <int F>
+m1_fn m1_pick_plain(int ts, int ntt, int senc, bool part, bool exact, int pro);
+template <int F>
+m1_fn m1_pick_folded(int ts, int ntt, int senc, bool part, bool exact, int pro);
+
+#define VQ_M1_PLAIN(F)                                                                         \
+    template <>                                                                                \
+    m1_fn m1_pick_plain<F>(int ts, int ntt, int senc, bool part, bool exact, int pro) {        \
+        return pro == PRO_INT8 ? m1_pick_pro<F, PRO_INT8>(ts, ntt, senc, part, exact)          \
+                               : m1_pick_pro<F, PRO_BF16>(ts, ntt, senc, part, exact);         \
+    }
+#define VQ_M1_FOLDED(F)                                                                        \
+    template <>                                                                                \
+    m1_fn m1_pick_folded<F>(int ts, int ntt, int senc, bool part, bool exact, int pro) {       \
+        return pro == PRO_SWIGLU ? m1_pick_pro<F, PRO_SWIGLU>(ts, ntt, senc, part, exact)      \
+                                 : m1_pick_pro<F, PRO_RMSNORM>(ts, ntt, senc, part, exact);    \
     }
 
 }  // namespace vq

@@ -1,8 +1,8 @@
-// M = 1 GEMV kernels of format 6 (the template is in qgemv_m1.h).
+// M = 1 GEMV kernels of format 6, quantize and int8 prologues (the template is in qgemv_m1.h).
 #include "qgemv_m1.h"
 
 namespace vq {
 
-VQ_M1_PICK(6)
+VQ_M1_PLAIN(6)
 
 }  // namespace vq

@@ -1,0 +1,8 @@
+// M = 1 GEMV kernels of format 6, rmsnorm and swiglu prologues (the template is in qgemv_m1.h).
+#include "qgemv_m1.h"
+
+namespace vq {
+
+VQ_M1_FOLDED(6)
+
+}  // namespace vq

@@ -1,8 +1,8 @@
-// M = 1 GEMV kernels of format 8 (the template is in qgemv_m1.h).
+// M = 1 GEMV kernels of format 8, quantize and int8 prologues (the template is in qgemv_m1.h).
 #include "qgemv_m1.h"
 
 namespace vq {
 
-VQ_M1_PICK(8)
+VQ_M1_PLAIN(8)
 
 }  // namespace vq

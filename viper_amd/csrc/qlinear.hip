@@ -158,8 +158,11 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     rc = validate_second(b, qtype, senc, group, N, K, M, res, part);
     if (rc != VIPER_OK) return rc;
     hipStream_t st = (hipStream_t)stream;
-    if (fused_ok(qtype, M, K))
-        return launch_m1(qtype, w, s, senc, N, K, x, nullptr, y, res, part, b.w, b.s, b.y, st, ev0, ev1);
+    if (fused_ok(qtype, M, K)) {
+        const M1Out outs[2] = {{w, s, y, N}, {b.w, b.s, b.y, N}};
+        return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, b.w ? 2 : 1, res, part, st,
+                         ev0, ev1);
+    }
     const size_t need = workspace_need(qtype, K, M);
     if (wsp == nullptr || wsp_bytes < need || misaligned(wsp, 16)) return VIPER_INVALID_ARGUMENT;
     const bool mf = mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s));
@@ -189,9 +192,11 @@ static int prequant_common(int qtype, const void* w, const void* s, int senc, in
     rc = validate_second(b, qtype, senc, group, N, K, M, res, nullptr);
     if (rc != VIPER_OK) return rc;
     hipStream_t st = (hipStream_t)stream;
-    if (fused_ok(qtype, M, K))
-        return launch_m1(qtype, w, s, senc, N, K, xq, (const float*)xs, y, res, nullptr, b.w, b.s, b.y,
-                         st, nullptr, nullptr);
+    if (fused_ok(qtype, M, K)) {
+        const M1Out outs[2] = {{w, s, y, N}, {b.w, b.s, b.y, N}};
+        return launch_m1(qtype, senc, K, PRO_INT8, xq, xs, 0.0f, nullptr, outs, b.w ? 2 : 1, res, nullptr, st,
+                         nullptr, nullptr);
+    }
     if (mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s)))
         return launch_mfma(qtype, w, s, senc, N, K, xq, xs, true, M, y, res, nullptr, b.w, b.s, b.y, st,
                            nullptr, nullptr);
@@ -283,6 +288,34 @@ extern "C" int viper_hip_qlinear_fused2_prequantized(int qtype, const void* w0_p
     if (w1_packed == nullptr || w1_scales == nullptr || y1_bf16 == nullptr) return VIPER_INVALID_ARGUMENT;
     return vq::prequant_common(qtype, w0_packed, w0_scales, scale_enc, group, N, K, xq, xs, M, y0_bf16,
                                nullptr, stream, vq::Second{w1_packed, w1_scales, y1_bf16});
+}
+
+extern "C" int viper_hip_qlinear_m1(int qtype, int scale_enc, int group, int K, int prologue, const void* a,
+                                    const void* b, float eps, void* norm_out, int n_out,
+                                    const void* const* w_packed, const void* const* w_scales, const int* N,
+                                    void* const* y_bf16, const void* residual_bf16, void* stream) {
+    if (n_out < 1 || n_out > 3 || w_packed == nullptr || w_scales == nullptr || N == nullptr || y_bf16 == nullptr)
+        return VIPER_INVALID_ARGUMENT;
+    if (prologue < VIPER_PROLOGUE_BF16 || prologue > VIPER_PROLOGUE_SWIGLU) return VIPER_INVALID_ARGUMENT;
+    vq::M1Out outs[3];
+    for (int i = 0; i < n_out; ++i) {
+        const int rc = vq::validate_weights(qtype, w_packed[i], w_scales[i], scale_enc, group, N[i], K, 1);
+        if (rc != VIPER_OK) return rc;
+        if (y_bf16[i] == nullptr || vq::misaligned(y_bf16[i], 2)) return VIPER_INVALID_ARGUMENT;
+        outs[i] = vq::M1Out{w_packed[i], w_scales[i], y_bf16[i], N[i]};
+    }
+    if (a == nullptr || (prologue != VIPER_PROLOGUE_BF16 && b == nullptr)) return VIPER_INVALID_ARGUMENT;
+    const size_t align_a = prologue == VIPER_PROLOGUE_INT8 ? 8 : 16;
+    const size_t align_b = prologue == VIPER_PROLOGUE_INT8 ? 4 : 16;
+    if (vq::misaligned(a, align_a) || vq::misaligned(b, align_b) || vq::misaligned(norm_out, 16) ||
+        vq::misaligned(residual_bf16, 2))
+        return VIPER_INVALID_ARGUMENT;
+    if (norm_out != nullptr && prologue != VIPER_PROLOGUE_RMSNORM) return VIPER_INVALID_ARGUMENT;
+    if (vq::lds_m1(qtype, K) > (size_t)vq::LDS_MAX) return VIPER_INVALID_ARGUMENT;
+    if ((prologue == VIPER_PROLOGUE_RMSNORM || prologue == VIPER_PROLOGUE_SWIGLU) && !vq::m1_folded_ok(qtype, K, N[0]))
+        return VIPER_INVALID_ARGUMENT;
+    return vq::launch_m1(qtype, scale_enc, K, prologue, a, b, eps, norm_out, outs, n_out, residual_bf16, nullptr,
+                         (hipStream_t)stream, nullptr, nullptr);
 }
 
 extern "C" int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream) {

@@ -266,6 +266,15 @@ template <int AUX = 0>
 __device__ __forceinline__ uint32_t bload4(__amdgpu_buffer_rsrc_t r, int off) {
     return (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, AUX);
 }
+// Compiler-only fence for memory operations: loads issued before it stay
+// before it, so the weight stream cannot be hoisted above the activation
+// loads.  (Activation pointers are also kept free of __restrict__: a load
+// through a restrict-qualified read-only pointer counts as invariant, and
+// the register allocator then re-issues it at its first use, after the
+// weight loads, where the wait for it waits for the whole weight stream -
+// loads retire in issue order.)
+__device__ __forceinline__ void issue_fence() { asm volatile("" ::: "memory"); }
+
 __device__ __forceinline__ uint32_t bload2(__amdgpu_buffer_rsrc_t r, int off) {
     return (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }

@@ -72,13 +72,22 @@ inline int device_cus() {
 
 // ---- launchers (one translation unit each)
 
-// M = 1 (qgemv_m1.hip): x bf16 with the quantize fused (xs == nullptr), or
-// x int8 + xs fp32 already quantized; w1/s1/y1 non-null: a second matrix of
-// the same shape in the same launch.
+// M = 1 (qgemv_m1.hip): one to three matrices of the same K (any N each)
+// on one activation row produced by the prologue `pro` (PRO_BF16: x bf16,
+// PRO_INT8: x int8 + xa scales, PRO_RMSNORM: x, xa = gamma, eps, xout,
+// PRO_SWIGLU: x = gate, xa = up).  res and part belong to matrix 0.
+enum { PRO_BF16 = 0, PRO_INT8 = 1, PRO_RMSNORM = 2, PRO_SWIGLU = 3 };
+struct M1Out {
+    const void* w;
+    const void* s;
+    void* y;
+    int n;
+};
 size_t lds_m1(int qtype, int K);
-int launch_m1(int qtype, const void* w, const void* s, int senc, int N, int K, const void* x,
-              const float* xs, void* y, const void* res, int32_t* part, const void* w1,
-              const void* s1, void* y1, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
+bool m1_folded_ok(int qtype, int K, int N);
+int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
+              const M1Out* outs, int nouts, const void* res, int32_t* part, hipStream_t st,
+              hipEvent_t ev0, hipEvent_t ev1);
 
 // M <= 16 over prequantized activations, v_dot4 (qgemm_pre.hip).
 int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,

@@ -127,6 +127,7 @@ _SYMBOLS = (
     "viper_hip_swiglu_quantize",
     "viper_hip_linear_bf16",
     "viper_hip_sampling_greedy",
+    "viper_hip_qlinear_m1",
 )
 
 
@@ -170,6 +171,8 @@ def lib():
     L.viper_hip_linear_bf16.restype = i32
     L.viper_hip_sampling_greedy.argtypes = [vp, vp, i32, i32, vp]
     L.viper_hip_sampling_greedy.restype = i32
+    L.viper_hip_qlinear_m1.argtypes = [i32, i32, i32, i32, i32, vp, vp, C.c_float, vp, i32, vp, vp, vp, vp, vp, vp]
+    L.viper_hip_qlinear_m1.restype = i32
     _lib = L
     return L
 
@@ -308,6 +311,33 @@ def swiglu_quantize(gate, up, group, xq, xs, out=None, stream=None) -> Status:
     rc = lib().viper_hip_swiglu_quantize(ptr(gate), ptr(up), M, I, group, ptr(out), ptr(xq), ptr(xs),
                                          _stream(stream))
     return _status(rc, "viper_hip_swiglu_quantize")
+
+
+class Prologue(enum.IntEnum):
+    BF16 = 0
+    INT8 = 1
+    RMSNORM = 2
+    SWIGLU = 3
+
+
+def linear_m1(ws, prologue, a, b, ys, eps=0.0, norm_out=None, residual=None, stream=None) -> Status:
+    """One launch at M = 1: ys[i] = linear(ws[i], v) for 1..3 weights of one kind and K,
+    v produced by the prologue from a (and b): bf16 x; int8 xq + fp32 xs;
+    rmsnorm(x) * gamma; silu(gate) * up.  residual is added to ys[0]."""
+    n = len(ws)
+    if n < 1 or n > 3 or len(ys) != n:
+        return Status(StatusCode.INVALID_ARGUMENT, "linear_m1: 1 to 3 weights, one output each")
+    w0 = ws[0]
+    if any((w.qtype, w.cols, w.group_size, w.scale_enc) != (w0.qtype, w0.cols, w0.group_size, w0.scale_enc)
+           for w in ws):
+        return Status(StatusCode.SHAPE_MISMATCH, "linear_m1: weights differ in kind or K")
+    arr = lambda vals: (C.c_void_p * n)(*vals)
+    rc = lib().viper_hip_qlinear_m1(int(w0.qtype), int(w0.scale_enc), w0.group_size, w0.cols, int(prologue),
+                                    ptr(a), ptr(b), float(eps), ptr(norm_out), n,
+                                    arr([ptr(w.data) for w in ws]), arr([ptr(w.scales) for w in ws]),
+                                    (C.c_int * n)(*[w.rows for w in ws]), arr([ptr(y) for y in ys]),
+                                    ptr(residual), _stream(stream))
+    return _status(rc, "viper_hip_qlinear_m1")
 
 
 def linear_bf16(w, x, y, stream=None) -> Status:
