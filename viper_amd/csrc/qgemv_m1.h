@@ -293,13 +293,14 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, float eps,
 typedef void (*m1_fn)(const void*, const void*, int, float, uint16_t*, const uint16_t*, int32_t*, M1Mats);
 
 // Launch shapes instantiated for every format: (team size, workgroup size).
-constexpr int M1_SHAPES[][2] = {{8, 320}, {16, 256}, {16, 640}, {32, 320}, {32, 640}, {64, 640}};
+constexpr int M1_SHAPES[][2] = {{8, 128}, {8, 192}, {8, 320}, {16, 256}, {16, 640}, {32, 320}, {32, 640}, {64, 640}};
 
 template <int F, int SENC, bool PART, bool EXACT, int PRO>
 m1_fn m1_kernel_v(int ts, int ntt) {
 #define VQ_M1(TS_, NTT_) \
     if (ts == TS_ && ntt == NTT_) return qgemv_m1_kernel<F, TS_, NTT_, SENC, PART, EXACT, PRO, M1_DELAY>;
-    VQ_M1(8, 320) VQ_M1(16, 256) VQ_M1(16, 640) VQ_M1(32, 320) VQ_M1(32, 640) VQ_M1(64, 640)
+    VQ_M1(8, 128) VQ_M1(8, 192) VQ_M1(8, 320) VQ_M1(16, 256) VQ_M1(16, 640) VQ_M1(32, 320) VQ_M1(32, 640)
+    VQ_M1(64, 640)
 #undef VQ_M1
     return nullptr;
 }

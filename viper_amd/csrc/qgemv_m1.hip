@@ -35,7 +35,7 @@ static m1_fn m1_kernel(int qtype, int ts, int ntt, int senc, bool part, bool exa
 static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt) {
     int ts = 8;
     while (ts < 64 && ts * M1_CPL < cpr) ts *= 2;
-    static const int cand[] = {256, 320, 640};
+    static const int cand[] = {128, 192, 256, 320, 640};
     M1Shape best{ts, 0};
     long best_load = -1;
     for (int ntt : cand) {
