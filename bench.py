@@ -285,7 +285,20 @@ def main():
         extras["config3_step_us"] = round(s3_ms * 1e3, 1)
         extras["config3_step_gbs"] = round(s3_bytes / (s3_ms * 1e-3) / 1e9, 1)
         extras["config3_launches_per_step"] = 9 * stk.layers * stk.passes + 3
-        del g3, stk
+        del g3
+        # the same step with the producers folded into the GEMVs (4 launches per slot)
+        stk.step_fused()
+        torch.cuda.synchronize()
+        g4 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g4):
+            stk.step_fused()
+        g4.replay()
+        torch.cuda.synchronize()
+        s4_ms = time_graph(torch, g4, 10) / 10
+        extras["config3_fused_step_us"] = round(s4_ms * 1e3, 1)
+        extras["config3_fused_step_gbs"] = round(s3_bytes / (s4_ms * 1e-3) / 1e9, 1)
+        extras["config3_fused_launches_per_step"] = 4 * stk.layers * stk.passes + 3
+        del g4, stk
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_q4_m1_k2560_n10240.json")

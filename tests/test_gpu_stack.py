@@ -26,16 +26,18 @@ def u16(t):
     return t.contiguous().view(__import__("torch").int16).cpu().numpy().view(np.uint16)
 
 
-def test_stack_step_wiring_and_determinism(torch_dev):
+@pytest.mark.parametrize("fused", [False, True])
+def test_stack_step_wiring_and_determinism(torch_dev, fused):
     torch = torch_dev
     from viper_amd.stack import Stack
     s = Stack(torch, hidden=256, inter=512, n_heads=2, n_kv_heads=1, head_dim=128, layers=2, passes=2,
               vocab=1000, seed=7)
-    s.step()
+    run = s.step_fused if fused else s.step
+    run()
     torch.cuda.synchronize()
     logits = u16(s.logits)
     token = int(s.token.item())
-    s.step()
+    run()
     torch.cuda.synchronize()
     np.testing.assert_array_equal(u16(s.logits), logits)
 

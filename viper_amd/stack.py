@@ -12,9 +12,17 @@ on this path; its output is a fixed activation):
     rmsnorm_quantize(x, post_ln)   -> fused2(gate, up)
     swiglu_quantize(gate, up)      -> down GEMV + residual (in place on x)
 
+step_fused() is the same computation in 4 launches per slot instead of 9:
+the producers are folded into the GEMV prologues and q/k/v share a launch
+(viper_hip_qlinear_m1):
+
+    [rmsnorm(x, input_ln) -> q, k, v]   [quantize(attn) -> o + residual]
+    [rmsnorm(x, post_ln) -> gate, up]   [swiglu(gate, up) -> down + residual]
+
 Device buffers are torch tensors (allocation only); every launch is a C ABI
 call on the current stream, so a whole step can be captured in a HIP graph.
 """
+import ctypes as C
 import math
 
 from . import qlinear as _q
@@ -71,6 +79,36 @@ class Stack:
     def _ok(self, rc, what):
         if rc != 0:
             raise RuntimeError(f"{what} failed: {rc}")
+
+    def _m1(self, pro, a, b, outs, eps=0.0, residual=None, st=None):
+        n = len(outs)
+        vp = C.c_void_p * n
+        rc = self.L.viper_hip_qlinear_m1(Q4, 0, 64, outs[0][0][3], pro, a, b, eps, None, n,
+                                         vp(*[o[0][0].data_ptr() for o in outs]),
+                                         vp(*[o[0][1].data_ptr() for o in outs]),
+                                         (C.c_int * n)(*[o[0][2] for o in outs]),
+                                         vp(*[o[1].data_ptr() for o in outs]), residual, st)
+        self._ok(rc, "qlinear_m1")
+
+    def step_fused(self):
+        """One decode step, 4 launches per slot (producers folded, q/k/v together)."""
+        torch, L = self.torch, self.L
+        st = torch.cuda.current_stream().cuda_stream
+        H, I = self.H, self.I
+        p = lambda t: t.data_ptr()
+        x = self.x
+        x.copy_(self.x0)
+        for loop in range(self.passes):
+            for l in range(self.layers):
+                wq, wk, wv, wo, wg, wu, wd = self.w[l]
+                self._m1(2, p(x), p(self.ln[2 * l]), [(wq, self.q), (wk, self.k), (wv, self.v)], eps=self.eps, st=st)
+                self._m1(0, p(self.attn), None, [(wo, x)], residual=p(x), st=st)
+                self._m1(2, p(x), p(self.ln[2 * l + 1]), [(wg, self.gt), (wu, self.ut)], eps=self.eps, st=st)
+                self._m1(3, p(self.gt), p(self.ut), [(wd, x)], residual=p(x), st=st)
+        self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(self.final_ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
+                                              p(self.xs), st), "final norm")
+        self._ok(L.viper_hip_linear_bf16(p(self.head), p(self.xn), p(self.logits), 1, self.V, H, st), "lm_head")
+        self._ok(L.viper_hip_sampling_greedy(p(self.logits), p(self.token), 1, self.V, st), "greedy")
 
     def step(self):
         """One decode step of the linear path, reference launch sequence."""
