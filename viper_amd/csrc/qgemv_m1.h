@@ -39,20 +39,6 @@ constexpr int M1_CPL = 10;  // chunk slots per lane per row segment
 constexpr int M1_XS = 4;    // activation octets per thread loaded before the weights
 constexpr int M1_DELAY = 4; // weight-issue delay, s_sleep units
 
-// Matrices of one launch (passed by value in the kernel arguments).
-struct M1Mats {
-    const uint8_t* w0;
-    const uint8_t* w1;
-    const uint8_t* w2;
-    const uint16_t* s0;
-    const uint16_t* s1;
-    const uint16_t* s2;
-    uint16_t* y0;
-    uint16_t* y1;
-    uint16_t* y2;
-    int n0, n1, n2;
-    int e0, e1;  // workgroup ends of matrices 0 and 1
-};
 
 // LDS: xq [K], per-chunk records, 16 floats of cross-wave sums
 template <int F>
@@ -71,8 +57,10 @@ __host__ __device__ constexpr size_t m1_lds_bytes(int K) {
 // first workgroup.
 template <int F, int TS, int NTT, int SENC, bool PART, bool EXACT, int PRO, int DELAY>
 __global__ void __launch_bounds__(NTT)
-qgemv_m1_kernel(const void* x, const void* xa, int K, float eps,
-                uint16_t* __restrict__ xout, const uint16_t* res, int32_t* __restrict__ part, M1Mats mats) {
+qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint8_t* w0, const uint16_t* s0,
+                uint16_t* y0, int n0, float eps, uint16_t* __restrict__ xout, const uint16_t* res,
+                int32_t* __restrict__ part, const uint8_t* w1, const uint16_t* s1, uint16_t* y1, int n1,
+                const uint8_t* w2, const uint16_t* s2, uint16_t* y2, int n2) {
     using FT = Fmt<F>;
     constexpr bool PRE = PRO == PRO_INT8;
     constexpr bool TWO = PRO == PRO_RMSNORM || PRO == PRO_SWIGLU;  // two bf16 inputs
@@ -91,14 +79,29 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, float eps,
     const int tid = (int)threadIdx.x;
     const int l = tid % TS;
     const int rr = tid / TS;  // row within the workgroup
+    // matrix of this workgroup (matrix 0's arguments lead the argument list,
+    // so its workgroups need nothing beyond the preloaded arguments)
     int bid = (int)blockIdx.x;
-    const int z = bid < mats.e0 ? 0 : bid < mats.e1 ? 1 : 2;
-    bid -= z == 0 ? 0 : z == 1 ? mats.e0 : mats.e1;
-    const uint8_t* w = z == 0 ? mats.w0 : z == 1 ? mats.w1 : mats.w2;
-    const uint16_t* ws = z == 0 ? mats.s0 : z == 1 ? mats.s1 : mats.s2;
-    uint16_t* y = z == 0 ? mats.y0 : z == 1 ? mats.y1 : mats.y2;
-    const int N = z == 0 ? mats.n0 : z == 1 ? mats.n1 : mats.n2;
-    if (z != 0) res = nullptr;
+    const uint8_t* w = w0;
+    const uint16_t* ws = s0;
+    uint16_t* y = y0;
+    int N = n0;
+    if (bid >= e0) {
+        res = nullptr;
+        if (bid >= e1) {
+            bid -= e1;
+            w = w2;
+            ws = s2;
+            y = y2;
+            N = n2;
+        } else {
+            bid -= e0;
+            w = w1;
+            ws = s1;
+            y = y1;
+            N = n1;
+        }
+    }
     const int row0 = bid * ROWS;
     const int row = row0 + rr;
     const int nrows = min(ROWS, N - row0);
@@ -290,7 +293,9 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, float eps,
     }
 }
 
-typedef void (*m1_fn)(const void*, const void*, int, float, uint16_t*, const uint16_t*, int32_t*, M1Mats);
+typedef void (*m1_fn)(const void*, const void*, int, int, int, const uint8_t*, const uint16_t*, uint16_t*, int,
+                      float, uint16_t*, const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*,
+                      int, const uint8_t*, const uint16_t*, uint16_t*, int);
 
 // Launch shapes instantiated for every format: (team size, workgroup size).
 constexpr int M1_SHAPES[][2] = {{8, 128}, {8, 192}, {8, 320}, {16, 256}, {16, 640}, {32, 320}, {32, 640}, {64, 640}};

@@ -85,27 +85,18 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     const int rows = sh.ntt / sh.ts;
     const size_t lds = lds_m1(qtype, K);
     if (lds > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
-    M1Mats m{};
     int nb[3] = {0, 0, 0};
     for (int i = 0; i < nouts; ++i) nb[i] = (outs[i].n + rows - 1) / rows;
     const M1Out o0 = outs[0], o1 = nouts > 1 ? outs[1] : outs[0], o2 = nouts > 2 ? outs[2] : outs[0];
-    m.w0 = (const uint8_t*)o0.w;
-    m.w1 = (const uint8_t*)o1.w;
-    m.w2 = (const uint8_t*)o2.w;
-    m.s0 = (const uint16_t*)o0.s;
-    m.s1 = (const uint16_t*)o1.s;
-    m.s2 = (const uint16_t*)o2.s;
-    m.y0 = (uint16_t*)o0.y;
-    m.y1 = (uint16_t*)o1.y;
-    m.y2 = (uint16_t*)o2.y;
-    m.n0 = o0.n;
-    m.n1 = o1.n;
-    m.n2 = o2.n;
-    m.e0 = nb[0];
-    m.e1 = nb[0] + nb[1];
+    const uint8_t *w0 = (const uint8_t*)o0.w, *w1 = (const uint8_t*)o1.w, *w2 = (const uint8_t*)o2.w;
+    const uint16_t *s0 = (const uint16_t*)o0.s, *s1 = (const uint16_t*)o1.s, *s2 = (const uint16_t*)o2.s;
+    uint16_t *y0 = (uint16_t*)o0.y, *y1 = (uint16_t*)o1.y, *y2 = (uint16_t*)o2.y;
+    int n0 = o0.n, n1 = o1.n, n2 = o2.n;
+    int e0 = nb[0], e1 = nb[0] + nb[1];
     const unsigned grid = (unsigned)(nb[0] + nb[1] + nb[2]);
     const uint16_t* r = (const uint16_t*)res;
-    void* args[] = {&x, &xa, &K, &eps, &xout, &r, &part, &m};
+    void* args[] = {&x, &xa, &K, &e0, &e1, &w0, &s0, &y0, &n0, &eps, &xout, &r, &part,
+                    &w1, &s1, &y1, &n1, &w2, &s2, &y2, &n2};
     launch((const void*)fn, grid, (unsigned)sh.ntt, lds, st, args, ev0, ev1);
     return status_of(hipGetLastError());
 }
