@@ -104,11 +104,10 @@ __host__ __device__ constexpr size_t mf_lds_bytes(bool xnat, int W, int T, int N
 // PART: also store every int32 group dot (test and debug entry point).
 template <int F, int T, int W, bool ONE, bool XNAT, bool PART>
 __global__ void __launch_bounds__(64 * W)
-qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws, int senc,
-                  const int8_t* xq, const float* xs,
-                  uint16_t* y, const uint16_t* res, int32_t* __restrict__ part,
-                  int N, int K, int M, const uint8_t* __restrict__ w1,
-                  const uint16_t* __restrict__ ws1, uint16_t* y1, int nb0) {
+qgemm_mfma_kernel(const int8_t* xq, const float* xs, int K, int M, int N, int nb0, int senc,
+                  const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws, uint16_t* y,
+                  const uint16_t* res, int32_t* __restrict__ part, const uint8_t* __restrict__ w1,
+                  const uint16_t* __restrict__ ws1, uint16_t* y1) {
     using FT = Fmt<F>;
     constexpr int PS = ONE ? MF_PS_ONE : MF_PS_LOOP;
     constexpr bool NIB = F != 8;
@@ -335,9 +334,8 @@ qgemm_mfma_kernel(const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws
 
 // ------------------------------------------------------------------ host side
 
-typedef void (*mf_fn)(const uint8_t*, const uint16_t*, int, const int8_t*, const float*, uint16_t*,
-                      const uint16_t*, int32_t*, int, int, int, const uint8_t*, const uint16_t*,
-                      uint16_t*, int);
+typedef void (*mf_fn)(const int8_t*, const float*, int, int, int, int, int, const uint8_t*, const uint16_t*,
+                      uint16_t*, const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*);
 
 struct MfShape {
     int t, w;
@@ -421,7 +419,7 @@ int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K,
     const uint8_t* b0 = (const uint8_t*)w1;
     const uint16_t* b1 = (const uint16_t*)s1;
     uint16_t* b2 = (uint16_t*)y1;
-    void* args[] = {&a0, &a1, &senc, &a3, &a4, &a5, &a6, &part, &N, &K, &M, &b0, &b1, &b2, &nb0};
+    void* args[] = {&a3, &a4, &K, &M, &N, &nb0, &senc, &a0, &a1, &a5, &a6, &part, &b0, &b1, &b2};
     launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args, ev0, ev1);
     return status_of(hipGetLastError());
 }

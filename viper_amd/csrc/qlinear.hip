@@ -44,7 +44,7 @@ namespace vq {
 // and xs [M][K/G].
 template <int G, bool MF>
 __global__ void __launch_bounds__(NT)
-quantize_act_kernel(const uint16_t* __restrict__ x, int8_t* __restrict__ xq,
+quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
                     float* __restrict__ xs, int oct_total, int K) {
     const int o = (int)blockIdx.x * NT + (int)threadIdx.x;
     const bool ok = o < oct_total;
