@@ -115,9 +115,10 @@ __device__ __forceinline__ void better(float& v, int& i, float ov, int oi) {
 }
 
 constexpr int AM_NT = 1024;
+constexpr int AM_BATCH = 8;
 
 __global__ void __launch_bounds__(AM_NT)
-argmax_bf16_kernel(const uint16_t* __restrict__ logits, int32_t* __restrict__ out, int V) {
+argmax_bf16_kernel(const uint16_t* logits, int32_t* __restrict__ out, int V) {
     __shared__ float sv[AM_NT / 64];
     __shared__ int si[AM_NT / 64];
     const int b = (int)blockIdx.x;
@@ -128,15 +129,26 @@ argmax_bf16_kernel(const uint16_t* __restrict__ logits, int32_t* __restrict__ ou
     // octets first (16-byte loads when the row is 16-byte aligned), then the tail
     const bool vec = ((((uintptr_t)row) & 15) == 0);
     const int noct = vec ? V / 8 : 0;
-    for (int o = tid; o < noct; o += AM_NT) {
-        const u32x4 q = *(const u32x4*)(row + (size_t)o * 8);
-        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+    // AM_BATCH octets per lane in flight at once (buffer loads: past the row
+    // they read zero and are skipped by the index bound)
+    const auto rr = buf(row, (uint32_t)noct * 16);
+    for (int o0 = tid; o0 < noct; o0 += AM_NT * AM_BATCH) {
+        u32x4 q[AM_BATCH];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const float f = bf16f((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-            if (f > best) {
-                best = f;
-                idx = o * 8 + j;
+        for (int b = 0; b < AM_BATCH; ++b) q[b] = bload16(rr, (o0 + b * AM_NT) * 16);
+#pragma unroll
+        for (int b = 0; b < AM_BATCH; ++b) {
+            const int o = o0 + b * AM_NT;
+            if (o < noct) {
+                const uint32_t wd[4] = {q[b].x, q[b].y, q[b].z, q[b].w};
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float f = bf16f((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
+                    if (f > best) {
+                        best = f;
+                        idx = o * 8 + j;
+                    }
+                }
             }
         }
     }
