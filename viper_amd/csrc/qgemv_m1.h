@@ -32,22 +32,31 @@ namespace vq {
 // two halves meet by a DPP lane swap of the int32 partial, and the even lane
 // of the pair applies the group's scales.
 //
-// LDS: xq [K] int8 (octets in the format's dot order) and, per chunk,
-// {-OFF * sum(q) over the chunk (int32), xs (fp32)}.
+// LDS: xq [K] int8 (octets in the format's dot order), per chunk
+// {-OFF * sum(q) over the chunk (int32), xs (fp32)}, 16 floats of cross-wave
+// sums and, for exact tilings, the workgroup's block of weight scales.
 
-constexpr int M1_CPL = 10;  // chunk slots per lane per row segment
 constexpr int M1_XS = 4;    // activation octets per thread loaded before the weights
-constexpr int M1_DELAY = 4; // weight-issue delay, s_sleep units
+constexpr int M1_DELAY = 8; // weight-issue delay, s_sleep units
 
-
-// LDS: xq [K], per-chunk records, 16 floats of cross-wave sums
-template <int F>
-__host__ __device__ constexpr size_t m1_lds_bytes(int K) {
-    return (size_t)K + (size_t)(K / Fmt<F>::CK) * 8 + 64;
+// Weight-scale block of an exact-tiled workgroup: rows x groups 16-bit scales.
+__host__ __device__ constexpr size_t m1_scale_block(int rows, int ngr) {
+    return ((size_t)rows * ngr * 2 + 15) / 16 * 16;
 }
 
-// EXACT: every lane's chunks of every slot lie inside its row (the row has
-// exactly TS * M1_CPL chunks), so no chunk needs masking.
+// LDS bytes of a launch: xq [K], per-chunk records, cross-wave sums, the
+// scale block of `rows` rows (exact tilings).
+template <int F>
+__host__ __device__ constexpr size_t m1_lds_bytes(int K, int rows) {
+    return (size_t)K + (size_t)(K / Fmt<F>::CK) * 8 + 64 + m1_scale_block(rows, K / Fmt<F>::G);
+}
+
+// EXACT: every lane's chunks lie inside its row (the row has exactly TS * CPL
+// chunks) and a row's scales fill whole 16-byte words (groups % 8 == 0), so no
+// chunk needs masking and the workgroup's scale block is loaded with one
+// 16-byte load per thread into LDS instead of one 2-byte load per chunk (those
+// small loads slow the weight issue several-fold).  CPL: chunk slots per lane
+// per row segment.
 // DELAY: s_sleep units (64 clocks) between issuing the activation loads and
 // the weight loads.  The activation is a few KB read by every workgroup; a
 // short head start lets its requests through the memory pipeline before the
@@ -55,7 +64,7 @@ __host__ __device__ constexpr size_t m1_lds_bytes(int K) {
 // xa: PRO_INT8 the group scales, PRO_RMSNORM gamma, PRO_SWIGLU up.
 // xout (PRO_RMSNORM, may be null): the bf16 normalized row, written by the
 // first workgroup.
-template <int F, int TS, int NTT, int SENC, bool PART, bool EXACT, int PRO, int DELAY>
+template <int F, int TS, int NTT, int CPL, int SENC, bool PART, bool EXACT, int PRO, int DELAY>
 __global__ void __launch_bounds__(NTT)
 qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint8_t* w0, const uint16_t* s0,
                 uint16_t* y0, int n0, float eps, uint16_t* __restrict__ xout, const uint16_t* res,
@@ -64,7 +73,6 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint
     using FT = Fmt<F>;
     constexpr bool PRE = PRO == PRO_INT8;
     constexpr bool TWO = PRO == PRO_RMSNORM || PRO == PRO_SWIGLU;  // two bf16 inputs
-    constexpr int CPL = M1_CPL;
     constexpr int XS = M1_XS;
     constexpr int ROWS = NTT / TS;
     constexpr int HB = FT::HIW * 4;  // high-plane bytes per chunk: Q5 4, Q6 8
@@ -75,6 +83,7 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint
     int8_t* lxq = (int8_t*)smem;
     u32x2* lcs = (u32x2*)(smem + K);
     float* lred = (float*)(smem + K + (size_t)CPR * 8);
+    uint16_t* lsc = (uint16_t*)(smem + K + (size_t)CPR * 8 + 64);
 
     const int tid = (int)threadIdx.x;
     const int l = tid % TS;
@@ -123,15 +132,21 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint
             return bload16(xr, o * 16);
         }
     };
+    // rounds past the row are not issued (the bound is workgroup-uniform)
     u32x4 xv[XS], av[XS];
 #pragma unroll
-    for (int i = 0; i < XS; ++i) xv[i] = load_x(tid + NTT * i);
-    if constexpr (TWO) {
-#pragma unroll
-        for (int i = 0; i < XS; ++i) av[i] = bload16(xsr, (tid + NTT * i) * 16);
+    for (int i = 0; i < XS; ++i) {
+        xv[i] = u32x4{0u, 0u, 0u, 0u};
+        av[i] = xv[i];
+        if (i == 0 || NTT * i < noct) {
+            xv[i] = load_x(tid + NTT * i);
+            if constexpr (TWO) av[i] = bload16(xsr, (tid + NTT * i) * 16);
+        }
     }
     issue_fence();
     const auto sr = buf(ws + (size_t)row0 * NGR, (uint32_t)(nrows * NGR) * 2);
+    u32x4 sblk = {0u, 0u, 0u, 0u};
+    if constexpr (EXACT) sblk = bload16(sr, tid * 16);
     const bool lead = (l & 1) == 0;  // the even lane of a chunk pair owns the group
 
     const uint32_t rbytes = (uint32_t)CPR * 16;
@@ -149,7 +164,8 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint
             wv[j] = bload16<AUX_NT>(wr, in ? rr * (int)rbytes + c * 16 : OOB);
             // odd lanes and chunks past the row read scale 0, which zeroes
             // their term without any select
-            sv[j] = bload2(sr, (in && lead) ? (rr * NGR + (c >> 1)) * 2 : OOB);
+            sv[j] = 0u;
+            if constexpr (!EXACT) sv[j] = bload2(sr, (in && lead) ? (rr * NGR + (c >> 1)) * 2 : OOB);
             h0[j] = 0u;
             h1[j] = 0u;
             if constexpr (FT::HIW == 1) {
@@ -169,6 +185,8 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint
     //    octet as (ql nibbles, qh nibbles); Q5/Q6 as [k even | k odd] int8;
     //    W8 in k order.
     const int xiters = (noct + NTT - 1) / NTT;
+    if constexpr (EXACT)
+        if (tid * 16 < nrows * NGR * 2) *(u32x4*)((uint8_t*)lsc + tid * 16) = sblk;
     // PRO_RMSNORM: the row's sum of squares (per-thread fma chain over its
     // octets in order, DPP within the wave, wave sums in wave order)
     float inv = 0.0f;
@@ -282,7 +300,9 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint
             const int g = cc >> 1;
             if constexpr (PART)
                 if (ok && lead && row_ok) part[(size_t)row * NGR + g] = dot;
-            const float wsf = SENC ? bf16f(sv[j]) : f16f(sv[j]);
+            uint32_t svj = sv[j];
+            if constexpr (EXACT) svj = lead ? (uint32_t)lsc[rr * NGR + (c >> 1)] : 0u;
+            const float wsf = SENC ? bf16f(svj) : f16f(svj);
             acc = __builtin_fmaf(wsf * __uint_as_float(cs.y), (float)dot, acc);
         }
     }
@@ -297,47 +317,52 @@ typedef void (*m1_fn)(const void*, const void*, int, int, int, const uint8_t*, c
                       float, uint16_t*, const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*,
                       int, const uint8_t*, const uint16_t*, uint16_t*, int);
 
-// Launch shapes instantiated for every format: (team size, workgroup size).
-constexpr int M1_SHAPES[][2] = {{8, 128}, {8, 192}, {8, 320}, {16, 256}, {16, 640}, {32, 320}, {32, 640}, {64, 640}};
+// Launch shapes instantiated for every format: (team size, workgroup size,
+// chunk slots per lane).
+constexpr int M1_SHAPES[][3] = {{8, 128, 10}, {8, 192, 10}, {8, 320, 10}, {16, 256, 10}, {16, 640, 10},
+                                {32, 320, 10}, {32, 640, 10}, {64, 640, 10}, {16, 256, 5}, {16, 320, 5},
+                                {16, 640, 5}, {32, 640, 5}, {64, 640, 5}};
 
 template <int F, int SENC, bool PART, bool EXACT, int PRO>
-m1_fn m1_kernel_v(int ts, int ntt) {
-#define VQ_M1(TS_, NTT_) \
-    if (ts == TS_ && ntt == NTT_) return qgemv_m1_kernel<F, TS_, NTT_, SENC, PART, EXACT, PRO, M1_DELAY>;
-    VQ_M1(8, 128) VQ_M1(8, 192) VQ_M1(8, 320) VQ_M1(16, 256) VQ_M1(16, 640) VQ_M1(32, 320) VQ_M1(32, 640)
-    VQ_M1(64, 640)
+m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
+#define VQ_M1(TS_, NTT_, CPL_)                  \
+    if (ts == TS_ && ntt == NTT_ && cpl == CPL_) \
+        return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, PART, EXACT, PRO, M1_DELAY>;
+    VQ_M1(8, 128, 10) VQ_M1(8, 192, 10) VQ_M1(8, 320, 10) VQ_M1(16, 256, 10) VQ_M1(16, 640, 10)
+    VQ_M1(32, 320, 10) VQ_M1(32, 640, 10) VQ_M1(64, 640, 10) VQ_M1(16, 256, 5) VQ_M1(16, 320, 5)
+    VQ_M1(16, 640, 5) VQ_M1(32, 640, 5) VQ_M1(64, 640, 5)
 #undef VQ_M1
     return nullptr;
 }
 
 template <int F, int PRO>
-m1_fn m1_pick_pro(int ts, int ntt, int senc, bool part, bool exact) {
+m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, bool part, bool exact) {
     if (exact) {
-        if (senc) return part ? m1_kernel_v<F, 1, true, true, PRO>(ts, ntt) : m1_kernel_v<F, 1, false, true, PRO>(ts, ntt);
-        return part ? m1_kernel_v<F, 0, true, true, PRO>(ts, ntt) : m1_kernel_v<F, 0, false, true, PRO>(ts, ntt);
+        if (senc) return part ? m1_kernel_v<F, 1, true, true, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 1, false, true, PRO>(ts, ntt, cpl);
+        return part ? m1_kernel_v<F, 0, true, true, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 0, false, true, PRO>(ts, ntt, cpl);
     }
-    if (senc) return part ? m1_kernel_v<F, 1, true, false, PRO>(ts, ntt) : m1_kernel_v<F, 1, false, false, PRO>(ts, ntt);
-    return part ? m1_kernel_v<F, 0, true, false, PRO>(ts, ntt) : m1_kernel_v<F, 0, false, false, PRO>(ts, ntt);
+    if (senc) return part ? m1_kernel_v<F, 1, true, false, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 1, false, false, PRO>(ts, ntt, cpl);
+    return part ? m1_kernel_v<F, 0, true, false, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 0, false, false, PRO>(ts, ntt, cpl);
 }
 
 // Kernels of format F with the quantize / int8 prologues and with the folded
 // rmsnorm / swiglu prologues (each defined in its own translation unit).
 template <int F>
-m1_fn m1_pick_plain(int ts, int ntt, int senc, bool part, bool exact, int pro);
+m1_fn m1_pick_plain(int ts, int ntt, int cpl, int senc, bool part, bool exact, int pro);
 template <int F>
-m1_fn m1_pick_folded(int ts, int ntt, int senc, bool part, bool exact, int pro);
+m1_fn m1_pick_folded(int ts, int ntt, int cpl, int senc, bool part, bool exact, int pro);
 
 #define VQ_M1_PLAIN(F)                                                                         \
     template <>                                                                                \
-    m1_fn m1_pick_plain<F>(int ts, int ntt, int senc, bool part, bool exact, int pro) {        \
-        return pro == PRO_INT8 ? m1_pick_pro<F, PRO_INT8>(ts, ntt, senc, part, exact)          \
-                               : m1_pick_pro<F, PRO_BF16>(ts, ntt, senc, part, exact);         \
+    m1_fn m1_pick_plain<F>(int ts, int ntt, int cpl, int senc, bool part, bool exact, int pro) { \
+        return pro == PRO_INT8 ? m1_pick_pro<F, PRO_INT8>(ts, ntt, cpl, senc, part, exact)       \
+                               : m1_pick_pro<F, PRO_BF16>(ts, ntt, cpl, senc, part, exact);      \
     }
 #define VQ_M1_FOLDED(F)                                                                        \
     template <>                                                                                \
-    m1_fn m1_pick_folded<F>(int ts, int ntt, int senc, bool part, bool exact, int pro) {       \
-        return pro == PRO_SWIGLU ? m1_pick_pro<F, PRO_SWIGLU>(ts, ntt, senc, part, exact)      \
-                                 : m1_pick_pro<F, PRO_RMSNORM>(ts, ntt, senc, part, exact);    \
+    m1_fn m1_pick_folded<F>(int ts, int ntt, int cpl, int senc, bool part, bool exact, int pro) { \
+        return pro == PRO_SWIGLU ? m1_pick_pro<F, PRO_SWIGLU>(ts, ntt, cpl, senc, part, exact)     \
+                                 : m1_pick_pro<F, PRO_RMSNORM>(ts, ntt, cpl, senc, part, exact);   \
     }
 
 }  // namespace vq

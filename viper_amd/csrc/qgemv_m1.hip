@@ -4,59 +4,92 @@
 namespace vq {
 
 struct M1Shape {
-    int ts, ntt;
+    int ts, ntt, cpl;
 };
 
-static bool m1_instantiated(int ts, int ntt) {
-    for (const auto& s : M1_SHAPES)
-        if (s[0] == ts && s[1] == ntt) return true;
-    return false;
-}
-
-static m1_fn m1_kernel(int qtype, int ts, int ntt, int senc, bool part, bool exact, int pro) {
+static m1_fn m1_kernel(int qtype, const M1Shape& sh, int senc, bool part, bool exact, int pro) {
     const bool folded = pro == PRO_RMSNORM || pro == PRO_SWIGLU;
+    const int ts = sh.ts, ntt = sh.ntt, cpl = sh.cpl;
     switch (qtype) {
         case VIPER_QTYPE_Q4_G64:
-            return folded ? m1_pick_folded<4>(ts, ntt, senc, part, exact, pro) : m1_pick_plain<4>(ts, ntt, senc, part, exact, pro);
+            return folded ? m1_pick_folded<4>(ts, ntt, cpl, senc, part, exact, pro)
+                          : m1_pick_plain<4>(ts, ntt, cpl, senc, part, exact, pro);
         case VIPER_QTYPE_Q5_G64:
-            return folded ? m1_pick_folded<5>(ts, ntt, senc, part, exact, pro) : m1_pick_plain<5>(ts, ntt, senc, part, exact, pro);
+            return folded ? m1_pick_folded<5>(ts, ntt, cpl, senc, part, exact, pro)
+                          : m1_pick_plain<5>(ts, ntt, cpl, senc, part, exact, pro);
         case VIPER_QTYPE_Q6_G64:
-            return folded ? m1_pick_folded<6>(ts, ntt, senc, part, exact, pro) : m1_pick_plain<6>(ts, ntt, senc, part, exact, pro);
+            return folded ? m1_pick_folded<6>(ts, ntt, cpl, senc, part, exact, pro)
+                          : m1_pick_plain<6>(ts, ntt, cpl, senc, part, exact, pro);
         default:
-            return folded ? m1_pick_folded<8>(ts, ntt, senc, part, exact, pro) : m1_pick_plain<8>(ts, ntt, senc, part, exact, pro);
+            return folded ? m1_pick_folded<8>(ts, ntt, cpl, senc, part, exact, pro)
+                          : m1_pick_plain<8>(ts, ntt, cpl, senc, part, exact, pro);
     }
 }
 
-// Team size: the smallest of 8..64 lanes covering a row in at most M1_CPL
-// chunks per lane (longer rows loop over segments of 64 lanes).  Workgroup
-// size: among the instantiated ones for that team, the one whose per-CU row
-// load ceil(ceil(N/rows)/CUs)*rows is smallest (ties: more rows per group,
-// i.e. fewer redundant activation quantizations).
+// Per-CU row load of a shape: ceil(ceil(N / rows) / CUs) * rows.
+static long m1_load(const M1Shape& sh, int N, int cus) {
+    const long rows = sh.ntt / sh.ts;
+    const long groups = (N + rows - 1) / rows;
+    return ((groups + cus - 1) / cus) * rows;
+}
+
+// Launch shape.  Exact tilings (TS * CPL == chunks per row) come first: their
+// lanes need no masking and their scales arrive in one block.  Among them the
+// smallest per-CU row load wins, then fewer chunk slots per lane (more lanes
+// per row, so each lane's dot chain after the weights arrive is shorter), then
+// the smaller workgroup (two 320-thread workgroups per CU beat one of 640 on
+// the north-star shape: each quantizes and passes its barrier on its own).
+// With no exact tiling: the smallest team covering a row in 10 slots per lane
+// (longer rows loop over segments of 64 lanes), workgroup size by row load,
+// ties to more rows per workgroup (fewer redundant activation quantizations).
 static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt) {
-    int ts = 8;
-    while (ts < 64 && ts * M1_CPL < cpr) ts *= 2;
-    static const int cand[] = {128, 192, 256, 320, 640};
-    M1Shape best{ts, 0};
+    M1Shape best{0, 0, 0};
     long best_load = -1;
-    for (int ntt : cand) {
-        if (!m1_instantiated(ts, ntt) || ntt < min_ntt) continue;
-        const long rows = ntt / ts;
-        const long groups = (N + rows - 1) / rows;
-        const long load = ((groups + cus - 1) / cus) * rows;
-        if (best_load < 0 || load < best_load || (load == best_load && ntt > best.ntt)) {
+    for (const auto& s : M1_SHAPES) {
+        const M1Shape c{s[0], s[1], s[2]};
+        if (c.ntt < min_ntt || c.ts * c.cpl != cpr) continue;
+        const long load = m1_load(c, N, cus);
+        const bool take = best_load < 0 || load < best_load ||
+                          (load == best_load && (c.cpl < best.cpl || (c.cpl == best.cpl && c.ntt < best.ntt)));
+        if (take) {
+            best = c;
             best_load = load;
-            best.ntt = ntt;
+        }
+    }
+    if (best.ntt != 0) return best;
+    int ts = 8;
+    while (ts < 64 && ts * 10 < cpr) ts *= 2;
+    for (const auto& s : M1_SHAPES) {
+        const M1Shape c{s[0], s[1], s[2]};
+        if (c.ts != ts || c.cpl != 10 || c.ntt < min_ntt) continue;
+        const long load = m1_load(c, N, cus);
+        if (best_load < 0 || load < best_load || (load == best_load && c.ntt > best.ntt)) {
+            best = c;
+            best_load = load;
         }
     }
     return best;
 }
 
+// Upper bound over the launch shapes (an exact tiling's scale block holds at
+// most NTT * CPL bytes).
 size_t lds_m1(int qtype, int K) {
+    constexpr int kBlockMax = 640 * 10;
     switch (qtype) {
-        case VIPER_QTYPE_Q4_G64: return m1_lds_bytes<4>(K);
-        case VIPER_QTYPE_Q5_G64: return m1_lds_bytes<5>(K);
-        case VIPER_QTYPE_Q6_G64: return m1_lds_bytes<6>(K);
-        default: return m1_lds_bytes<8>(K);
+        case VIPER_QTYPE_Q4_G64: return m1_lds_bytes<4>(K, 0) + kBlockMax;
+        case VIPER_QTYPE_Q5_G64: return m1_lds_bytes<5>(K, 0) + kBlockMax;
+        case VIPER_QTYPE_Q6_G64: return m1_lds_bytes<6>(K, 0) + kBlockMax;
+        default: return m1_lds_bytes<8>(K, 0) + kBlockMax;
+    }
+}
+
+static size_t lds_m1_launch(int qtype, int K, int rows, bool exact) {
+    const int r = exact ? rows : 0;
+    switch (qtype) {
+        case VIPER_QTYPE_Q4_G64: return m1_lds_bytes<4>(K, r);
+        case VIPER_QTYPE_Q5_G64: return m1_lds_bytes<5>(K, r);
+        case VIPER_QTYPE_Q6_G64: return m1_lds_bytes<6>(K, r);
+        default: return m1_lds_bytes<8>(K, r);
     }
 }
 
@@ -79,11 +112,12 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     const int min_ntt = folded ? (K / 8 + M1_XS - 1) / M1_XS : 0;
     const M1Shape sh = m1_shape(K / ck, ntot, device_cus(), min_ntt);
     if (sh.ntt == 0) return VIPER_INVALID_ARGUMENT;
-    const bool exact = (K / ck) == sh.ts * M1_CPL;
-    const m1_fn fn = m1_kernel(qtype, sh.ts, sh.ntt, senc, part != nullptr, exact, pro);
+    const int group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
+    const bool exact = (K / ck) == sh.ts * sh.cpl && (K / group) % 8 == 0;
+    const m1_fn fn = m1_kernel(qtype, sh, senc, part != nullptr, exact, pro);
     if (fn == nullptr) return VIPER_INTERNAL;
     const int rows = sh.ntt / sh.ts;
-    const size_t lds = lds_m1(qtype, K);
+    const size_t lds = lds_m1_launch(qtype, K, rows, exact);
     if (lds > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
     int nb[3] = {0, 0, 0};
     for (int i = 0; i < nouts; ++i) nb[i] = (outs[i].n + rows - 1) / rows;
