@@ -281,29 +281,41 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint
 
     lds_barrier();
 
-    // 3. chunk dots, group sums, fp32 combine; each chunk waits only for its
-    //    own weights and scale
+    // 3. chunk dots, group sums, fp32 combine.  Every LDS operand of the
+    //    segment is read before the first dot: the reads then overlap the
+    //    wait for the weights instead of sitting between the dots (0.3 us of
+    //    the north-star dispatch).  Each chunk waits only for its own weights.
     float acc = 0.0f;
     for (int seg = 0; seg < nseg; ++seg) {
         if (seg) load_seg(seg);
+        u32x4 A0[CPL], A1[CPL];
+        u32x2 CS[CPL];
+        uint32_t SV[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = seg * segw + j * TS + l;
+            const int cc = EXACT ? c : min(c, CPR - 1);
+            CS[j] = lcs[cc];
+            const u32x4* a = (const u32x4*)(lxq + (size_t)cc * FT::CK);
+            A0[j] = a[0];
+            A1[j] = FT::OFF ? a[1] : a[0];
+            SV[j] = sv[j];
+            if constexpr (EXACT) SV[j] = lead ? (uint32_t)lsc[rr * NGR + (c >> 1)] : 0u;
+        }
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = seg * segw + j * TS + l;
             const bool ok = EXACT || c < CPR;
             const int cc = EXACT ? c : min(c, CPR - 1);
-            const u32x2 cs = lcs[cc];
-            const u32x4* a = (const u32x4*)(lxq + (size_t)cc * FT::CK);
             int dot;
-            if constexpr (F == 4) dot = chunk_dot_q4(wv[j], a[0], a[1], (int)cs.x);
-            else dot = chunk_dot<F>(wv[j], h0[j], h1[j], a[0], FT::OFF ? a[1] : a[0], (int)cs.x);
+            if constexpr (F == 4) dot = chunk_dot_q4(wv[j], A0[j], A1[j], (int)CS[j].x);
+            else dot = chunk_dot<F>(wv[j], h0[j], h1[j], A0[j], A1[j], (int)CS[j].x);
             dot += dpp_i<DPP_SWAP1>(dot);
             const int g = cc >> 1;
             if constexpr (PART)
                 if (ok && lead && row_ok) part[(size_t)row * NGR + g] = dot;
-            uint32_t svj = sv[j];
-            if constexpr (EXACT) svj = lead ? (uint32_t)lsc[rr * NGR + (c >> 1)] : 0u;
-            const float wsf = SENC ? bf16f(svj) : f16f(svj);
-            acc = __builtin_fmaf(wsf * __uint_as_float(cs.y), (float)dot, acc);
+            const float wsf = SENC ? bf16f(SV[j]) : f16f(SV[j]);
+            acc = __builtin_fmaf(wsf * __uint_as_float(CS[j].y), (float)dot, acc);
         }
     }
     acc = team_sum<TS>(acc);
