@@ -66,8 +66,8 @@ __host__ __device__ constexpr size_t m1_lds_bytes(int K, int rows) {
 // first workgroup.
 template <int F, int TS, int NTT, int CPL, int SENC, bool PART, bool EXACT, int PRO, int DELAY>
 __global__ void __launch_bounds__(NTT)
-qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint8_t* w0, const uint16_t* s0,
-                uint16_t* y0, int n0, float eps, uint16_t* __restrict__ xout, const uint16_t* res,
+qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* y0, int K, int n0, int e0,
+                int e1, const uint16_t* res, const void* xa, float eps, uint16_t* __restrict__ xout,
                 int32_t* __restrict__ part, const uint8_t* w1, const uint16_t* s1, uint16_t* y1, int n1,
                 const uint8_t* w2, const uint16_t* s2, uint16_t* y2, int n2) {
     using FT = Fmt<F>;
@@ -325,9 +325,9 @@ qgemv_m1_kernel(const void* x, const void* xa, int K, int e0, int e1, const uint
     }
 }
 
-typedef void (*m1_fn)(const void*, const void*, int, int, int, const uint8_t*, const uint16_t*, uint16_t*, int,
-                      float, uint16_t*, const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*,
-                      int, const uint8_t*, const uint16_t*, uint16_t*, int);
+typedef void (*m1_fn)(const void*, const uint8_t*, const uint16_t*, uint16_t*, int, int, int, int, const uint16_t*,
+                      const void*, float, uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*, int,
+                      const uint8_t*, const uint16_t*, uint16_t*, int);
 
 // Launch shapes instantiated for every format: (team size, workgroup size,
 // chunk slots per lane).

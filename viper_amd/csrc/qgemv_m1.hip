@@ -129,7 +129,7 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     int e0 = nb[0], e1 = nb[0] + nb[1];
     const unsigned grid = (unsigned)(nb[0] + nb[1] + nb[2]);
     const uint16_t* r = (const uint16_t*)res;
-    void* args[] = {&x, &xa, &K, &e0, &e1, &w0, &s0, &y0, &n0, &eps, &xout, &r, &part,
+    void* args[] = {&x, &w0, &s0, &y0, &K, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,
                     &w1, &s1, &y1, &n1, &w2, &s2, &y2, &n2};
     launch((const void*)fn, grid, (unsigned)sh.ntt, lds, st, args, ev0, ev1);
     return status_of(hipGetLastError());
