@@ -39,8 +39,8 @@ namespace vq {
 
 // ------------------------------------------------ standalone activation quantize
 
-// MF: the fragment order qgemm_mfma_kernel reads (octets of 64-groups stored
-// as [even k | odd k], xs transposed to [K/G][16]); else xq [M][K] in k order
+// MF: the fragment order the matrix-core kernels read (xs transposed to
+// [K/G][16]; 64-groups use quantize_frag64_kernel); else xq [M][K] in k order
 // and xs [M][K/G].
 template <int G, bool MF>
 __global__ void __launch_bounds__(NT)
@@ -71,6 +71,40 @@ quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
             if ((o & (G / 8 - 1)) == 0) xs[(size_t)o * 8 / G] = s;
         }
     }
+}
+
+// Fragment order of 64-groups, one wave per group: lane l = 16 * kb + m
+// quantizes row m's quarter bit-swap(kb) of the group (16 values) and stores
+// its 16-byte fragment, so a wave writes the group's 1 KB contiguously.  The
+// group amax is the max over the 4 lanes of row m (lanes m, m + 16, m + 32,
+// m + 48).  Rows m >= M are neither read nor written.
+__global__ void __launch_bounds__(64)
+quantize_frag64_kernel(const uint16_t* x, int M, int K, int8_t* __restrict__ xq, float* __restrict__ xs) {
+    const int L = (int)threadIdx.x, g = (int)blockIdx.x;
+    const int m = L & 15, kb = L >> 4, qi = ((kb & 1) << 1) | (kb >> 1);
+    const bool ok = m < M;
+    const auto xr = buf(x, (uint32_t)M * (uint32_t)K * 2u);
+    const int off = ok ? (m * K + g * 64 + 16 * qi) * 2 : OOB;
+    const u32x4 v0 = bload16(xr, off), v1 = bload16(xr, off + 16);
+    const uint32_t wd[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+    float f[16];
+    float a = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        f[i] = bf16f((wd[i >> 1] >> (16 * (i & 1))) & 0xffffu);
+        a = fmaxf(a, fabsf(f[i]));
+    }
+    a = fmaxf(a, __shfl_xor(a, 16, 64));
+    a = fmaxf(a, __shfl_xor(a, 32, 64));
+    float s, r;
+    group_scale(a, s, r);
+    uint32_t t[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t[i] = qbits(f[i], s, r);
+    const u32x4 o = {bytes4(t[0], t[2], t[4], t[6]), bytes4(t[1], t[3], t[5], t[7]), bytes4(t[8], t[10], t[12], t[14]),
+                     bytes4(t[9], t[11], t[13], t[15])};
+    if (ok) *(u32x4*)(xq + ((size_t)g * 64 + L) * 16) = o;
+    if (ok && kb == 0) xs[g * 16 + m] = s;
 }
 
 // --------------------------------------------------- quantizer self-check
@@ -107,9 +141,14 @@ static int launch_quantize(int group, const void* x, int M, int K, void* xq, voi
     const uint16_t* a0 = (const uint16_t*)x;
     int8_t* a1 = (int8_t*)xq;
     float* a2 = (float*)xs;
+    if (mf && group == 64) {
+        void* fargs[] = {&a0, &M, &K, &a1, &a2};
+        launch((const void*)quantize_frag64_kernel, (unsigned)(K / 64), 64, 0, st, fargs, nullptr, nullptr);
+        return status_of(hipGetLastError());
+    }
     void* args[] = {&a0, &a1, &a2, (void*)&oct_total, &K};
     const void* fn;
-    if (group == 64) fn = mf ? (const void*)quantize_act_kernel<64, true> : (const void*)quantize_act_kernel<64, false>;
+    if (group == 64) fn = (const void*)quantize_act_kernel<64, false>;
     else fn = mf ? (const void*)quantize_act_kernel<32, true> : (const void*)quantize_act_kernel<32, false>;
     launch(fn, grid, NT, 0, st, args, nullptr, nullptr);
     return status_of(hipGetLastError());
