@@ -7,24 +7,17 @@
 // kernels/ops/dp4a_smem_kernel.cu:25-74 and linear_multim.cu:64-130, weight
 // layout as tools/convert/convert.cpp:91-127.  The design is gfx950's own.
 //
-// M = 1 (qgemv_m1_kernel, the decode GEMV):
-//  * a team of TS lanes (a power of two) streams one output row; a lane owns
-//    whole quantization groups (32 bytes of the main plane = two 16-byte
-//    non-temporal loads, plus the group's high-plane bytes and scale);
-//  * every lane first issues its activation loads, then all its weight loads
-//    (the vector-memory counter retires in issue order, so the activation
-//    arrives first), then quantizes the bf16 activation into LDS while the
-//    weight bytes are still in flight;
-//  * nibbles are not sign-converted: v_dot4 runs on the offset codes u (u in
-//    [0, 63] read as int8) and each group's -OFF * sum(q) correction is
-//    computed once per workgroup into LDS, so the int32 group dot D is exact;
-//  * fp32 (ws*xs)*D is accumulated per lane and the team is reduced with DPP
-//    row operations in a fixed order (deterministic).
+// M = 1 (qgemv_m1_kernel in qgemv_m1.h, the decode GEMV): teams of 16-64
+// lanes stream output rows with 16-byte non-temporal loads; each workgroup
+// quantizes the bf16 activation into LDS while its weights are in flight,
+// the int32 group dots are exact (v_dot8 on split activation nibbles for Q4,
+// v_dot4 on offset codes for Q5/Q6/W8) and the fp32 combine is reduced with
+// DPP in a fixed order (deterministic).
 //
-// M = 2..16 and prequantized activations (qgemm_pre_kernel): activations are
-// quantized once into a caller workspace (quantize_act_kernel) or supplied by
-// the caller, staged into LDS per workgroup, and every weight byte is read
-// once for all M rows.
+// M = 2..16 (qgemm_q4t.hip, qgemm_mfma.hip, qgemm_pre.hip): activations are
+// quantized once into a caller workspace (quantize_frag64_kernel in the
+// matrix-core fragment order, else quantize_act_kernel) or supplied by the
+// caller, and every weight byte is read once for all M rows.
 //
 // The activation quantizer never divides per element: with s the group scale
 // and r = 1/s (both IEEE divides, once per group), q0 = x*r and
