@@ -139,6 +139,22 @@ def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
     run_case(torch_dev, qtype, N, K, M, seed=3000 + N + M, scale_enc=senc, residual=(M % 2 == 1))
 
 
+# Q4 with K a multiple of 256 runs the row-contiguous matrix-core kernel: rows
+# per workgroup 8..48 (one workgroup per CU where N allows), one or two
+# 4-group quads per wave (K up to 2560, up to 5120), 4-wave workgroups for
+# short K, ragged last blocks.
+@pytest.mark.parametrize("N,K,M", [
+    (4000, 2560, 16),
+    (6001, 5120, 9),
+    (8000, 4096, 4),
+    (10240, 5120, 16),
+    (12003, 1024, 2),
+    (300, 2816, 13),
+])
+def test_q4_rowcontig_shapes(torch_dev, N, K, M):
+    run_case(torch_dev, O.Q4_G64, N, K, M, seed=5000 + K + M, residual=(M % 2 == 0))
+
+
 def test_verify_m16_full_size(torch_dev):
     # config 2: M=16 speculative verify at the north-star shape
     run_case(torch_dev, O.Q4_G64, 10240, 2560, 16, seed=0x5EED0002)
@@ -194,7 +210,7 @@ def test_row_matches_single_row_call(torch_dev):
         np.testing.assert_array_equal(p1.cpu().numpy()[0], pm.cpu().numpy()[m])
 
 
-@pytest.mark.parametrize("N,K,M", [(200, 2560, 3), (70, 10240, 16), (40, 192, 2)])
+@pytest.mark.parametrize("N,K,M", [(200, 2560, 3), (70, 10240, 16), (40, 192, 2), (6001, 4096, 16)])
 def test_prequantized_entry(torch_dev, N, K, M):
     # activations in viper_hip_quantize_act's layout ([M][K] int8, [M][K/G] fp32)
     torch = torch_dev
