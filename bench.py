@@ -38,12 +38,48 @@ def algorithmic_bytes(qtype_bytes_per_row, N, K, M, G=64):
     return N * qtype_bytes_per_row + N * (K // G) * 2 + M * K * 2 + M * N * 2
 
 
-def make_weights(torch, copies, N, K, gen):
-    """Uniform bytes = uniform nibbles in [-8, 7]; fp16 scales log-uniform in [1e-3, 1e-2]."""
-    w = torch.randint(0, 256, (copies, N * K // 2), dtype=torch.uint8, device="cuda", generator=gen)
-    u = torch.rand((copies, N * (K // 64)), device="cuda", generator=gen, dtype=torch.float32)
+def make_weights(torch, copies, N, K, gen, row_bytes=None, G=64):
+    """Uniform bytes = uniform codes over each format's range (Q4 nibbles in [-8, 7], the Q5/Q6 low
+    and high planes, W8 bytes; W8's -128 code is the only value outside its stated range and does not
+    change the timing); fp16 scales log-uniform in [1e-3, 1e-2]."""
+    rb = K // 2 if row_bytes is None else row_bytes
+    w = torch.randint(0, 256, (copies, N * rb), dtype=torch.uint8, device="cuda", generator=gen)
+    u = torch.rand((copies, N * (K // G)), device="cuda", generator=gen, dtype=torch.float32)
     s = torch.exp(math.log(1e-3) + u * math.log(10.0)).to(torch.float16)
     return w, s
+
+
+# bytes per weight row and group size of each format (the layouts of DESIGN.md section 3)
+ROW_BYTES = {4: lambda K: K // 2, 5: lambda K: K * 5 // 8, 6: lambda K: K * 6 // 8, 8: lambda K: K}
+GROUP = {4: 64, 5: 64, 6: 64, 8: 32}
+
+
+def time_linear(torch, L, gen, qtype, N, K, M, steps=400):
+    """us per call of viper_hip_qlinear (bf16 x, fused or separate quantize) over rotating weights."""
+    G = GROUP[qtype]
+    rb = ROW_BYTES[qtype](K)
+    copy_bytes = N * rb + N * (K // G) * 2
+    copies = max(2, -(-ROTATE_BYTES // copy_bytes) + 1)
+    W, S = make_weights(torch, copies, N, K, gen, row_bytes=rb, G=G)
+    x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    nws = L.viper_hip_qlinear_workspace_bytes(qtype, N, K, M)
+    ws = torch.empty(max(nws, 16), dtype=torch.uint8, device="cuda")
+
+    def launch(i):
+        c = i % copies
+        rc = L.viper_hip_qlinear(qtype, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K, x.data_ptr(), M,
+                                 y.data_ptr(), None, ws.data_ptr() if nws else None, nws,
+                                 torch.cuda.current_stream().cuda_stream)
+        if rc != 0:
+            raise RuntimeError(f"qlinear qtype={qtype} N={N} K={K} M={M} failed: {rc}")
+    for i in range(20):
+        launch(i)
+    g, r = capture(torch, launch, copies, steps)
+    us = time_graph(torch, g, r) * 1e3 / (r * copies)
+    del g, W, S
+    alg = algorithmic_bytes(rb, N, K, M, G)
+    return round(us, 3), round(alg / (us * 1e-6) / 1e9, 1)
 
 
 def capture(torch, launch, copies, steps):
@@ -173,6 +209,20 @@ def main():
         extras["m16_verify_us"] = round(m16_us, 3)
         extras["m16_verify_gbs"] = round(alg16 / (m16_us * 1e-6) / 1e9, 1)
         del g16
+
+        # config 2: the other speculative-verify row counts at the north-star shape, and M=16 at the
+        # down-projection shape
+        for Mv in (2, 4, 8):
+            us_v, gbs_v = time_linear(torch, L, gen, qtype, N, K, Mv)
+            extras[f"verify_m{Mv}_us"], extras[f"verify_m{Mv}_gbs"] = us_v, gbs_v
+        us_v, gbs_v = time_linear(torch, L, gen, qtype, 2560, 10240, 16)
+        extras["verify_m16_down_us"], extras["verify_m16_down_gbs"] = us_v, gbs_v
+
+        # config 4: Q5_G64, Q6_G64 and W8_G32 at M=1 and M=8, K=2560, N=10240
+        for qt, nm in ((5, "q5"), (6, "q6"), (8, "w8")):
+            for Mv in (1, 8):
+                us_v, gbs_v = time_linear(torch, L, gen, qt, N, K, Mv)
+                extras[f"{nm}_m{Mv}_us"], extras[f"{nm}_m{Mv}_gbs"] = us_v, gbs_v
 
         # down projection shape (K=10240, N=2560), M=1, fused quantize
         Kd, Nd = 10240, 2560
