@@ -191,6 +191,13 @@ def test_format_sweep_full_size(torch_dev, qtype):
     run_case(torch_dev, qtype, 10240, 2560, 1, seed=0x5EED0004, outlier=0.05, check_partials=False)
 
 
+@pytest.mark.parametrize("qtype", FORMATS)
+def test_format_sweep_m8_full_size(torch_dev, qtype):
+    # config 4 at M=8: 40-row workgroups of the row-contiguous matrix-core kernel
+    # (W8: two 4-group quads per wave)
+    run_case(torch_dev, qtype, 10240, 2560, 8, seed=0x5EED0005, outlier=0.05, residual=True)
+
+
 def test_row_matches_single_row_call(torch_dev):
     # row m of an M-row call equals an M=1 call on row m, bit for bit
     torch = torch_dev

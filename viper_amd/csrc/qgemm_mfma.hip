@@ -1,4 +1,6 @@
-// M = 2..16: quantized skinny GEMM on the i8 matrix cores of gfx950.
+// M = 2..16: quantized skinny GEMM on the i8 matrix cores of gfx950, for K a
+// multiple of two groups that the row-contiguous kernels (qgemm_rc.h, K a
+// multiple of four groups) do not take.
 //
 // Semantics are those of the reference's multi-row path
 // (kernels/ops/linear_multim.cu:64-130): per group, the int32 dot of the
@@ -383,7 +385,7 @@ static bool staged_fits(int NG, MfShape sh) {
 }
 
 bool mfma_staged(int qtype, int N, int K) {
-    if (q4t_ok(qtype, K)) return true;  // reads fragments straight from the workspace
+    if (rc_ok(qtype, K)) return true;  // reads fragments straight from the workspace
     const int G = group_of(qtype);
     if (G == 0) return false;
     const int NG = K / G;
@@ -395,8 +397,8 @@ int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K,
                 const void* w1, const void* s1, void* y1, hipStream_t st, hipEvent_t ev0,
                 hipEvent_t ev1) {
     if (!mfma_ok(qtype, K, M, s)) return VIPER_INTERNAL;
-    if (q4t_ok(qtype, K))
-        return launch_q4t(w, s, senc, N, K, xq, xs, xnat, M, y, res, part, w1, s1, y1, st, ev0, ev1);
+    if (rc_ok(qtype, K))
+        return launch_rc(qtype, w, s, senc, N, K, xq, xs, xnat, M, y, res, part, w1, s1, y1, st, ev0, ev1);
     const int NG = K / group_of(qtype);
     const int NP = NG / 2;
     const MfShape sh = mf_shape(N, NP, device_cus());

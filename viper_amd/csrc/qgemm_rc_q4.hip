@@ -1,0 +1,8 @@
+// Row-contiguous matrix-core kernels of format 4 (the template is in qgemm_rc.h).
+#include "qgemm_rc.h"
+
+namespace vq {
+
+VQ_RC_PICK(4)
+
+}  // namespace vq

@@ -14,7 +14,7 @@
 // v_dot4 on offset codes for Q5/Q6/W8) and the fp32 combine is reduced with
 // DPP in a fixed order (deterministic).
 //
-// M = 2..16 (qgemm_q4t.hip, qgemm_mfma.hip, qgemm_pre.hip): activations are
+// M = 2..16 (qgemm_rc.h, qgemm_mfma.hip, qgemm_pre.hip): activations are
 // quantized once into a caller workspace (quantize_frag64_kernel in the
 // matrix-core fragment order, else quantize_act_kernel) or supplied by the
 // caller, and every weight byte is read once for all M rows.

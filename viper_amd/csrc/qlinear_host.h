@@ -100,13 +100,13 @@ int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K, 
 // true> writes, which the shape must support (mfma_staged).
 bool mfma_ok(int qtype, int K, int M, const void* s);
 
-// M = 2..16, Q4_G64 with K a multiple of 256 (qgemm_q4t.hip): row-contiguous
-// weight loads transposed into the matrix-core layout through LDS.  Reads the
-// fragment order of quantize_act_kernel<64, true> or (xnat) the natural layout.
-bool q4t_ok(int qtype, int K);
-int launch_q4t(const void* w, const void* s, int senc, int N, int K, const void* xq, const void* xs, bool xnat,
-               int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
-               hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
+// M = 2..16, K a multiple of 4 groups (qgemm_rc.hip): row-contiguous weight
+// loads moved into the matrix-core layout through LDS.  Reads the fragment
+// order of the fragment quantize or (xnat) the natural layout.
+bool rc_ok(int qtype, int K);
+int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq, const void* xs,
+              bool xnat, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
+              hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
 bool mfma_staged(int qtype, int N, int K);
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
