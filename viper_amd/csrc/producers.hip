@@ -129,7 +129,7 @@ swiglu_quantize_kernel(const uint16_t* gate, const uint16_t* __restrict__ up, in
         unpack8(*(const u32x4*)(gate + base), g);
         unpack8(*(const u32x4*)(up + base), u);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) g[j] = g[j] / (1.0f + __expf(-g[j])) * u[j];
+        for (int j = 0; j < 8; ++j) g[j] = silu_mul(g[j], u[j]);
         v = pack8(g);
         if (out != nullptr) *(u32x4*)(out + base) = v;
     }

@@ -17,7 +17,7 @@ namespace vq {
 //                gamma), then quantized (the reference's rmsnorm_quantize,
 //                kernels/ops/rmsnorm_quantize.cu:37-104, folded into the GEMV:
 //                every workgroup recomputes the row's sum of squares);
-//   PRO_SWIGLU   bf16 gate and up: v = bf16(g / (1 + exp(-g)) * u), then
+//   PRO_SWIGLU   bf16 gate and up: v = bf16(silu(g) * u) (silu_mul), then
 //                quantized (swiglu_quantize.cu:35-78 folded in).
 // The two folded prologues need the whole row in one load round
 // (K / 8 <= M1_XS * NTT octets).
@@ -224,8 +224,8 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
                 f0 = (f0 * inv) * g0;
                 f1 = (f1 * inv) * g1;
             } else {
-                f0 = f0 / (1.0f + __expf(-f0)) * g0;
-                f1 = f1 / (1.0f + __expf(-f1)) * g1;
+                f0 = silu_mul(f0, g0);
+                f1 = silu_mul(f1, g1);
             }
             o[j] = (uint32_t)f2bf(f0) | ((uint32_t)f2bf(f1) << 16);
         }

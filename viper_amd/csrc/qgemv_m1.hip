@@ -35,22 +35,27 @@ static long m1_load(const M1Shape& sh, int N, int cus) {
 
 // Launch shape.  Exact tilings (TS * CPL == chunks per row) come first: their
 // lanes need no masking and their scales arrive in one block.  Among them the
-// smallest per-CU row load wins, then fewer chunk slots per lane (more lanes
-// per row, so each lane's dot chain after the weights arrive is shorter), then
-// the smaller workgroup (two 320-thread workgroups per CU beat one of 640 on
-// the north-star shape: each quantizes and passes its barrier on its own).
-// With no exact tiling: the smallest team covering a row in 10 slots per lane
-// (longer rows loop over segments of 64 lanes), workgroup size by row load,
-// ties to more rows per workgroup (fewer redundant activation quantizations).
-static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt) {
+// smallest per-CU row load wins, then a workgroup that stages the activation
+// row in one round (noct <= NTT: one octet per thread, a single quantize
+// pass), then fewer chunk slots per lane (more lanes per row, so each lane's
+// dot chain after the weights arrive is shorter), then the smaller workgroup
+// (two 320-thread workgroups per CU beat one of 640 on the north-star shape:
+// each quantizes and passes its barrier on its own).  With no exact tiling:
+// the smallest team covering a row in 10 slots per lane (longer rows loop over
+// segments of 64 lanes), workgroup size by row load, ties to more rows per
+// workgroup (fewer redundant activation quantizations).
+static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct) {
     M1Shape best{0, 0, 0};
     long best_load = -1;
     for (const auto& s : M1_SHAPES) {
         const M1Shape c{s[0], s[1], s[2]};
         if (c.ntt < min_ntt || c.ts * c.cpl != cpr) continue;
         const long load = m1_load(c, N, cus);
+        const bool one = c.ntt >= noct, best_one = best.ntt >= noct;
         const bool take = best_load < 0 || load < best_load ||
-                          (load == best_load && (c.cpl < best.cpl || (c.cpl == best.cpl && c.ntt < best.ntt)));
+                          (load == best_load &&
+                           (one > best_one ||
+                            (one == best_one && (c.cpl < best.cpl || (c.cpl == best.cpl && c.ntt < best.ntt)))));
         if (take) {
             best = c;
             best_load = load;
@@ -96,7 +101,7 @@ static size_t lds_m1_launch(int qtype, int K, int rows, bool exact) {
 bool m1_folded_ok(int qtype, int K, int N) {
     const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32;
     const int noct = K / 8;
-    const M1Shape sh = m1_shape(K / ck, N, device_cus(), (noct + M1_XS - 1) / M1_XS);
+    const M1Shape sh = m1_shape(K / ck, N, device_cus(), (noct + M1_XS - 1) / M1_XS, noct);
     return sh.ntt != 0 && lds_m1(qtype, K) <= (size_t)LDS_MAX;
 }
 
@@ -108,9 +113,15 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     const bool folded = pro == PRO_RMSNORM || pro == PRO_SWIGLU;
     int ntot = 0;
     for (int i = 0; i < nouts; ++i) ntot += outs[i].n;
-    // the folded prologues hold the whole row after one load round
-    const int min_ntt = folded ? (K / 8 + M1_XS - 1) / M1_XS : 0;
-    const M1Shape sh = m1_shape(K / ck, ntot, device_cus(), min_ntt);
+    // The folded prologues hold the whole row after one load round, and run
+    // fastest with one octet per thread (rmsnorm's row sum and swiglu's
+    // element work are then a single pass): take such a workgroup when an
+    // exact tiling allows it, even at a higher row load.
+    const int noct = K / 8;
+    const int cus = device_cus();
+    M1Shape sh{0, 0, 0};
+    if (folded) sh = m1_shape(K / ck, ntot, cus, noct < 640 ? noct : 640, noct);
+    if (sh.ntt == 0) sh = m1_shape(K / ck, ntot, cus, folded ? (noct + M1_XS - 1) / M1_XS : 0, noct);
     if (sh.ntt == 0) return VIPER_INVALID_ARGUMENT;
     const int group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
     const bool exact = (K / ck) == sh.ts * sh.cpl && (K / group) % 8 == 0;

@@ -96,6 +96,14 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// silu(g) * u as the swiglu producers compute it: g * rcp(1 + exp(-g)) * u with
+// the hardware exp and reciprocal (each within 1 ulp; the reference computes
+// g / (1 + __expf(-g)) * u under fast math, swiglu_quantize.cu:39-41).  The
+// bf16-rounded result stays within one bf16 ulp of the IEEE-divide value.
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
+}
+
 // ------------------------------------------------------------- quantizer
 
 constexpr float RND_MAGIC = 12582912.0f;  // 1.5 * 2^23
