@@ -168,6 +168,22 @@ int viper_hip_qlinear_m1(int qtype, int scale_enc, int group, int K, int prologu
                          const void* const* w_scales, const int* N, void* const* y_bf16,
                          const void* residual_bf16, void* stream);
 
+/* M = 1 gate/up pair with the swiglu epilogue, one launch:
+ *   g = linear(w_gate, v), u = linear(w_up, v)   two matrices of one qtype,
+ *                                                scale encoding and shape N x K;
+ *   h[n] = bf16(silu(g[n]) * u[n])               from the bf16-rounded g and u,
+ * where v is the activation row of the BF16 or RMSNORM prologue (a, b, eps
+ * and norm_out as viper_hip_qlinear_m1).  h equals, bit for bit, the bf16
+ * output of viper_hip_swiglu_quantize applied to the two outputs of
+ * viper_hip_qlinear_m1 for the same matrices.  gate_bf16 and up_bf16 (may be
+ * NULL) receive g and u.  Replaces dp4a_smem_gemv_fused2(gate, up) followed by
+ * swiglu_quantize_bf16's silu (include/viper/model_impl.cuh:724-727), with the
+ * int8 quantize of h left to the down projection's prologue. */
+int viper_hip_qlinear_m1_swiglu(int qtype, int scale_enc, int group, int K, int prologue, const void* a,
+                                const void* b, float eps, void* norm_out, const void* w_gate,
+                                const void* s_gate, const void* w_up, const void* s_up, int N, void* h_bf16,
+                                void* gate_bf16, void* up_bf16, void* stream);
+
 /* Producer-side activation quantize, per row m < M of H (or I) elements:
  *   rmsnorm: v = bf16_RNE((x * rsqrt(sum(x^2)/H + eps)) * gamma),
  *   swiglu:  v = bf16_RNE(gate / (1 + exp(-gate)) * up),

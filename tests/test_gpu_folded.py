@@ -91,6 +91,71 @@ def test_swiglu_down_residual_equals_two_launches(torch_dev):
     np.testing.assert_array_equal(u16(y), u16(r))
 
 
+# gate/up pair with the swiglu epilogue: equal, bit for bit, to the two GEMVs
+# of one viper_hip_qlinear_m1 launch followed by the standalone swiglu kernel;
+# the engine shape (rmsnorm prologue, K=2560, N=10240), the bf16 prologue,
+# every format, exact and masked tilings, ragged N, optional gate/up outputs.
+@pytest.mark.parametrize("qtype,N,K,pro", [
+    (O.Q4_G64, 10240, 2560, P.RMSNORM),
+    (O.Q4_G64, 1000, 2560, P.BF16),
+    (O.Q4_G64, 333, 1536, P.RMSNORM),
+    (O.Q5_G64, 2100, 2560, P.BF16),
+    (O.Q6_G64, 517, 4096, P.RMSNORM),
+    (O.W8_G32, 777, 2560, P.BF16),
+    (O.Q4_G64, 2560, 10240, P.BF16),
+])
+def test_gate_up_swiglu_equals_chain(torch_dev, qtype, N, K, pro):
+    torch = torch_dev
+    print(f"gate_up_swiglu qtype={qtype} N={N} K={K} pro={int(pro)}", flush=True)
+    eps = 1e-6
+    wg = weights(torch, qtype, N, K, 540 + K)[0]
+    wu = weights(torch, qtype, N, K, 541 + K)[0]
+    x = dev(torch, O.gen_act(1, K, 542, outlier_frac=0.02))
+    rng = np.random.default_rng(543)
+    gamma = dev(torch, bf16(1.0 + 0.1 * rng.standard_normal(K))) if pro == P.RMSNORM else None
+    z = lambda: torch.zeros((1, N), dtype=torch.int16, device="cuda")
+    h, g1, u1, h_only = z(), z(), z(), z()
+    assert va.linear_m1_swiglu(wg, wu, pro, x, gamma, h, eps=eps, gate_out=g1, up_out=u1).ok()
+    assert va.linear_m1_swiglu(wg, wu, pro, x, gamma, h_only, eps=eps).ok()
+    # chain: one launch for both GEMVs, then the standalone swiglu (its int8 output unused here)
+    g2, u2, h2 = z(), z(), z()
+    assert va.linear_m1([wg, wu], pro, x, gamma, [g2, u2], eps=eps).ok()
+    G = O.group_size(qtype)
+    xq = torch.zeros((1, N), dtype=torch.int8, device="cuda")
+    xs = torch.zeros((1, max(N // G, 1)), dtype=torch.float32, device="cuda")
+    if N % G == 0:
+        assert va.swiglu_quantize(g2, u2, G, xq, xs, out=h2).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(g1), u16(g2))
+    np.testing.assert_array_equal(u16(u1), u16(u2))
+    np.testing.assert_array_equal(u16(h), u16(h_only))
+    if N % G == 0:
+        np.testing.assert_array_equal(u16(h), u16(h2))
+    # the product against the oracle's swiglu of the device's own gate/up: within 1 bf16 ulp.
+    # Below 2^-100 in magnitude both sides only need to be below 2^-100: for gate < -87 the
+    # hardware reciprocal of 1 + exp(-gate) > 2^126 flushes to zero, as the reference's
+    # fast-math division does, where the oracle's IEEE divide keeps a denormal-range value.
+    h_ref = O.swiglu_bf16(u16(g1), u16(u1))
+    hd, hr = u16(h), h_ref
+    tiny = 2.0 ** -100
+    small = np.abs(O.bf16_to_f32(hr)) < tiny
+    assert (np.abs(O.bf16_to_f32(hd))[small] < tiny).all()
+    d = np.abs(hd.astype(np.int32) - hr.astype(np.int32))[~small]
+    assert int(d.max(initial=0)) <= 1, int(d.max())
+
+
+def test_gate_up_swiglu_errors(torch_dev):
+    torch = torch_dev
+    wg = weights(torch, O.Q4_G64, 64, 256, 550)[0]
+    wu = weights(torch, O.Q4_G64, 32, 256, 551)[0]
+    x = dev(torch, O.gen_act(1, 256, 552))
+    h = torch.zeros((1, 64), dtype=torch.int16, device="cuda")
+    assert va.linear_m1_swiglu(wg, wu, P.BF16, x, None, h).code == va.StatusCode.SHAPE_MISMATCH
+    assert va.linear_m1_swiglu(wg, wg, P.SWIGLU, x, x, h).code == va.StatusCode.INVALID_ARGUMENT
+    assert va.linear_m1_swiglu(wg, wg, P.RMSNORM, x, None, h).code == va.StatusCode.INVALID_ARGUMENT
+    assert va.linear_m1_swiglu(wg, wg, P.BF16, x, None, None).code == va.StatusCode.INVALID_ARGUMENT
+
+
 @pytest.mark.parametrize("qtype", [O.Q4_G64, O.Q5_G64, O.Q6_G64, O.W8_G32])
 def test_rmsnorm_prologue_against_oracle(torch_dev, qtype):
     torch = torch_dev

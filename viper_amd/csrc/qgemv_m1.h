@@ -39,16 +39,28 @@ namespace vq {
 constexpr int M1_XS = 4;    // activation octets per thread loaded before the weights
 constexpr int M1_DELAY = 8; // weight-issue delay, s_sleep units
 
+// Kernel modes: plain, with the int32 group dots (test entry point), or the
+// gate/up pair with the swiglu epilogue (M1_SWIGLU): the first NTT/2 threads
+// stream P = ROWS/2 rows of the gate matrix (w0), the others the same P rows
+// of the up matrix (w1), and the workgroup writes h = bf16(silu(g) * u) from
+// the two bf16-rounded outputs.  P must be a whole number of waves' teams so
+// every wave reads one matrix.
+enum { M1_PLAIN = 0, M1_PART = 1, M1_SWIGLU = 2 };
+__host__ __device__ constexpr bool m1_pair_ok(int ts, int ntt) {
+    return (ntt / ts) % 2 == 0 && ((ntt / ts) / 2) % (64 / ts) == 0;
+}
+
 // Weight-scale block of an exact-tiled workgroup: rows x groups 16-bit scales.
 __host__ __device__ constexpr size_t m1_scale_block(int rows, int ngr) {
     return ((size_t)rows * ngr * 2 + 15) / 16 * 16;
 }
 
 // LDS bytes of a launch: xq [K], per-chunk records, cross-wave sums, the
-// scale block of `rows` rows (exact tilings).
+// swiglu epilogue's gate values (up to 32), the scale block of `rows` rows
+// (exact tilings).
 template <int F>
 __host__ __device__ constexpr size_t m1_lds_bytes(int K, int rows) {
-    return (size_t)K + (size_t)(K / Fmt<F>::CK) * 8 + 64 + m1_scale_block(rows, K / Fmt<F>::G);
+    return (size_t)K + (size_t)(K / Fmt<F>::CK) * 8 + 128 + m1_scale_block(rows, K / Fmt<F>::G);
 }
 
 // EXACT: every lane's chunks lie inside its row (the row has exactly TS * CPL
@@ -64,13 +76,15 @@ __host__ __device__ constexpr size_t m1_lds_bytes(int K, int rows) {
 // xa: PRO_INT8 the group scales, PRO_RMSNORM gamma, PRO_SWIGLU up.
 // xout (PRO_RMSNORM, may be null): the bf16 normalized row, written by the
 // first workgroup.
-template <int F, int TS, int NTT, int CPL, int SENC, bool PART, bool EXACT, int PRO, int DELAY>
+template <int F, int TS, int NTT, int CPL, int SENC, int MODE, bool EXACT, int PRO, int DELAY>
 __global__ void __launch_bounds__(NTT)
 qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* y0, int K, int n0, int e0,
                 int e1, const uint16_t* res, const void* xa, float eps, uint16_t* __restrict__ xout,
                 int32_t* __restrict__ part, const uint8_t* w1, const uint16_t* s1, uint16_t* y1, int n1,
                 const uint8_t* w2, const uint16_t* s2, uint16_t* y2, int n2) {
     using FT = Fmt<F>;
+    constexpr bool PART = MODE == M1_PART;
+    constexpr bool SWI = MODE == M1_SWIGLU;
     constexpr bool PRE = PRO == PRO_INT8;
     constexpr bool TWO = PRO == PRO_RMSNORM || PRO == PRO_SWIGLU;  // two bf16 inputs
     constexpr int XS = M1_XS;
@@ -83,7 +97,8 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     int8_t* lxq = (int8_t*)smem;
     u32x2* lcs = (u32x2*)(smem + K);
     float* lred = (float*)(smem + K + (size_t)CPR * 8);
-    uint16_t* lsc = (uint16_t*)(smem + K + (size_t)CPR * 8 + 64);
+    uint16_t* lepi = (uint16_t*)(smem + K + (size_t)CPR * 8 + 64);
+    uint16_t* lsc = (uint16_t*)(smem + K + (size_t)CPR * 8 + 128);
 
     const int tid = (int)threadIdx.x;
     const int l = tid % TS;
@@ -111,10 +126,25 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             N = n1;
         }
     }
-    const int row0 = bid * ROWS;
-    const int row = row0 + rr;
-    const int nrows = min(ROWS, N - row0);
-    const bool row_ok = rr < nrows;
+    // swiglu pair: waves of the second half read the up matrix; rt is the
+    // team's row within its matrix's block of P rows
+    constexpr int P = SWI ? ROWS / 2 : ROWS;
+    int rt = rr;
+    bool up = false;
+    if constexpr (SWI) {
+        up = __builtin_amdgcn_readfirstlane(tid >> 6) * (64 / TS) >= P;  // wave-uniform
+        if (up) {
+            w = w1;
+            ws = s1;
+            rt = rr - P;
+        }
+        res = nullptr;
+    }
+    const int row0 = bid * P;
+    const int row = row0 + rt;
+    const int nrows = min(P, N - row0);
+    const bool row_ok = rt < nrows;
+    const int ltid = up ? tid - P * TS : tid;  // thread index within the matrix's half
 
     // 1. activation octets, then every weight byte and group scale of the
     //    first row segment, all in flight at once
@@ -146,7 +176,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     issue_fence();
     const auto sr = buf(ws + (size_t)row0 * NGR, (uint32_t)(nrows * NGR) * 2);
     u32x4 sblk = {0u, 0u, 0u, 0u};
-    if constexpr (EXACT) sblk = bload16(sr, tid * 16);
+    if constexpr (EXACT) sblk = bload16(sr, ltid * 16);
     const bool lead = (l & 1) == 0;  // the even lane of a chunk pair owns the group
 
     const uint32_t rbytes = (uint32_t)CPR * 16;
@@ -161,17 +191,17 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         for (int j = 0; j < CPL; ++j) {
             const int c = seg * segw + j * TS + l;
             const bool in = EXACT || c < CPR;
-            wv[j] = bload16<AUX_NT>(wr, in ? rr * (int)rbytes + c * 16 : OOB);
+            wv[j] = bload16<AUX_NT>(wr, in ? rt * (int)rbytes + c * 16 : OOB);
             // odd lanes and chunks past the row read scale 0, which zeroes
             // their term without any select
             sv[j] = 0u;
-            if constexpr (!EXACT) sv[j] = bload2(sr, (in && lead) ? (rr * NGR + (c >> 1)) * 2 : OOB);
+            if constexpr (!EXACT) sv[j] = bload2(sr, (in && lead) ? (rt * NGR + (c >> 1)) * 2 : OOB);
             h0[j] = 0u;
             h1[j] = 0u;
             if constexpr (FT::HIW == 1) {
-                h0[j] = bload4<AUX_NT>(hr, in ? (rr * CPR + c) * HB : OOB);
+                h0[j] = bload4<AUX_NT>(hr, in ? (rt * CPR + c) * HB : OOB);
             } else if constexpr (FT::HIW == 2) {
-                const u32x2 hh = bload8<AUX_NT>(hr, in ? (rr * CPR + c) * HB : OOB);
+                const u32x2 hh = bload8<AUX_NT>(hr, in ? (rt * CPR + c) * HB : OOB);
                 h0[j] = hh.x;
                 h1[j] = hh.y;
             }
@@ -185,8 +215,9 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     //    octet as (ql nibbles, qh nibbles); Q5/Q6 as [k even | k odd] int8;
     //    W8 in k order.
     const int xiters = (noct + NTT - 1) / NTT;
+    // (the up matrix's block follows the gate block: lsc[rr * NGR + g] for every team)
     if constexpr (EXACT)
-        if (tid * 16 < nrows * NGR * 2) *(u32x4*)((uint8_t*)lsc + tid * 16) = sblk;
+        if (ltid * 16 < nrows * NGR * 2) *(u32x4*)((uint8_t*)lsc + (up ? P * NGR * 2 : 0) + ltid * 16) = sblk;
     // PRO_RMSNORM: the row's sum of squares (per-thread fma chain over its
     // octets in order, DPP within the wave, wave sums in wave order)
     float inv = 0.0f;
@@ -319,9 +350,25 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         }
     }
     acc = team_sum<TS>(acc);
-    if (l == 0 && row_ok) {
-        if (res != nullptr) acc += bf16f(res[row]);
-        y[row] = f2bf(acc);
+    if constexpr (SWI) {
+        // gate values through LDS; y0 / y1 (may be null) receive gate and up,
+        // y2 the product
+        const uint16_t vb = f2bf(acc);
+        if (l == 0 && row_ok) {
+            if (!up) {
+                lepi[rt] = vb;
+                if (y0 != nullptr) y0[row] = vb;
+            } else if (y1 != nullptr) {
+                y1[row] = vb;
+            }
+        }
+        lds_barrier();
+        if (up && l == 0 && row_ok) y2[row] = f2bf(silu_mul(bf16f(lepi[rt]), bf16f(vb)));
+    } else {
+        if (l == 0 && row_ok) {
+            if (res != nullptr) acc += bf16f(res[row]);
+            y[row] = f2bf(acc);
+        }
     }
 }
 
@@ -335,11 +382,12 @@ constexpr int M1_SHAPES[][3] = {{8, 128, 10}, {8, 192, 10}, {8, 320, 10}, {16, 2
                                 {32, 320, 10}, {32, 640, 10}, {64, 640, 10}, {16, 256, 5}, {16, 320, 5},
                                 {16, 640, 5}, {32, 640, 5}, {64, 640, 5}};
 
-template <int F, int SENC, bool PART, bool EXACT, int PRO>
+template <int F, int SENC, int MODE, bool EXACT, int PRO>
 m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
-#define VQ_M1(TS_, NTT_, CPL_)                  \
-    if (ts == TS_ && ntt == NTT_ && cpl == CPL_) \
-        return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, PART, EXACT, PRO, M1_DELAY>;
+#define VQ_M1(TS_, NTT_, CPL_)                                                       \
+    if constexpr (MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_))                        \
+        if (ts == TS_ && ntt == NTT_ && cpl == CPL_)                                 \
+            return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, M1_DELAY>;
     VQ_M1(8, 128, 10) VQ_M1(8, 192, 10) VQ_M1(8, 320, 10) VQ_M1(16, 256, 10) VQ_M1(16, 640, 10)
     VQ_M1(32, 320, 10) VQ_M1(32, 640, 10) VQ_M1(64, 640, 10) VQ_M1(16, 256, 5) VQ_M1(16, 320, 5)
     VQ_M1(16, 640, 5) VQ_M1(32, 640, 5) VQ_M1(64, 640, 5)
@@ -347,34 +395,40 @@ m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
     return nullptr;
 }
 
+template <int F, int PRO, int MODE>
+m1_fn m1_pick_mode(int ts, int ntt, int cpl, int senc, bool exact) {
+    if (exact) return senc ? m1_kernel_v<F, 1, MODE, true, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 0, MODE, true, PRO>(ts, ntt, cpl);
+    return senc ? m1_kernel_v<F, 1, MODE, false, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 0, MODE, false, PRO>(ts, ntt, cpl);
+}
+// The swiglu pair is built for the BF16 and RMSNORM prologues (the inputs of
+// the engine's gate/up projection).
 template <int F, int PRO>
-m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, bool part, bool exact) {
-    if (exact) {
-        if (senc) return part ? m1_kernel_v<F, 1, true, true, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 1, false, true, PRO>(ts, ntt, cpl);
-        return part ? m1_kernel_v<F, 0, true, true, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 0, false, true, PRO>(ts, ntt, cpl);
-    }
-    if (senc) return part ? m1_kernel_v<F, 1, true, false, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 1, false, false, PRO>(ts, ntt, cpl);
-    return part ? m1_kernel_v<F, 0, true, false, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 0, false, false, PRO>(ts, ntt, cpl);
+m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, int mode, bool exact) {
+    if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART>(ts, ntt, cpl, senc, exact);
+    if constexpr (PRO == PRO_BF16 || PRO == PRO_RMSNORM)
+        if (mode == M1_SWIGLU) return m1_pick_mode<F, PRO, M1_SWIGLU>(ts, ntt, cpl, senc, exact);
+    if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN>(ts, ntt, cpl, senc, exact);
+    return nullptr;
 }
 
 // Kernels of format F with the quantize / int8 prologues and with the folded
 // rmsnorm / swiglu prologues (each defined in its own translation unit).
 template <int F>
-m1_fn m1_pick_plain(int ts, int ntt, int cpl, int senc, bool part, bool exact, int pro);
+m1_fn m1_pick_plain(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro);
 template <int F>
-m1_fn m1_pick_folded(int ts, int ntt, int cpl, int senc, bool part, bool exact, int pro);
+m1_fn m1_pick_folded(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro);
 
 #define VQ_M1_PLAIN(F)                                                                         \
     template <>                                                                                \
-    m1_fn m1_pick_plain<F>(int ts, int ntt, int cpl, int senc, bool part, bool exact, int pro) { \
-        return pro == PRO_INT8 ? m1_pick_pro<F, PRO_INT8>(ts, ntt, cpl, senc, part, exact)       \
-                               : m1_pick_pro<F, PRO_BF16>(ts, ntt, cpl, senc, part, exact);      \
+    m1_fn m1_pick_plain<F>(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro) { \
+        return pro == PRO_INT8 ? m1_pick_pro<F, PRO_INT8>(ts, ntt, cpl, senc, mode, exact)       \
+                               : m1_pick_pro<F, PRO_BF16>(ts, ntt, cpl, senc, mode, exact);      \
     }
 #define VQ_M1_FOLDED(F)                                                                        \
     template <>                                                                                \
-    m1_fn m1_pick_folded<F>(int ts, int ntt, int cpl, int senc, bool part, bool exact, int pro) { \
-        return pro == PRO_SWIGLU ? m1_pick_pro<F, PRO_SWIGLU>(ts, ntt, cpl, senc, part, exact)     \
-                                 : m1_pick_pro<F, PRO_RMSNORM>(ts, ntt, cpl, senc, part, exact);   \
+    m1_fn m1_pick_folded<F>(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro) { \
+        return pro == PRO_SWIGLU ? m1_pick_pro<F, PRO_SWIGLU>(ts, ntt, cpl, senc, mode, exact)     \
+                                 : m1_pick_pro<F, PRO_RMSNORM>(ts, ntt, cpl, senc, mode, exact);   \
     }
 
 }  // namespace vq

@@ -7,28 +7,30 @@ struct M1Shape {
     int ts, ntt, cpl;
 };
 
-static m1_fn m1_kernel(int qtype, const M1Shape& sh, int senc, bool part, bool exact, int pro) {
+static m1_fn m1_kernel(int qtype, const M1Shape& sh, int senc, int mode, bool exact, int pro) {
     const bool folded = pro == PRO_RMSNORM || pro == PRO_SWIGLU;
     const int ts = sh.ts, ntt = sh.ntt, cpl = sh.cpl;
     switch (qtype) {
         case VIPER_QTYPE_Q4_G64:
-            return folded ? m1_pick_folded<4>(ts, ntt, cpl, senc, part, exact, pro)
-                          : m1_pick_plain<4>(ts, ntt, cpl, senc, part, exact, pro);
+            return folded ? m1_pick_folded<4>(ts, ntt, cpl, senc, mode, exact, pro)
+                          : m1_pick_plain<4>(ts, ntt, cpl, senc, mode, exact, pro);
         case VIPER_QTYPE_Q5_G64:
-            return folded ? m1_pick_folded<5>(ts, ntt, cpl, senc, part, exact, pro)
-                          : m1_pick_plain<5>(ts, ntt, cpl, senc, part, exact, pro);
+            return folded ? m1_pick_folded<5>(ts, ntt, cpl, senc, mode, exact, pro)
+                          : m1_pick_plain<5>(ts, ntt, cpl, senc, mode, exact, pro);
         case VIPER_QTYPE_Q6_G64:
-            return folded ? m1_pick_folded<6>(ts, ntt, cpl, senc, part, exact, pro)
-                          : m1_pick_plain<6>(ts, ntt, cpl, senc, part, exact, pro);
+            return folded ? m1_pick_folded<6>(ts, ntt, cpl, senc, mode, exact, pro)
+                          : m1_pick_plain<6>(ts, ntt, cpl, senc, mode, exact, pro);
         default:
-            return folded ? m1_pick_folded<8>(ts, ntt, cpl, senc, part, exact, pro)
-                          : m1_pick_plain<8>(ts, ntt, cpl, senc, part, exact, pro);
+            return folded ? m1_pick_folded<8>(ts, ntt, cpl, senc, mode, exact, pro)
+                          : m1_pick_plain<8>(ts, ntt, cpl, senc, mode, exact, pro);
     }
 }
 
-// Per-CU row load of a shape: ceil(ceil(N / rows) / CUs) * rows.
-static long m1_load(const M1Shape& sh, int N, int cus) {
-    const long rows = sh.ntt / sh.ts;
+// Per-CU row load of a shape: ceil(ceil(N / rows) / CUs) * rows (rows per
+// workgroup are halved for the swiglu pair, whose workgroups also read the
+// same rows of the second matrix).
+static long m1_load(const M1Shape& sh, int N, int cus, bool pair = false) {
+    const long rows = pair ? sh.ntt / sh.ts / 2 : sh.ntt / sh.ts;
     const long groups = (N + rows - 1) / rows;
     return ((groups + cus - 1) / cus) * rows;
 }
@@ -44,13 +46,13 @@ static long m1_load(const M1Shape& sh, int N, int cus) {
 // the smallest team covering a row in 10 slots per lane (longer rows loop over
 // segments of 64 lanes), workgroup size by row load, ties to more rows per
 // workgroup (fewer redundant activation quantizations).
-static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct) {
+static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct, bool pair = false) {
     M1Shape best{0, 0, 0};
     long best_load = -1;
     for (const auto& s : M1_SHAPES) {
         const M1Shape c{s[0], s[1], s[2]};
-        if (c.ntt < min_ntt || c.ts * c.cpl != cpr) continue;
-        const long load = m1_load(c, N, cus);
+        if (c.ntt < min_ntt || c.ts * c.cpl != cpr || (pair && !m1_pair_ok(c.ts, c.ntt))) continue;
+        const long load = m1_load(c, N, cus, pair);
         const bool one = c.ntt >= noct, best_one = best.ntt >= noct;
         const bool take = best_load < 0 || load < best_load ||
                           (load == best_load &&
@@ -66,8 +68,8 @@ static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct) {
     while (ts < 64 && ts * 10 < cpr) ts *= 2;
     for (const auto& s : M1_SHAPES) {
         const M1Shape c{s[0], s[1], s[2]};
-        if (c.ts != ts || c.cpl != 10 || c.ntt < min_ntt) continue;
-        const long load = m1_load(c, N, cus);
+        if (c.ts != ts || c.cpl != 10 || c.ntt < min_ntt || (pair && !m1_pair_ok(c.ts, c.ntt))) continue;
+        const long load = m1_load(c, N, cus, pair);
         if (best_load < 0 || load < best_load || (load == best_load && c.ntt > best.ntt)) {
             best = c;
             best_load = load;
@@ -125,7 +127,7 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     if (sh.ntt == 0) return VIPER_INVALID_ARGUMENT;
     const int group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
     const bool exact = (K / ck) == sh.ts * sh.cpl && (K / group) % 8 == 0;
-    const m1_fn fn = m1_kernel(qtype, sh, senc, part != nullptr, exact, pro);
+    const m1_fn fn = m1_kernel(qtype, sh, senc, part != nullptr ? M1_PART : M1_PLAIN, exact, pro);
     if (fn == nullptr) return VIPER_INTERNAL;
     const int rows = sh.ntt / sh.ts;
     const size_t lds = lds_m1_launch(qtype, K, rows, exact);
@@ -143,6 +145,39 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     void* args[] = {&x, &w0, &s0, &y0, &K, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,
                     &w1, &s1, &y1, &n1, &w2, &s2, &y2, &n2};
     launch((const void*)fn, grid, (unsigned)sh.ntt, lds, st, args, ev0, ev1);
+    return status_of(hipGetLastError());
+}
+
+int launch_m1_swiglu(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
+                     const void* wg, const void* sg, const void* wu, const void* su, int N, void* h, void* g_out,
+                     void* u_out, hipStream_t st) {
+    if (pro != PRO_BF16 && pro != PRO_RMSNORM) return VIPER_INVALID_ARGUMENT;
+    const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32;
+    const int noct = K / 8;
+    const int cus = device_cus();
+    M1Shape sh{0, 0, 0};
+    if (pro == PRO_RMSNORM) sh = m1_shape(K / ck, N, cus, noct < 640 ? noct : 640, noct, true);
+    if (sh.ntt == 0) sh = m1_shape(K / ck, N, cus, pro == PRO_RMSNORM ? (noct + M1_XS - 1) / M1_XS : 0, noct, true);
+    if (sh.ntt == 0) return VIPER_INVALID_ARGUMENT;
+    const int group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
+    const bool exact = (K / ck) == sh.ts * sh.cpl && (K / group) % 8 == 0;
+    const m1_fn fn = m1_kernel(qtype, sh, senc, M1_SWIGLU, exact, pro);
+    if (fn == nullptr) return VIPER_INTERNAL;
+    const int rows = sh.ntt / sh.ts;
+    const size_t lds = lds_m1_launch(qtype, K, rows, exact);
+    if (lds > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
+    int n0 = N, n1 = N, n2 = N;
+    int e0 = (N + rows / 2 - 1) / (rows / 2);  // every workgroup is a pair: no second-matrix range
+    int e1 = e0;
+    const unsigned grid = (unsigned)e0;
+    const uint8_t *w0 = (const uint8_t*)wg, *w1 = (const uint8_t*)wu, *w2 = nullptr;
+    const uint16_t *s0 = (const uint16_t*)sg, *s1 = (const uint16_t*)su, *s2 = nullptr;
+    uint16_t *y0 = (uint16_t*)g_out, *y1 = (uint16_t*)u_out, *y2 = (uint16_t*)h;
+    const uint16_t* r = nullptr;
+    int32_t* part = nullptr;
+    void* args[] = {&x, &w0, &s0, &y0, &K, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,
+                    &w1, &s1, &y1, &n1, &w2, &s2, &y2, &n2};
+    launch((const void*)fn, grid, (unsigned)sh.ntt, lds, st, args, nullptr, nullptr);
     return status_of(hipGetLastError());
 }
 

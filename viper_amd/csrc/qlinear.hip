@@ -350,6 +350,26 @@ extern "C" int viper_hip_qlinear_m1(int qtype, int scale_enc, int group, int K, 
                          (hipStream_t)stream, nullptr, nullptr);
 }
 
+extern "C" int viper_hip_qlinear_m1_swiglu(int qtype, int scale_enc, int group, int K, int prologue, const void* a,
+                                           const void* b, float eps, void* norm_out, const void* w_gate,
+                                           const void* s_gate, const void* w_up, const void* s_up, int N,
+                                           void* h_bf16, void* gate_bf16, void* up_bf16, void* stream) {
+    if (prologue != VIPER_PROLOGUE_BF16 && prologue != VIPER_PROLOGUE_RMSNORM) return VIPER_INVALID_ARGUMENT;
+    int rc = vq::validate_weights(qtype, w_gate, s_gate, scale_enc, group, N, K, 1);
+    if (rc != VIPER_OK) return rc;
+    rc = vq::validate_weights(qtype, w_up, s_up, scale_enc, group, N, K, 1);
+    if (rc != VIPER_OK) return rc;
+    if (h_bf16 == nullptr || vq::misaligned(h_bf16, 2) || vq::misaligned(gate_bf16, 2) || vq::misaligned(up_bf16, 2))
+        return VIPER_INVALID_ARGUMENT;
+    if (a == nullptr || (prologue == VIPER_PROLOGUE_RMSNORM && b == nullptr)) return VIPER_INVALID_ARGUMENT;
+    if (vq::misaligned(a, 16) || vq::misaligned(b, 16) || vq::misaligned(norm_out, 16)) return VIPER_INVALID_ARGUMENT;
+    if (norm_out != nullptr && prologue != VIPER_PROLOGUE_RMSNORM) return VIPER_INVALID_ARGUMENT;
+    if (vq::lds_m1(qtype, K) > (size_t)vq::LDS_MAX) return VIPER_INVALID_ARGUMENT;
+    if (prologue == VIPER_PROLOGUE_RMSNORM && !vq::m1_folded_ok(qtype, K, N)) return VIPER_INVALID_ARGUMENT;
+    return vq::launch_m1_swiglu(qtype, scale_enc, K, prologue, a, b, eps, norm_out, w_gate, s_gate, w_up, s_up, N,
+                                h_bf16, gate_bf16, up_bf16, (hipStream_t)stream);
+}
+
 extern "C" int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream) {
     if (counts == nullptr || exp_lo < 0 || exp_hi > 254 || exp_lo > exp_hi)
         return VIPER_INVALID_ARGUMENT;

@@ -88,6 +88,12 @@ bool m1_folded_ok(int qtype, int K, int N);
 int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
               const M1Out* outs, int nouts, const void* res, int32_t* part, hipStream_t st,
               hipEvent_t ev0, hipEvent_t ev1);
+// M = 1 gate/up pair (one shape) with the swiglu epilogue: h = bf16(silu(g)
+// * u) from the bf16-rounded outputs; g_out / u_out may be null.  Prologue
+// PRO_BF16 or PRO_RMSNORM.
+int launch_m1_swiglu(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
+                     const void* wg, const void* sg, const void* wu, const void* su, int N, void* h, void* g_out,
+                     void* u_out, hipStream_t st);
 
 // M <= 16 over prequantized activations, v_dot4 (qgemm_pre.hip).
 int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,

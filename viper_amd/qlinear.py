@@ -128,6 +128,7 @@ _SYMBOLS = (
     "viper_hip_linear_bf16",
     "viper_hip_sampling_greedy",
     "viper_hip_qlinear_m1",
+    "viper_hip_qlinear_m1_swiglu",
 )
 
 
@@ -173,6 +174,9 @@ def lib():
     L.viper_hip_sampling_greedy.restype = i32
     L.viper_hip_qlinear_m1.argtypes = [i32, i32, i32, i32, i32, vp, vp, C.c_float, vp, i32, vp, vp, vp, vp, vp, vp]
     L.viper_hip_qlinear_m1.restype = i32
+    L.viper_hip_qlinear_m1_swiglu.argtypes = [i32, i32, i32, i32, i32, vp, vp, C.c_float, vp, vp, vp, vp, vp, i32,
+                                              vp, vp, vp, vp]
+    L.viper_hip_qlinear_m1_swiglu.restype = i32
     _lib = L
     return L
 
@@ -338,6 +342,21 @@ def linear_m1(ws, prologue, a, b, ys, eps=0.0, norm_out=None, residual=None, str
                                     (C.c_int * n)(*[w.rows for w in ws]), arr([ptr(y) for y in ys]),
                                     ptr(residual), _stream(stream))
     return _status(rc, "viper_hip_qlinear_m1")
+
+
+def linear_m1_swiglu(w_gate, w_up, prologue, a, b, h, eps=0.0, norm_out=None, gate_out=None, up_out=None,
+                     stream=None) -> Status:
+    """One launch at M = 1: g = linear(w_gate, v), u = linear(w_up, v) and h = bf16(silu(g) * u) from the
+    bf16-rounded g and u; v from the BF16 or RMSNORM prologue as in linear_m1.  gate_out / up_out
+    (optional) receive g and u."""
+    if (w_gate.qtype, w_gate.rows, w_gate.cols, w_gate.group_size, w_gate.scale_enc) != \
+            (w_up.qtype, w_up.rows, w_up.cols, w_up.group_size, w_up.scale_enc):
+        return Status(StatusCode.SHAPE_MISMATCH, "linear_m1_swiglu: gate and up differ in kind or shape")
+    rc = lib().viper_hip_qlinear_m1_swiglu(int(w_gate.qtype), int(w_gate.scale_enc), w_gate.group_size, w_gate.cols,
+                                           int(prologue), ptr(a), ptr(b), float(eps), ptr(norm_out),
+                                           ptr(w_gate.data), ptr(w_gate.scales), ptr(w_up.data), ptr(w_up.scales),
+                                           w_gate.rows, ptr(h), ptr(gate_out), ptr(up_out), _stream(stream))
+    return _status(rc, "viper_hip_qlinear_m1_swiglu")
 
 
 def linear_bf16(w, x, y, stream=None) -> Status:

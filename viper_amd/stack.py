@@ -13,11 +13,14 @@ on this path; its output is a fixed activation):
     swiglu_quantize(gate, up)      -> down GEMV + residual (in place on x)
 
 step_fused() is the same computation in 4 launches per slot instead of 9:
-the producers are folded into the GEMV prologues and q/k/v share a launch
-(viper_hip_qlinear_m1):
+the producers are folded into the GEMV prologues, q/k/v share a launch
+(viper_hip_qlinear_m1), and the gate/up launch pairs the rows of both matrices
+so its epilogue writes h = silu(gate) * up (viper_hip_qlinear_m1_swiglu,
+bit-identical to the swiglu of the two outputs); the down projection then
+quantizes h in its prologue:
 
-    [rmsnorm(x, input_ln) -> q, k, v]   [quantize(attn) -> o + residual]
-    [rmsnorm(x, post_ln) -> gate, up]   [swiglu(gate, up) -> down + residual]
+    [rmsnorm(x, input_ln) -> q, k, v]          [quantize(attn) -> o + residual]
+    [rmsnorm(x, post_ln) -> gate, up -> h]     [quantize(h) -> down + residual]
 
 Device buffers are torch tensors (allocation only); every launch is a C ABI
 call on the current stream, so a whole step can be captured in a HIP graph.
@@ -90,6 +93,12 @@ class Stack:
                                          vp(*[o[1].data_ptr() for o in outs]), residual, st)
         self._ok(rc, "qlinear_m1")
 
+    def _m1_swiglu(self, pro, a, b, wg, wu, h, eps=0.0, st=None):
+        rc = self.L.viper_hip_qlinear_m1_swiglu(Q4, 0, 64, wg[3], pro, a, b, eps, None, wg[0].data_ptr(),
+                                                wg[1].data_ptr(), wu[0].data_ptr(), wu[1].data_ptr(), wg[2],
+                                                h.data_ptr(), None, None, st)
+        self._ok(rc, "qlinear_m1_swiglu")
+
     def step_fused(self):
         """One decode step, 4 launches per slot (producers folded, q/k/v together)."""
         torch, L = self.torch, self.L
@@ -103,8 +112,8 @@ class Stack:
                 wq, wk, wv, wo, wg, wu, wd = self.w[l]
                 self._m1(2, p(x), p(self.ln[2 * l]), [(wq, self.q), (wk, self.k), (wv, self.v)], eps=self.eps, st=st)
                 self._m1(0, p(self.attn), None, [(wo, x)], residual=p(x), st=st)
-                self._m1(2, p(x), p(self.ln[2 * l + 1]), [(wg, self.gt), (wu, self.ut)], eps=self.eps, st=st)
-                self._m1(3, p(self.gt), p(self.ut), [(wd, x)], residual=p(x), st=st)
+                self._m1_swiglu(2, p(x), p(self.ln[2 * l + 1]), wg, wu, self.gt, eps=self.eps, st=st)
+                self._m1(0, p(self.gt), None, [(wd, x)], residual=p(x), st=st)
         self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(self.final_ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
                                               p(self.xs), st), "final norm")
         self._ok(L.viper_hip_linear_bf16(p(self.head), p(self.xn), p(self.logits), 1, self.V, H, st), "lm_head")
