@@ -321,7 +321,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         if (seg) load_seg(seg);
         u32x4 A0[CPL], A1[CPL];
         u32x2 CS[CPL];
-        uint32_t SV[CPL];
+        float SC[CPL];  // ws * xs of the chunk's group (0 on the odd lane of a pair)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = seg * segw + j * TS + l;
@@ -330,8 +330,13 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             const u32x4* a = (const u32x4*)(lxq + (size_t)cc * FT::CK);
             A0[j] = a[0];
             A1[j] = FT::OFF ? a[1] : a[0];
-            SV[j] = sv[j];
-            if constexpr (EXACT) SV[j] = lead ? (uint32_t)lsc[rr * NGR + (c >> 1)] : 0u;
+            if constexpr (EXACT) {
+                // read on every lane (in bounds), select after: no branch, no
+                // wait between the LDS reads, product formed before the weights
+                const uint32_t sraw = lsc[rr * NGR + (c >> 1)];
+                const float wsf = SENC ? bf16f(sraw) : f16f(sraw);
+                SC[j] = (lead ? wsf : 0.0f) * __uint_as_float(CS[j].y);
+            }
         }
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
@@ -345,8 +350,10 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             const int g = cc >> 1;
             if constexpr (PART)
                 if (ok && lead && row_ok) part[(size_t)row * NGR + g] = dot;
-            const float wsf = SENC ? bf16f(SV[j]) : f16f(SV[j]);
-            acc = __builtin_fmaf(wsf * __uint_as_float(CS[j].y), (float)dot, acc);
+            float scj;
+            if constexpr (EXACT) scj = SC[j];
+            else scj = (SENC ? bf16f(sv[j]) : f16f(sv[j])) * __uint_as_float(CS[j].y);
+            acc = __builtin_fmaf(scj, (float)dot, acc);
         }
     }
     acc = team_sum<TS>(acc);
