@@ -122,6 +122,15 @@ def test_multi_row(torch_dev, qtype, M):
     run_case(torch_dev, qtype, 77, K, M, seed=2000 + M, residual=(M % 2 == 0))
 
 
+# M = 2..4 at long K: rows staged in all eight rounds of a 640-thread
+# workgroup (M * K / 8 = 5120 octets), and past that bound (the matrix-core
+# path takes the call).
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("M,K", [(2, 10240), (4, 10240), (3, 12288), (4, 16384)])
+def test_multi_row_long_k(torch_dev, qtype, M, K):
+    run_case(torch_dev, qtype, 45, K, M, seed=2100 + M + K, residual=(M == 4))
+
+
 # M = 2..16 run on the i8 matrix cores when K is a multiple of two groups:
 # one load segment per wave (K <= 40 groups per 4 waves), the double-buffered
 # loop (long K), two 16-row tiles per wave (N >= 64 tiles per CU), partial

@@ -37,6 +37,7 @@ namespace vq {
 // sums and, for exact tilings, the workgroup's block of weight scales.
 
 constexpr int M1_XS = 4;    // activation octets per thread loaded before the weights
+constexpr int M1_XS_MR = 8; // the same for MR > 1 rows (all of them: no later rounds)
 constexpr int M1_DELAY = 8; // weight-issue delay, s_sleep units
 
 // Kernel modes: plain, with the int32 group dots (test entry point), or the
@@ -59,8 +60,99 @@ __host__ __device__ constexpr size_t m1_scale_block(int rows, int ngr) {
 // swiglu epilogue's gate values (up to 32), the scale block of `rows` rows
 // (exact tilings).
 template <int F>
-__host__ __device__ constexpr size_t m1_lds_bytes(int K, int rows) {
-    return (size_t)K + (size_t)(K / Fmt<F>::CK) * 8 + 128 + m1_scale_block(rows, K / Fmt<F>::G);
+__host__ __device__ constexpr size_t m1_lds_bytes(int K, int rows, int mr = 1) {
+    return (size_t)mr * K + (size_t)mr * (K / Fmt<F>::CK) * 8 + 128 + m1_scale_block(rows, K / Fmt<F>::G);
+}
+
+// Shapes instantiated for MR > 1 activation rows (the workgroups that stage
+// MR rows hold 320 or 640 threads).
+__host__ __device__ constexpr bool m1_mr_shape_ok(int ts, int ntt, int cpl) {
+    return (ntt == 320 && ts == 16 && cpl == 5) || (ntt == 320 && ts == 8 && cpl == 10) ||
+           (ntt == 640 && cpl == 5 && ts >= 16) || (ntt == 640 && cpl == 10 && ts >= 16);
+}
+
+
+// Dot phase for MR > 1 activation rows: per chunk the weights are decoded
+// once (Q4: the sign flip for the high-nibble dot; Q5/Q6/W8: the int8 offset
+// codes) and dotted with each row's activation from LDS; per row one fp32
+// accumulator, one team reduction and one bf16 store (+ residual).
+template <int F, int TS, int CPL, int SENC, bool PART, bool EXACT, int MR, typename LoadSeg>
+__device__ __forceinline__ void m1_dots_rows(u32x4 (&wv)[CPL], uint32_t (&h0)[CPL], uint32_t (&h1)[CPL],
+                                             uint32_t (&sv)[CPL], LoadSeg& load_seg, const int8_t* lxq,
+                                             const u32x2* lcs, const uint16_t* lsc, int32_t* part,
+                                             const uint16_t* res, uint16_t* y, int M, int N, int K, int CPR,
+                                             int NGR, int segw, int nseg, int rr, int l, int row, bool row_ok,
+                                             bool lead) {
+    using FT = Fmt<F>;
+    float acc[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[m] = 0.0f;
+    for (int seg = 0; seg < nseg; ++seg) {
+        if (seg) load_seg(seg);
+        float WS[CPL];  // weight scale of the chunk's group (0 on the odd lane of a pair)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = seg * segw + j * TS + l;
+            uint32_t sraw = sv[j];
+            if constexpr (EXACT) sraw = lsc[rr * NGR + (c >> 1)];
+            const float wsf = SENC ? bf16f(sraw) : f16f(sraw);
+            WS[j] = (EXACT && !lead) ? 0.0f : wsf;
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = seg * segw + j * TS + l;
+            const bool ok = EXACT || c < CPR;
+            const int cc = EXACT ? c : min(c, CPR - 1);
+            const u32x4 p = wv[j];
+            u32x4 px = p;
+            uint32_t wd[8];
+            if constexpr (F == 4) px = u32x4{p.x ^ 0x88888888u, p.y ^ 0x88888888u, p.z ^ 0x88888888u, p.w ^ 0x88888888u};
+            else decode<F>(p, h0[j], h1[j], wd);
+            // every row's operands first (rows >= M read staged but unused LDS:
+            // no branch, so the reads overlap), then the dots
+            u32x2 cs[MR];
+            u32x4 a0[MR], a1[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                cs[m] = lcs[m * CPR + cc];
+                const u32x4* a = (const u32x4*)(lxq + (size_t)m * K + (size_t)cc * FT::CK);
+                a0[m] = a[0];
+                a1[m] = FT::OFF ? a[1] : a[0];
+            }
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                int dot;
+                if constexpr (F == 4) {
+                    dot = chunk_dot_q4x(p, px, a0[m], a1[m], (int)cs[m].x);
+                } else {
+                    dot = (int)cs[m].x;
+                    dot = sdot4(wd[0], a0[m].x, dot);
+                    dot = sdot4(wd[1], a0[m].y, dot);
+                    dot = sdot4(wd[2], a0[m].z, dot);
+                    dot = sdot4(wd[3], a0[m].w, dot);
+                    if constexpr (F != 8) {
+                        dot = sdot4(wd[4], a1[m].x, dot);
+                        dot = sdot4(wd[5], a1[m].y, dot);
+                        dot = sdot4(wd[6], a1[m].z, dot);
+                        dot = sdot4(wd[7], a1[m].w, dot);
+                    }
+                }
+                dot += dpp_i<DPP_SWAP1>(dot);
+                if constexpr (PART)
+                    if (m < M && ok && lead && row_ok) part[((size_t)m * N + row) * NGR + (cc >> 1)] = dot;
+                acc[m] = __builtin_fmaf(WS[j] * __uint_as_float(cs[m].y), (float)dot, acc[m]);
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        float v = team_sum<TS>(acc[m]);
+        if (m < M && l == 0 && row_ok) {
+            const size_t o = (size_t)m * N + row;
+            if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
+            y[o] = f2bf(v);
+        }
+    }
 }
 
 // EXACT: every lane's chunks lie inside its row (the row has exactly TS * CPL
@@ -76,7 +168,11 @@ __host__ __device__ constexpr size_t m1_lds_bytes(int K, int rows) {
 // xa: PRO_INT8 the group scales, PRO_RMSNORM gamma, PRO_SWIGLU up.
 // xout (PRO_RMSNORM, may be null): the bf16 normalized row, written by the
 // first workgroup.
-template <int F, int TS, int NTT, int CPL, int SENC, int MODE, bool EXACT, int PRO, int DELAY>
+// MR > 1 (PRO_BF16 / PRO_INT8, one matrix): M = e1 <= MR activation rows
+// (x [M][K], y and the residual [M][N]); every workgroup stages all M rows,
+// each lane decodes its weight chunk once and dots it with every row.  Small
+// verify batches then need no separate quantize launch.
+template <int F, int TS, int NTT, int CPL, int SENC, int MODE, bool EXACT, int PRO, int MR, int DELAY>
 __global__ void __launch_bounds__(NTT)
 qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* y0, int K, int n0, int e0,
                 int e1, const uint16_t* res, const void* xa, float eps, uint16_t* __restrict__ xout,
@@ -87,30 +183,38 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     constexpr bool SWI = MODE == M1_SWIGLU;
     constexpr bool PRE = PRO == PRO_INT8;
     constexpr bool TWO = PRO == PRO_RMSNORM || PRO == PRO_SWIGLU;  // two bf16 inputs
-    constexpr int XS = M1_XS;
+    constexpr int XS = MR == 1 ? M1_XS : M1_XS_MR;
     constexpr int ROWS = NTT / TS;
+    const int M = MR == 1 ? 1 : e1;  // activation rows
     constexpr int HB = FT::HIW * 4;  // high-plane bytes per chunk: Q5 4, Q6 8
     constexpr int OPC = FT::CK / 8;  // octets per chunk (4, or 2 for W8)
     extern __shared__ __align__(16) uint8_t smem[];
     const int CPR = K / FT::CK;      // chunks per row
     const int NGR = K / FT::G;       // groups per row
-    int8_t* lxq = (int8_t*)smem;
-    u32x2* lcs = (u32x2*)(smem + K);
-    float* lred = (float*)(smem + K + (size_t)CPR * 8);
-    uint16_t* lepi = (uint16_t*)(smem + K + (size_t)CPR * 8 + 64);
-    uint16_t* lsc = (uint16_t*)(smem + K + (size_t)CPR * 8 + 128);
+    const size_t lact = (size_t)MR * K + (size_t)MR * CPR * 8;  // activation rows and their records
+    int8_t* lxq = (int8_t*)smem;                                  // [MR][K]
+    u32x2* lcs = (u32x2*)(smem + (size_t)MR * K);                // [MR][CPR]
+    float* lred = (float*)(smem + lact);
+    uint16_t* lepi = (uint16_t*)(smem + lact + 64);
+    uint16_t* lsc = (uint16_t*)(smem + lact + 128);
 
     const int tid = (int)threadIdx.x;
     const int l = tid % TS;
     const int rr = tid / TS;  // row within the workgroup
     // matrix of this workgroup (matrix 0's arguments lead the argument list,
-    // so its workgroups need nothing beyond the preloaded arguments)
+    // so its workgroups need nothing beyond the preloaded arguments).  The
+    // rare paths of the kernel (other matrices, the residual, activation
+    // rounds past the first XS) are marked unlikely: the compiler then lays
+    // the common path out straight and schedules it on its own, which takes
+    // 0.05 us off the north-star launch; MR > 1 launches are single-matrix and
+    // stage their rows in XS rounds, so those paths are not compiled there
+    // (0.5 us of an M = 2 launch).
     int bid = (int)blockIdx.x;
     const uint8_t* w = w0;
     const uint16_t* ws = s0;
     uint16_t* y = y0;
     int N = n0;
-    if (bid >= e0) {
+    if (MR == 1 && __builtin_expect(bid >= e0, 0)) {
         res = nullptr;
         if (bid >= e1) {
             bid -= e1;
@@ -148,10 +252,10 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
 
     // 1. activation octets, then every weight byte and group scale of the
     //    first row segment, all in flight at once
-    const int noct = K / 8;
+    const int noct = M * (K / 8);  // octets of all rows (rows follow each other)
     constexpr int OPG = FT::G / 8;   // octets per group
-    const auto xr = buf(x, (uint32_t)K * (PRE ? 1 : 2));
-    const auto xsr = buf(xa, PRE ? (uint32_t)(K / FT::G) * 4 : TWO ? (uint32_t)K * 2 : 0u);
+    const auto xr = buf(x, (uint32_t)(M * K) * (PRE ? 1 : 2));
+    const auto xsr = buf(xa, PRE ? (uint32_t)(M * (K / FT::G)) * 4 : TWO ? (uint32_t)K * 2 : 0u);
     // bf16 octet, or {int8 octet, int8 octet, group scale of a chunk's first octet}
     auto load_x = [&](int o) -> u32x4 {
         if constexpr (PRE) {
@@ -305,17 +409,23 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             }
         }
     }
-    if constexpr (!TWO) {
-        for (int i = XS; i < xiters; ++i)
-            if (wave0 + NTT * i < noct) quant_store(tid + NTT * i, load_x(tid + NTT * i));
+    if constexpr (!TWO && MR == 1) {
+        if (__builtin_expect(xiters > XS, 0))
+            for (int i = XS; i < xiters; ++i)
+                if (wave0 + NTT * i < noct) quant_store(tid + NTT * i, load_x(tid + NTT * i));
     }
 
     lds_barrier();
 
-    // 3. chunk dots, group sums, fp32 combine.  Every LDS operand of the
+    // 3. chunk dots, group sums, fp32 combine (MR > 1: the loop after this one).  Every LDS operand of the
     //    segment is read before the first dot: the reads then overlap the
     //    wait for the weights instead of sitting between the dots (0.3 us of
     //    the north-star dispatch).  Each chunk waits only for its own weights.
+    if constexpr (MR > 1) {
+        m1_dots_rows<F, TS, CPL, SENC, PART, EXACT, MR>(wv, h0, h1, sv, load_seg, lxq, lcs, lsc, part, res, y, M, N,
+                                                         K, CPR, NGR, segw, nseg, rr, l, row, row_ok, lead);
+        return;
+    }
     float acc = 0.0f;
     for (int seg = 0; seg < nseg; ++seg) {
         if (seg) load_seg(seg);
@@ -373,7 +483,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         if (up && l == 0 && row_ok) y2[row] = f2bf(silu_mul(bf16f(lepi[rt]), bf16f(vb)));
     } else {
         if (l == 0 && row_ok) {
-            if (res != nullptr) acc += bf16f(res[row]);
+            if (__builtin_expect(res != nullptr, 0)) acc += bf16f(res[row]);
             y[row] = f2bf(acc);
         }
     }
@@ -389,12 +499,12 @@ constexpr int M1_SHAPES[][3] = {{8, 128, 10}, {8, 192, 10}, {8, 320, 10}, {16, 2
                                 {32, 320, 10}, {32, 640, 10}, {64, 640, 10}, {16, 256, 5}, {16, 320, 5},
                                 {16, 640, 5}, {32, 640, 5}, {64, 640, 5}};
 
-template <int F, int SENC, int MODE, bool EXACT, int PRO>
+template <int F, int SENC, int MODE, bool EXACT, int PRO, int MR>
 m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
-#define VQ_M1(TS_, NTT_, CPL_)                                                       \
-    if constexpr (MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_))                        \
-        if (ts == TS_ && ntt == NTT_ && cpl == CPL_)                                 \
-            return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, M1_DELAY>;
+#define VQ_M1(TS_, NTT_, CPL_)                                                                      \
+    if constexpr ((MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_)) && (MR == 1 || m1_mr_shape_ok(TS_, NTT_, CPL_))) \
+        if (ts == TS_ && ntt == NTT_ && cpl == CPL_)                                                \
+            return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, MR, M1_DELAY>;
     VQ_M1(8, 128, 10) VQ_M1(8, 192, 10) VQ_M1(8, 320, 10) VQ_M1(16, 256, 10) VQ_M1(16, 640, 10)
     VQ_M1(32, 320, 10) VQ_M1(32, 640, 10) VQ_M1(64, 640, 10) VQ_M1(16, 256, 5) VQ_M1(16, 320, 5)
     VQ_M1(16, 640, 5) VQ_M1(32, 640, 5) VQ_M1(64, 640, 5)
@@ -402,40 +512,55 @@ m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
     return nullptr;
 }
 
-template <int F, int PRO, int MODE>
+template <int F, int PRO, int MODE, int MR>
 m1_fn m1_pick_mode(int ts, int ntt, int cpl, int senc, bool exact) {
-    if (exact) return senc ? m1_kernel_v<F, 1, MODE, true, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 0, MODE, true, PRO>(ts, ntt, cpl);
-    return senc ? m1_kernel_v<F, 1, MODE, false, PRO>(ts, ntt, cpl) : m1_kernel_v<F, 0, MODE, false, PRO>(ts, ntt, cpl);
+    if (exact)
+        return senc ? m1_kernel_v<F, 1, MODE, true, PRO, MR>(ts, ntt, cpl) : m1_kernel_v<F, 0, MODE, true, PRO, MR>(ts, ntt, cpl);
+    return senc ? m1_kernel_v<F, 1, MODE, false, PRO, MR>(ts, ntt, cpl) : m1_kernel_v<F, 0, MODE, false, PRO, MR>(ts, ntt, cpl);
 }
 // The swiglu pair is built for the BF16 and RMSNORM prologues (the inputs of
-// the engine's gate/up projection).
+// the engine's gate/up projection); MR > 1 rows for BF16 and INT8, plain or
+// with partials.
 template <int F, int PRO>
-m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, int mode, bool exact) {
-    if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART>(ts, ntt, cpl, senc, exact);
+m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, int mode, bool exact, int mr) {
+    if constexpr (PRO == PRO_BF16 || PRO == PRO_INT8) {
+        if (mr == 2) {
+            if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 2>(ts, ntt, cpl, senc, exact);
+            if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 2>(ts, ntt, cpl, senc, exact);
+            return nullptr;
+        }
+        if (mr == 4) {
+            if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 4>(ts, ntt, cpl, senc, exact);
+            if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 4>(ts, ntt, cpl, senc, exact);
+            return nullptr;
+        }
+    }
+    if (mr != 1) return nullptr;
+    if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 1>(ts, ntt, cpl, senc, exact);
     if constexpr (PRO == PRO_BF16 || PRO == PRO_RMSNORM)
-        if (mode == M1_SWIGLU) return m1_pick_mode<F, PRO, M1_SWIGLU>(ts, ntt, cpl, senc, exact);
-    if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN>(ts, ntt, cpl, senc, exact);
+        if (mode == M1_SWIGLU) return m1_pick_mode<F, PRO, M1_SWIGLU, 1>(ts, ntt, cpl, senc, exact);
+    if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 1>(ts, ntt, cpl, senc, exact);
     return nullptr;
 }
 
 // Kernels of format F with the quantize / int8 prologues and with the folded
 // rmsnorm / swiglu prologues (each defined in its own translation unit).
 template <int F>
-m1_fn m1_pick_plain(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro);
+m1_fn m1_pick_plain(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro, int mr);
 template <int F>
-m1_fn m1_pick_folded(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro);
+m1_fn m1_pick_folded(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro, int mr);
 
-#define VQ_M1_PLAIN(F)                                                                         \
-    template <>                                                                                \
-    m1_fn m1_pick_plain<F>(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro) { \
-        return pro == PRO_INT8 ? m1_pick_pro<F, PRO_INT8>(ts, ntt, cpl, senc, mode, exact)       \
-                               : m1_pick_pro<F, PRO_BF16>(ts, ntt, cpl, senc, mode, exact);      \
+#define VQ_M1_PLAIN(F)                                                                                 \
+    template <>                                                                                        \
+    m1_fn m1_pick_plain<F>(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro, int mr) { \
+        return pro == PRO_INT8 ? m1_pick_pro<F, PRO_INT8>(ts, ntt, cpl, senc, mode, exact, mr)           \
+                               : m1_pick_pro<F, PRO_BF16>(ts, ntt, cpl, senc, mode, exact, mr);          \
     }
-#define VQ_M1_FOLDED(F)                                                                        \
-    template <>                                                                                \
-    m1_fn m1_pick_folded<F>(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro) { \
-        return pro == PRO_SWIGLU ? m1_pick_pro<F, PRO_SWIGLU>(ts, ntt, cpl, senc, mode, exact)     \
-                                 : m1_pick_pro<F, PRO_RMSNORM>(ts, ntt, cpl, senc, mode, exact);   \
+#define VQ_M1_FOLDED(F)                                                                                \
+    template <>                                                                                        \
+    m1_fn m1_pick_folded<F>(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro, int mr) { \
+        return pro == PRO_SWIGLU ? m1_pick_pro<F, PRO_SWIGLU>(ts, ntt, cpl, senc, mode, exact, mr)         \
+                                 : m1_pick_pro<F, PRO_RMSNORM>(ts, ntt, cpl, senc, mode, exact, mr);       \
     }
 
 }  // namespace vq

@@ -7,22 +7,22 @@ struct M1Shape {
     int ts, ntt, cpl;
 };
 
-static m1_fn m1_kernel(int qtype, const M1Shape& sh, int senc, int mode, bool exact, int pro) {
+static m1_fn m1_kernel(int qtype, const M1Shape& sh, int senc, int mode, bool exact, int pro, int mr = 1) {
     const bool folded = pro == PRO_RMSNORM || pro == PRO_SWIGLU;
     const int ts = sh.ts, ntt = sh.ntt, cpl = sh.cpl;
     switch (qtype) {
         case VIPER_QTYPE_Q4_G64:
-            return folded ? m1_pick_folded<4>(ts, ntt, cpl, senc, mode, exact, pro)
-                          : m1_pick_plain<4>(ts, ntt, cpl, senc, mode, exact, pro);
+            return folded ? m1_pick_folded<4>(ts, ntt, cpl, senc, mode, exact, pro, mr)
+                          : m1_pick_plain<4>(ts, ntt, cpl, senc, mode, exact, pro, mr);
         case VIPER_QTYPE_Q5_G64:
-            return folded ? m1_pick_folded<5>(ts, ntt, cpl, senc, mode, exact, pro)
-                          : m1_pick_plain<5>(ts, ntt, cpl, senc, mode, exact, pro);
+            return folded ? m1_pick_folded<5>(ts, ntt, cpl, senc, mode, exact, pro, mr)
+                          : m1_pick_plain<5>(ts, ntt, cpl, senc, mode, exact, pro, mr);
         case VIPER_QTYPE_Q6_G64:
-            return folded ? m1_pick_folded<6>(ts, ntt, cpl, senc, mode, exact, pro)
-                          : m1_pick_plain<6>(ts, ntt, cpl, senc, mode, exact, pro);
+            return folded ? m1_pick_folded<6>(ts, ntt, cpl, senc, mode, exact, pro, mr)
+                          : m1_pick_plain<6>(ts, ntt, cpl, senc, mode, exact, pro, mr);
         default:
-            return folded ? m1_pick_folded<8>(ts, ntt, cpl, senc, mode, exact, pro)
-                          : m1_pick_plain<8>(ts, ntt, cpl, senc, mode, exact, pro);
+            return folded ? m1_pick_folded<8>(ts, ntt, cpl, senc, mode, exact, pro, mr)
+                          : m1_pick_plain<8>(ts, ntt, cpl, senc, mode, exact, pro, mr);
     }
 }
 
@@ -46,18 +46,30 @@ static long m1_load(const M1Shape& sh, int N, int cus, bool pair = false) {
 // the smallest team covering a row in 10 slots per lane (longer rows loop over
 // segments of 64 lanes), workgroup size by row load, ties to more rows per
 // workgroup (fewer redundant activation quantizations).
-static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct, bool pair = false) {
+// MR > 1 rows: only the shapes m1_mr_shape_ok instantiates, with every row
+// staged in M1_XS_MR rounds; there a workgroup that stages the rows in at
+// most two rounds is taken first (the rows' quantize is repeated by every
+// workgroup, so fewer, larger workgroups do less of it: 4 rows at K = 2560,
+// 6.7 us with 640 threads against 7.4 us with 320), and the one-round
+// preference does not apply (2 rows: 5.04 us with 320 threads, 5.03 us with
+// 640).
+static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct, bool pair = false, int mr = 1) {
     M1Shape best{0, 0, 0};
     long best_load = -1;
+    auto extra = [&](const M1Shape& c) { const int r = (noct + c.ntt - 1) / c.ntt; return r > 2 ? r - 2 : 0; };
     for (const auto& s : M1_SHAPES) {
         const M1Shape c{s[0], s[1], s[2]};
         if (c.ntt < min_ntt || c.ts * c.cpl != cpr || (pair && !m1_pair_ok(c.ts, c.ntt))) continue;
+        if (mr > 1 && !m1_mr_shape_ok(c.ts, c.ntt, c.cpl)) continue;
         const long load = m1_load(c, N, cus, pair);
-        const bool one = c.ntt >= noct, best_one = best.ntt >= noct;
+        const bool one = mr == 1 && c.ntt >= noct, best_one = mr == 1 && best.ntt >= noct;
+        const int xr = extra(c), bxr = best.ntt ? extra(best) : 0;
         const bool take = best_load < 0 || load < best_load ||
                           (load == best_load &&
-                           (one > best_one ||
-                            (one == best_one && (c.cpl < best.cpl || (c.cpl == best.cpl && c.ntt < best.ntt)))));
+                           (xr < bxr ||
+                            (xr == bxr &&
+                             (one > best_one ||
+                              (one == best_one && (c.cpl < best.cpl || (c.cpl == best.cpl && c.ntt < best.ntt)))))));
         if (take) {
             best = c;
             best_load = load;
@@ -69,6 +81,7 @@ static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct, bool pai
     for (const auto& s : M1_SHAPES) {
         const M1Shape c{s[0], s[1], s[2]};
         if (c.ts != ts || c.cpl != 10 || c.ntt < min_ntt || (pair && !m1_pair_ok(c.ts, c.ntt))) continue;
+        if (mr > 1 && !m1_mr_shape_ok(c.ts, c.ntt, c.cpl)) continue;
         const long load = m1_load(c, N, cus, pair);
         if (best_load < 0 || load < best_load || (load == best_load && c.ntt > best.ntt)) {
             best = c;
@@ -90,14 +103,26 @@ size_t lds_m1(int qtype, int K) {
     }
 }
 
-static size_t lds_m1_launch(int qtype, int K, int rows, bool exact) {
+static size_t lds_m1_launch(int qtype, int K, int rows, bool exact, int mr = 1) {
     const int r = exact ? rows : 0;
     switch (qtype) {
-        case VIPER_QTYPE_Q4_G64: return m1_lds_bytes<4>(K, r);
-        case VIPER_QTYPE_Q5_G64: return m1_lds_bytes<5>(K, r);
-        case VIPER_QTYPE_Q6_G64: return m1_lds_bytes<6>(K, r);
-        default: return m1_lds_bytes<8>(K, r);
+        case VIPER_QTYPE_Q4_G64: return m1_lds_bytes<4>(K, r, mr);
+        case VIPER_QTYPE_Q5_G64: return m1_lds_bytes<5>(K, r, mr);
+        case VIPER_QTYPE_Q6_G64: return m1_lds_bytes<6>(K, r, mr);
+        default: return m1_lds_bytes<8>(K, r, mr);
     }
+}
+
+static int m1_mr(int M) { return M <= 1 ? 1 : (M == 2 ? 2 : 4); }
+
+bool m1_rows_ok(int qtype, int K, int M) {
+    // every row is staged in the first M1_XS_MR rounds of the workgroup, and
+    // some multi-row shape tiles the row (the shape does not depend on N)
+    if (M < 2 || M > 4 || (long)M * (K / 8) > (long)M1_XS_MR * 640) return false;
+    const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32, noct = M * (K / 8);
+    const M1Shape sh = m1_shape(K / ck, 1 << 14, device_cus(), (noct + M1_XS_MR - 1) / M1_XS_MR, noct, false, m1_mr(M));
+    constexpr int kBlockMax = 640 * 10;
+    return sh.ntt != 0 && lds_m1_launch(qtype, K, 0, false, m1_mr(M)) + kBlockMax <= (size_t)LDS_MAX;
 }
 
 bool m1_folded_ok(int qtype, int K, int N) {
@@ -109,8 +134,11 @@ bool m1_folded_ok(int qtype, int K, int N) {
 
 int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
               const M1Out* outs, int nouts, const void* res, int32_t* part, hipStream_t st,
-              hipEvent_t ev0, hipEvent_t ev1) {
+              hipEvent_t ev0, hipEvent_t ev1, int M) {
     if (nouts < 1 || nouts > 3) return VIPER_INVALID_ARGUMENT;
+    const int mr = m1_mr(M);
+    if (mr > 1 && (nouts != 1 || (pro != PRO_BF16 && pro != PRO_INT8) || !m1_rows_ok(qtype, K, M)))
+        return VIPER_INVALID_ARGUMENT;
     const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32;
     const bool folded = pro == PRO_RMSNORM || pro == PRO_SWIGLU;
     int ntot = 0;
@@ -119,18 +147,21 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     // fastest with one octet per thread (rmsnorm's row sum and swiglu's
     // element work are then a single pass): take such a workgroup when an
     // exact tiling allows it, even at a higher row load.
-    const int noct = K / 8;
+    const int noct = M * (K / 8);
     const int cus = device_cus();
     M1Shape sh{0, 0, 0};
     if (folded) sh = m1_shape(K / ck, ntot, cus, noct < 640 ? noct : 640, noct);
-    if (sh.ntt == 0) sh = m1_shape(K / ck, ntot, cus, folded ? (noct + M1_XS - 1) / M1_XS : 0, noct);
+    if (sh.ntt == 0) {
+        const int min_ntt = mr > 1 ? (noct + M1_XS_MR - 1) / M1_XS_MR : folded ? (noct + M1_XS - 1) / M1_XS : 0;
+        sh = m1_shape(K / ck, ntot, cus, min_ntt, noct, false, mr);
+    }
     if (sh.ntt == 0) return VIPER_INVALID_ARGUMENT;
     const int group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
     const bool exact = (K / ck) == sh.ts * sh.cpl && (K / group) % 8 == 0;
-    const m1_fn fn = m1_kernel(qtype, sh, senc, part != nullptr ? M1_PART : M1_PLAIN, exact, pro);
+    const m1_fn fn = m1_kernel(qtype, sh, senc, part != nullptr ? M1_PART : M1_PLAIN, exact, pro, mr);
     if (fn == nullptr) return VIPER_INTERNAL;
     const int rows = sh.ntt / sh.ts;
-    const size_t lds = lds_m1_launch(qtype, K, rows, exact);
+    const size_t lds = lds_m1_launch(qtype, K, rows, exact, mr);
     if (lds > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
     int nb[3] = {0, 0, 0};
     for (int i = 0; i < nouts; ++i) nb[i] = (outs[i].n + rows - 1) / rows;
@@ -140,6 +171,7 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     uint16_t *y0 = (uint16_t*)o0.y, *y1 = (uint16_t*)o1.y, *y2 = (uint16_t*)o2.y;
     int n0 = o0.n, n1 = o1.n, n2 = o2.n;
     int e0 = nb[0], e1 = nb[0] + nb[1];
+    if (mr > 1) e1 = M;  // one matrix: e1 carries the activation rows
     const unsigned grid = (unsigned)(nb[0] + nb[1] + nb[2]);
     const uint16_t* r = (const uint16_t*)res;
     void* args[] = {&x, &w0, &s0, &y0, &K, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,

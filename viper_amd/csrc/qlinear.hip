@@ -197,6 +197,12 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     }
     const size_t need = workspace_need(qtype, K, M);
     if (wsp == nullptr || wsp_bytes < need || misaligned(wsp, 16)) return VIPER_INVALID_ARGUMENT;
+    // 2..4 rows of one matrix: every workgroup quantizes the rows itself, one
+    // launch (the workspace stays required for M > 1 whichever kernel runs)
+    if (b.w == nullptr && m1_rows_ok(qtype, K, M)) {
+        const M1Out outs[1] = {{w, s, y, N}};
+        return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, ev0, ev1, M);
+    }
     const bool mf = mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s));
     const bool staged = mf && mfma_staged(qtype, N, K);
     if (!mf && lds_pre(qtype, M, K) > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
@@ -228,6 +234,11 @@ static int prequant_common(int qtype, const void* w, const void* s, int senc, in
         const M1Out outs[2] = {{w, s, y, N}, {b.w, b.s, b.y, N}};
         return launch_m1(qtype, senc, K, PRO_INT8, xq, xs, 0.0f, nullptr, outs, b.w ? 2 : 1, res, nullptr, st,
                          nullptr, nullptr);
+    }
+    if (b.w == nullptr && m1_rows_ok(qtype, K, M)) {
+        const M1Out outs[1] = {{w, s, y, N}};
+        return launch_m1(qtype, senc, K, PRO_INT8, xq, xs, 0.0f, nullptr, outs, 1, res, nullptr, st, nullptr,
+                         nullptr, M);
     }
     if (mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s)))
         return launch_mfma(qtype, w, s, senc, N, K, xq, xs, true, M, y, res, nullptr, b.w, b.s, b.y, st,

@@ -248,6 +248,23 @@ __device__ __forceinline__ int chunk_dot_q4(const u32x4& p, const u32x4& a0, con
     return (int)((uint32_t)hi * 16u + lo);
 }
 
+// chunk_dot_q4 with the sign-flipped words px = p ^ 0x88888888 computed once
+// by the caller (shared by the activation rows of a multi-row dot).
+__device__ __forceinline__ int chunk_dot_q4x(const u32x4& p, const u32x4& px, const u32x4& a0, const u32x4& a1,
+                                             int corr) {
+    uint32_t lo = (uint32_t)corr;
+    int hi = 0;
+    lo = udot8(p.x, a0.x, lo);
+    hi = sdot8(px.x, a0.y, hi);
+    lo = udot8(p.y, a0.z, lo);
+    hi = sdot8(px.y, a0.w, hi);
+    lo = udot8(p.z, a1.x, lo);
+    hi = sdot8(px.z, a1.y, hi);
+    lo = udot8(p.w, a1.z, lo);
+    hi = sdot8(px.w, a1.w, hi);
+    return (int)((uint32_t)hi * 16u + lo);
+}
+
 // Raw buffer loads: the resource's byte range bounds every access, and an
 // out-of-range lane reads 0 without touching memory, so the kernel issues
 // all its loads unconditionally and the compiler counts them exactly.

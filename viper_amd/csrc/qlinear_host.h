@@ -85,9 +85,12 @@ struct M1Out {
 };
 size_t lds_m1(int qtype, int K);
 bool m1_folded_ok(int qtype, int K, int N);
+// M (1..4) activation rows: M > 1 needs one matrix, PRO_BF16 or PRO_INT8 and
+// m1_rows_ok (x, y, res and part hold M rows).
 int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
               const M1Out* outs, int nouts, const void* res, int32_t* part, hipStream_t st,
-              hipEvent_t ev0, hipEvent_t ev1);
+              hipEvent_t ev0, hipEvent_t ev1, int M = 1);
+bool m1_rows_ok(int qtype, int K, int M);
 // M = 1 gate/up pair (one shape) with the swiglu epilogue: h = bf16(silu(g)
 // * u) from the bf16-rounded outputs; g_out / u_out may be null.  Prologue
 // PRO_BF16 or PRO_RMSNORM.
