@@ -226,6 +226,31 @@ def test_row_matches_single_row_call(torch_dev):
         np.testing.assert_array_equal(p1.cpu().numpy()[0], pm.cpu().numpy()[m])
 
 
+# M = 3..8 from bf16 x: every workgroup quantizes the rows into LDS and runs the
+# matrix-core kernel the prequantized entry runs on the workspace layout, with
+# the same quantize arithmetic and summation order, so at M = 5..8 (where the
+# prequantized entry takes that kernel too) the outputs are bit-identical.
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("N,K,M", [(1000, 2560, 5), (2100, 2560, 8), (64, 4096, 6), (10240, 2560, 7)])
+def test_bf16_rows_match_prequantized(torch_dev, qtype, N, K, M):
+    torch = torch_dev
+    G = O.group_size(qtype)
+    packed, scales = O.gen_weights(qtype, N, K, 60 + M, O.SCALE_BF16)
+    x = O.gen_act(M, K, 61 + M, outlier_frac=0.05, outlier_mul=20.0)
+    res = O.gen_act(M, N, 62 + M)
+    xq, xs = O.quantize_act(x, G)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, va.ScaleEnc.BF16)
+    ws = torch.zeros(va.workspace_bytes(qtype, N, K, M), dtype=torch.uint8, device="cuda")
+    ya = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    yb = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    assert va.linear(w, dev(torch, x), ya, residual=dev(torch, res), workspace=ws).ok()
+    assert va.linear_prequantized(w, dev(torch, xq), dev(torch, xs), yb, residual=dev(torch, res)).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(ya, np.uint16), host(yb, np.uint16))
+    y_ref, _, absterm = O.qlinear(qtype, packed, scales, O.SCALE_BF16, N, K, x, residual=res)
+    O.assert_bf16_close(host(ya, np.uint16), y_ref, absterm, rel=REL_TOL)
+
+
 @pytest.mark.parametrize("N,K,M", [(200, 2560, 3), (70, 10240, 16), (40, 192, 2), (6001, 4096, 16)])
 def test_prequantized_entry(torch_dev, N, K, M):
     # activations in viper_hip_quantize_act's layout ([M][K] int8, [M][K/G] fp32)
@@ -266,7 +291,7 @@ def test_prequantized_m1(torch_dev, qtype, N, K):
 # fused2 for k/v and gate/up): M = 1 (fused quantize), M > 1 (matrix cores),
 # K with an odd group count (two v_dot4 launches).
 @pytest.mark.parametrize("qtype", FORMATS)
-@pytest.mark.parametrize("N,K,M", [(300, 2560, 1), (70, 2560, 16), (33, 192, 3)])
+@pytest.mark.parametrize("N,K,M", [(300, 2560, 1), (70, 2560, 16), (90, 2560, 6), (33, 192, 3)])
 @pytest.mark.parametrize("prequantized", [False, True])
 def test_fused2(torch_dev, qtype, N, K, M, prequantized):
     torch = torch_dev

@@ -398,7 +398,8 @@ int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K,
                 hipEvent_t ev1) {
     if (!mfma_ok(qtype, K, M, s)) return VIPER_INTERNAL;
     if (rc_ok(qtype, K))
-        return launch_rc(qtype, w, s, senc, N, K, xq, xs, xnat, M, y, res, part, w1, s1, y1, st, ev0, ev1);
+        return launch_rc(qtype, w, s, senc, N, K, xq, xs, xnat ? RC_NAT : RC_FRAG, M, y, res, part, w1, s1, y1, st,
+                         ev0, ev1);
     const int NG = K / group_of(qtype);
     const int NP = NG / 2;
     const MfShape sh = mf_shape(N, NP, device_cus());

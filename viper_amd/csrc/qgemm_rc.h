@@ -39,6 +39,17 @@
 // through LDS, so results do not depend on timing.  Two matrices of one shape
 // may share a launch (fused pair): workgroups [0, nb0) use (w, ws, y), the
 // rest (w1, ws1, y1).
+//
+// Activation modes (AM): RC_FRAG reads the fragments and [group][16] scales
+// the fragment quantize wrote; RC_NAT gathers them from the natural layout
+// ([M][K] int8, [M][K/G] fp32); RC_BF16 takes the bf16 rows themselves: every
+// workgroup issues its share of the M rows' octets before the weight stream,
+// quantizes them while the weights are in flight into an LDS copy of the
+// fragment layout (the fragment quantize's arithmetic: group max over the
+// G/8 lanes of a group, the exact RNE quotient) and reads its operands from
+// there after one LDS barrier.  That needs no quantize launch and no
+// workspace traffic; it pays when few rows leave most of the lanes' quantize
+// work useful (every workgroup repeats it).
 #pragma once
 
 #include "qlinear_host.h"
@@ -54,11 +65,15 @@ template <> struct RcFmt<6> { static constexpr int QB = 16, HQ = 64, HSTR = 72, 
 template <> struct RcFmt<8> { static constexpr int QB = 8, HQ = 0, HSTR = 0, OFF = 0; };
 
 constexpr int RC_LSTR = 136;  // main-plane transpose row stride (bytes): 128 + 8 spreads banks
+constexpr int RC_XR = 8;      // RC_BF16: octets per thread held in registers (all rows in one pass)
 
 __host__ __device__ constexpr size_t rc_wave_lds(int hstr) { return (size_t)16 * (RC_LSTR + hstr); }
 __host__ __device__ constexpr size_t rc_lds_bytes(int hstr, int RB, int W) {
     return (size_t)W * rc_wave_lds(hstr) + (size_t)W * ((RB + 1) / 2) * 4 * 64 * 4;
 }
+// RC_BF16: the LDS copy of the fragments (64 lanes x QB bytes per group) and
+// of the [group][16] activation scales, after the regions above.
+__host__ __device__ constexpr size_t rc_act_lds_bytes(int qb, int ng) { return (size_t)ng * 64 * qb + (size_t)ng * 64; }
 
 template <int F, int RB, int QW>
 struct RcSeg {
@@ -70,7 +85,7 @@ struct RcSeg {
 };
 
 // ONE: the quads of every wave fit one load segment.
-template <int F, int RB, int W, int QW, bool ONE, bool XNAT, bool PART>
+template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART>
 __global__ void __launch_bounds__(64 * W)
 qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
                 int M, int N, int nb0, int senc, const uint16_t* res, int32_t* __restrict__ part,
@@ -78,6 +93,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     using FM = RcFmt<F>;
     using Seg = RcSeg<F, RB, QW>;
     constexpr int T = Seg::T;
+    constexpr bool XNAT = AM == RC_NAT, XBF = AM == RC_BF16;
     constexpr int G = F == 8 ? 32 : 64;
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = (int)threadIdx.x, L = tid & 63, wave = tid >> 6;
@@ -99,9 +115,25 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     const auto wr = buf(w + (size_t)row0 * rbytes, (uint32_t)(nrows * rbytes));
     const auto hr = buf(w + (size_t)N * rbytes + (size_t)row0 * hrb, (uint32_t)(nrows * hrb));
     const auto sr = buf(ws + (size_t)row0 * NG, (uint32_t)(nrows * NG * 2));
-    const auto xr = buf(xq, XNAT ? (uint32_t)(M * K) : (uint32_t)NG * 64 * FM::QB);
-    const auto xsr = buf(xs, XNAT ? (uint32_t)(M * NG * 4) : (uint32_t)NG * 64);
+    const auto xr = buf(xq, XNAT ? (uint32_t)(M * K) : XBF ? (uint32_t)(M * K) * 2 : (uint32_t)NG * 64 * FM::QB);
+    const auto xsr = buf(xs, XNAT ? (uint32_t)(M * NG * 4) : XBF ? 0u : (uint32_t)NG * 64);
     const bool m_ok = n16 < M;  // A row of this lane
+    // RC_BF16: the LDS fragments and scales (after the transpose buffers and
+    // the cross-wave sums)
+    int8_t* lxq = (int8_t*)(smem + rc_lds_bytes(FM::HSTR, RB, W));
+    float* lxs = (float*)(lxq + (size_t)NG * 64 * FM::QB);
+    constexpr int NTT = 64 * W;
+    const int KO = K / 8, noct = M * KO;  // RC_BF16: octets of all rows
+    u32x4 xv[XBF ? RC_XR : 1];
+    if constexpr (XBF) {
+        // every octet this thread quantizes, before any weight request
+#pragma unroll
+        for (int i = 0; i < RC_XR; ++i) {
+            xv[i] = u32x4{0u, 0u, 0u, 0u};
+            if (i == 0 || NTT * i < noct) xv[i] = bload16(xr, (tid + NTT * i) * 16);
+        }
+        issue_fence();
+    }
 
     auto load = [&](Seg& S, int seg) {
 #pragma unroll
@@ -109,7 +141,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
             const int Q = wave + W * (seg * QW + j);
             const bool ok = Q < NQ;
 #pragma unroll
-            for (int h = 0; h < 4; ++h) {
+            for (int h = 0; h < 4 && !XBF; ++h) {
                 const int g = 4 * Q + h;
                 int ao;
                 if constexpr (XNAT) ao = (ok && m_ok) ? n16 * K + g * G + FM::QB * qi : OOB;
@@ -178,7 +210,19 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                 i32x4 Av[4], C0[4];
 #pragma unroll
                 for (int h = 0; h < 4; ++h) {
-                    u32x4 a = S.A[j][h];
+                    u32x4 a;
+                    if constexpr (XBF) {
+                        const int8_t* fa = lxq + ((size_t)(4 * Q + h) * 64 + L) * FM::QB;
+                        if constexpr (FM::QB == 16) {
+                            a = *(const u32x4*)fa;
+                        } else {
+                            const u32x2 v = *(const u32x2*)fa;
+                            a = u32x4{v.x, v.y, 0u, 0u};
+                        }
+                        S.XS[j][h] = *(const u32x4*)(lxs + (4 * Q + h) * 16 + 4 * kb);
+                    } else {
+                        a = S.A[j][h];
+                    }
                     if constexpr (XNAT && F != 8)
                         a = u32x4{__builtin_amdgcn_perm(a.y, a.x, 0x06040200u), __builtin_amdgcn_perm(a.y, a.x, 0x07050301u),
                                   __builtin_amdgcn_perm(a.w, a.z, 0x06040200u), __builtin_amdgcn_perm(a.w, a.z, 0x07050301u)};
@@ -252,13 +296,44 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         }
     };
 
+    // RC_BF16: quantize the staged octets into the LDS fragments while the
+    // first segment's weights are in flight.  Octet o of row m = o / KO sits
+    // in group g = k8 / (G/8) at octet j = k8 % (G/8); the lane that supplies
+    // it to the MFMA is 16 * bitswap(quarter) + m (quarter = j / 2 for 64-groups,
+    // = j for 32-groups).  Trip counts are wave-uniform, so every DPP group
+    // reduction sees whole groups.
+    auto quantize = [&] {
+        const int wave0 = tid & ~63;
+#pragma unroll
+        for (int i = 0; i < RC_XR; ++i) {
+            if (wave0 + NTT * i < noct) {
+                const int o = tid + NTT * i;
+                uint32_t d0, d1;
+                float sc;
+                quantize_octet<G, (F != 8)>(xv[i], d0, d1, sc);
+                if (o < noct) {
+                    const int m = o / KO, k8 = o - m * KO;
+                    const int g = k8 / (G / 8), j = k8 % (G / 8);
+                    const int q = G == 64 ? j >> 1 : j;
+                    const int slot = ((q & 1) << 1) | (q >> 1);
+                    *(u32x2*)(lxq + ((size_t)g * 64 + 16 * slot + m) * FM::QB + (G == 64 ? (j & 1) * 8 : 0)) =
+                        u32x2{d0, d1};
+                    if (j == 0) lxs[g * 16 + m] = sc;
+                }
+            }
+        }
+        lds_barrier();
+    };
+
     if constexpr (ONE) {
         Seg S;
         load(S, 0);
+        if constexpr (XBF) quantize();
         compute(S, 0);
     } else {
         Seg S0, S1;
         load(S0, 0);
+        if constexpr (XBF) quantize();
         for (int seg = 0; seg < nseg; seg += 2) {
             load(S1, seg + 1);  // past the last segment every load is out of range: no traffic
             compute(S0, seg);
@@ -305,40 +380,42 @@ __host__ __device__ constexpr int rc_rb_qw2(int F) { return F == 8 ? 6 : F == 6 
 constexpr int RC_RB_LOOP = 2;
 
 template <int F, int RB, int W, int QW, bool ONE>
-rc_fn rc_pick4(bool xnat, bool part) {
-    if (xnat)
-        return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, true, true> : qgemm_rc_kernel<F, RB, W, QW, ONE, true, false>;
-    return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, false, true> : qgemm_rc_kernel<F, RB, W, QW, ONE, false, false>;
+rc_fn rc_pick4(int am, bool part) {
+    if (am == RC_NAT)
+        return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, true> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, false>;
+    if (am == RC_BF16)
+        return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, true> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, false>;
+    return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, true> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, false>;
 }
 template <int F, int RB>
-rc_fn rc_pick3(const RcShape& s, bool xnat, bool part) {
-    if (s.one && s.w == 4 && s.qw == 1) return rc_pick4<F, RB, 4, 1, true>(xnat, part);
-    if (s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, true>(xnat, part);
+rc_fn rc_pick3(const RcShape& s, int am, bool part) {
+    if (s.one && s.w == 4 && s.qw == 1) return rc_pick4<F, RB, 4, 1, true>(am, part);
+    if (s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, true>(am, part);
     if constexpr (RB <= rc_rb_qw2(F))
-        if (s.one && s.w == 10 && s.qw == 2) return rc_pick4<F, RB, 10, 2, true>(xnat, part);
+        if (s.one && s.w == 10 && s.qw == 2) return rc_pick4<F, RB, 10, 2, true>(am, part);
     if constexpr (RB <= RC_RB_LOOP)
-        if (!s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, false>(xnat, part);
+        if (!s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, false>(am, part);
     return nullptr;
 }
 template <int F>
-rc_fn rc_pick2(const RcShape& s, bool xnat, bool part) {
+rc_fn rc_pick2(const RcShape& s, int am, bool part) {
     switch (s.rb) {
-        case 1: return rc_pick3<F, 1>(s, xnat, part);
-        case 2: return rc_pick3<F, 2>(s, xnat, part);
-        case 3: return rc_pick3<F, 3>(s, xnat, part);
-        case 4: return rc_pick3<F, 4>(s, xnat, part);
-        case 5: return rc_pick3<F, 5>(s, xnat, part);
-        case 6: return rc_pick3<F, 6>(s, xnat, part);
+        case 1: return rc_pick3<F, 1>(s, am, part);
+        case 2: return rc_pick3<F, 2>(s, am, part);
+        case 3: return rc_pick3<F, 3>(s, am, part);
+        case 4: return rc_pick3<F, 4>(s, am, part);
+        case 5: return rc_pick3<F, 5>(s, am, part);
+        case 6: return rc_pick3<F, 6>(s, am, part);
         default: return nullptr;
     }
 }
 
 // Kernels of format F (each defined in its own translation unit).
 template <int F>
-rc_fn rc_pick(const RcShape& s, bool xnat, bool part);
+rc_fn rc_pick(const RcShape& s, int am, bool part);
 
 #define VQ_RC_PICK(F) \
     template <>       \
-    rc_fn rc_pick<F>(const RcShape& s, bool xnat, bool part) { return rc_pick2<F>(s, xnat, part); }
+    rc_fn rc_pick<F>(const RcShape& s, int am, bool part) { return rc_pick2<F>(s, am, part); }
 
 }  // namespace vq

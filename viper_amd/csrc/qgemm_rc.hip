@@ -37,25 +37,51 @@ bool rc_ok(int qtype, int K) {
     return G != 0 && K % (4 * G) == 0;
 }
 
+static int rc_hstr(int qtype) {
+    switch (qtype) {
+        case VIPER_QTYPE_Q5_G64: return RcFmt<5>::HSTR;
+        case VIPER_QTYPE_Q6_G64: return RcFmt<6>::HSTR;
+        default: return 0;
+    }
+}
+
+// LDS bytes of a launch (RC_BF16 adds the workgroup's copy of the fragments).
+static size_t rc_launch_lds(int qtype, const RcShape& sh, int K, int am) {
+    const int qb = qtype == VIPER_QTYPE_W8_G32 ? RcFmt<8>::QB : RcFmt<4>::QB;
+    return rc_lds_bytes(rc_hstr(qtype), sh.rb, sh.w) + (am == RC_BF16 ? rc_act_lds_bytes(qb, K / group_of(qtype)) : 0);
+}
+
+static RcShape rc_launch_shape(int qtype, int rows_total, int K) {
+    const int F = qtype == VIPER_QTYPE_W8_G32 ? 8 : qtype;
+    return rc_shape(F, rows_total, K / group_of(qtype) / 4, device_cus());
+}
+
+// RC_BF16: every row's octets in RC_XR rounds of the workgroup, and the
+// fragments fit LDS beside the kernel's own buffers.
+bool rc_bf16_ok(int qtype, int N, int K, int M, bool pair) {
+    if (!rc_ok(qtype, K) || M < 2 || M > 16) return false;
+    const RcShape sh = rc_launch_shape(qtype, pair ? 2 * N : N, K);
+    if ((long)M * (K / 8) > (long)RC_XR * 64 * sh.w) return false;
+    return rc_launch_lds(qtype, sh, K, RC_BF16) <= (size_t)device_lds_max();
+}
+
 int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq, const void* xs,
-              bool xnat, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
+              int am, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
               hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     if (!rc_ok(qtype, K) || M < 2 || M > 16) return VIPER_INTERNAL;
-    const int NQ = K / group_of(qtype) / 4;
-    const int F = qtype == VIPER_QTYPE_W8_G32 ? 8 : qtype;
-    const RcShape sh = rc_shape(F, w1 != nullptr ? 2 * N : N, NQ, device_cus());
+    if (am == RC_BF16 && !rc_bf16_ok(qtype, N, K, M, w1 != nullptr)) return VIPER_INTERNAL;
+    const RcShape sh = rc_launch_shape(qtype, w1 != nullptr ? 2 * N : N, K);
     rc_fn fn;
-    int hstr;
     switch (qtype) {
-        case VIPER_QTYPE_Q4_G64: fn = rc_pick<4>(sh, xnat, part != nullptr); hstr = RcFmt<4>::HSTR; break;
-        case VIPER_QTYPE_Q5_G64: fn = rc_pick<5>(sh, xnat, part != nullptr); hstr = RcFmt<5>::HSTR; break;
-        case VIPER_QTYPE_Q6_G64: fn = rc_pick<6>(sh, xnat, part != nullptr); hstr = RcFmt<6>::HSTR; break;
-        default: fn = rc_pick<8>(sh, xnat, part != nullptr); hstr = RcFmt<8>::HSTR; break;
+        case VIPER_QTYPE_Q4_G64: fn = rc_pick<4>(sh, am, part != nullptr); break;
+        case VIPER_QTYPE_Q5_G64: fn = rc_pick<5>(sh, am, part != nullptr); break;
+        case VIPER_QTYPE_Q6_G64: fn = rc_pick<6>(sh, am, part != nullptr); break;
+        default: fn = rc_pick<8>(sh, am, part != nullptr); break;
     }
     if (fn == nullptr) return VIPER_INTERNAL;
     int nb0 = (N + 8 * sh.rb - 1) / (8 * sh.rb);
     const unsigned grid = (unsigned)(w1 != nullptr ? 2 * nb0 : nb0);
-    const size_t lds = rc_lds_bytes(hstr, sh.rb, sh.w);
+    const size_t lds = rc_launch_lds(qtype, sh, K, am);
     const int8_t* a0 = (const int8_t*)xq;
     const float* a1 = (const float*)xs;
     const uint8_t* a2 = (const uint8_t*)w;

@@ -197,13 +197,24 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     }
     const size_t need = workspace_need(qtype, K, M);
     if (wsp == nullptr || wsp_bytes < need || misaligned(wsp, 16)) return VIPER_INVALID_ARGUMENT;
-    // 2..4 rows of one matrix: every workgroup quantizes the rows itself, one
-    // launch (the workspace stays required for M > 1 whichever kernel runs)
+    // Few rows: every workgroup quantizes the rows itself, one launch (the
+    // workspace stays required for M > 1 whichever kernel runs).  Two rows of
+    // one matrix on the M = 1 kernel's dot path; 3..8 rows on the matrix cores
+    // with the quantize into LDS (north-star shape: M = 3 6.15 us, 5 6.63 us,
+    // 8 7.49 us against 6.28 / 8.21 / 8.25 us for the next-best path; at
+    // M >= 10 the rows' quantize in every workgroup costs more than the
+    // quantize launch).
+    const bool mf = mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s));
+    if (b.w == nullptr && M == 2 && m1_rows_ok(qtype, K, M)) {
+        const M1Out outs[1] = {{w, s, y, N}};
+        return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, ev0, ev1, M);
+    }
+    if (mf && M >= 3 && M <= 8 && rc_bf16_ok(qtype, N, K, M, b.w != nullptr))
+        return launch_rc(qtype, w, s, senc, N, K, x, nullptr, RC_BF16, M, y, res, part, b.w, b.s, b.y, st, ev0, ev1);
     if (b.w == nullptr && m1_rows_ok(qtype, K, M)) {
         const M1Out outs[1] = {{w, s, y, N}};
         return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, ev0, ev1, M);
     }
-    const bool mf = mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s));
     const bool staged = mf && mfma_staged(qtype, N, K);
     if (!mf && lds_pre(qtype, M, K) > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
     uint8_t* xq = (uint8_t*)wsp;

@@ -70,6 +70,17 @@ inline int device_cus() {
     return cus;
 }
 
+// LDS one workgroup may allocate on the current device (160 KB on gfx950).
+// Most launch choices keep to LDS_MAX; the bf16-quantizing matrix-core mode
+// stages a workgroup's activation fragments and uses the device's full budget.
+inline int device_lds_max() {
+    int dev = 0, lds = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return LDS_MAX;
+    if (hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || lds < LDS_MAX)
+        return LDS_MAX;
+    return lds;
+}
+
 // ---- launchers (one translation unit each)
 
 // M = 1 (qgemv_m1.hip): one to three matrices of the same K (any N each)
@@ -110,11 +121,15 @@ int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K, 
 bool mfma_ok(int qtype, int K, int M, const void* s);
 
 // M = 2..16, K a multiple of 4 groups (qgemm_rc.hip): row-contiguous weight
-// loads moved into the matrix-core layout through LDS.  Reads the fragment
-// order of the fragment quantize or (xnat) the natural layout.
+// loads moved into the matrix-core layout through LDS.  am (RC_FRAG, RC_NAT,
+// RC_BF16 in qgemm_rc.h): reads the fragment order of the fragment quantize,
+// the natural layout (xq, xs of viper_hip_quantize_act), or bf16 x [M][K]
+// quantized by every workgroup (xq = x, xs unused; rc_bf16_ok must hold).
+enum { RC_FRAG = 0, RC_NAT = 1, RC_BF16 = 2 };
 bool rc_ok(int qtype, int K);
+bool rc_bf16_ok(int qtype, int N, int K, int M, bool pair);
 int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq, const void* xs,
-              bool xnat, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
+              int am, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
               hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
 bool mfma_staged(int qtype, int N, int K);
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
