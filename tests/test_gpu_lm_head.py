@@ -109,3 +109,30 @@ def test_sampling_greedy_random(torch_dev, B, V):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), O.argmax_bf16(lg))
     assert out.cpu().numpy()[0] == V // 3
+
+
+def test_sampling_greedy_ties_within_a_lane(torch_dev):
+    # Lane l scans octets l, l + 1024, ... in order: equal maxima in two octets
+    # of one lane and twice within one octet (16-byte aligned rows), and in
+    # the elements past the last octet (one row, V % 8 != 0), must all resolve
+    # to the smallest index.
+    torch = torch_dev
+    top = bf16([7.5])[0]
+    V = 166144
+    lg = np.full((2, V), bf16([-1.0])[0], dtype=np.uint16)
+    lg[0, 8 * 1030 + 6] = lg[0, 8 * 6 + 3] = top               # octets 6 and 1030: same lane
+    lg[1, 8 * 2000 + 4] = lg[1, 8 * 2000 + 2] = top             # one octet, two equal values
+    lg[1, 8 * 2000 + 1] = bf16([np.nan])[0]
+    out = torch.zeros(2, dtype=torch.int32, device="cuda")
+    assert va.sampling_greedy(dev(torch, lg), out).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy(), [8 * 6 + 3, 8 * 2000 + 2])
+    np.testing.assert_array_equal(out.cpu().numpy(), O.argmax_bf16(lg))
+    Vt = 166144 + 5
+    lt = np.full((1, Vt), bf16([-1.0])[0], dtype=np.uint16)
+    lt[0, Vt - 2] = lt[0, Vt - 1] = top                         # the tail past the last octet
+    lt[0, 8 * 17 + 1] = bf16([7.25])[0]
+    ot = torch.zeros(1, dtype=torch.int32, device="cuda")
+    assert va.sampling_greedy(dev(torch, lt), ot).ok()
+    torch.cuda.synchronize()
+    assert ot.cpu().numpy()[0] == Vt - 2 == O.argmax_bf16(lt)[0]

@@ -10,9 +10,11 @@
 // are in flight).  Each 16-byte chunk is 8 bf16 and costs 4 v_dot2_f32_bf16
 // per activation row; teams are reduced with DPP in a fixed order.
 //
-// Argmax: one workgroup per logits row scans 16-byte octets; a lane keeps the
-// first index of its largest value (strict >, so NaN never wins and ties keep
-// the smaller index); lanes and waves combine by (value, then smaller index).
+// Argmax: one workgroup per logits row; every lane requests all of its
+// 16-byte octets at once, keeps the first octet holding its largest value
+// (octet maxima by v_max, compared with strict >, so NaN never wins and ties
+// keep the smaller index), then finds the first element of that octet equal
+// to it; lanes and waves combine by (value, then smaller index).
 
 #include "qlinear_host.h"
 
@@ -115,7 +117,17 @@ __device__ __forceinline__ void better(float& v, int& i, float ov, int oi) {
 }
 
 constexpr int AM_NT = 1024;
-constexpr int AM_BATCH = 8;
+constexpr int AM_PT = 24;  // octets per lane in flight at once (the whole 166144-logit row in one pass)
+
+// Largest of the 8 bf16 values of an octet (v_max_f32 / v_max3_f32 return
+// the non-NaN operand, so NaN never wins, as with the strict > scan).
+__device__ __forceinline__ float octet_max(const u32x4& q) {
+    const float f0 = __uint_as_float(q.x << 16), f1 = __uint_as_float(q.x & 0xffff0000u);
+    const float f2 = __uint_as_float(q.y << 16), f3 = __uint_as_float(q.y & 0xffff0000u);
+    const float f4 = __uint_as_float(q.z << 16), f5 = __uint_as_float(q.z & 0xffff0000u);
+    const float f6 = __uint_as_float(q.w << 16), f7 = __uint_as_float(q.w & 0xffff0000u);
+    return fmaxf(fmaxf(fmaxf(f0, f1), fmaxf(f2, f3)), fmaxf(fmaxf(f4, f5), fmaxf(f6, f7)));
+}
 
 __global__ void __launch_bounds__(AM_NT)
 argmax_bf16_kernel(const uint16_t* logits, int32_t* __restrict__ out, int V) {
@@ -124,34 +136,41 @@ argmax_bf16_kernel(const uint16_t* logits, int32_t* __restrict__ out, int V) {
     const int b = (int)blockIdx.x;
     const int tid = (int)threadIdx.x;
     const uint16_t* row = logits + (size_t)b * V;
-    float best = -__builtin_inff();
-    int idx = 0;
-    // octets first (16-byte loads when the row is 16-byte aligned), then the tail
+    // octets (16-byte loads when the row is 16-byte aligned): per lane the
+    // first octet holding its largest value (octets are visited in increasing
+    // order per lane, strict >), all of a pass's loads in flight at once
+    // (buffer loads: past the row they read zero and are skipped by the
+    // index bound)
     const bool vec = ((((uintptr_t)row) & 15) == 0);
     const int noct = vec ? V / 8 : 0;
-    // AM_BATCH octets per lane in flight at once (buffer loads: past the row
-    // they read zero and are skipped by the index bound)
     const auto rr = buf(row, (uint32_t)noct * 16);
-    for (int o0 = tid; o0 < noct; o0 += AM_NT * AM_BATCH) {
-        u32x4 q[AM_BATCH];
+    float best = -__builtin_inff();
+    int boct = -1;
+    for (int o0 = tid; o0 < noct; o0 += AM_NT * AM_PT) {
+        u32x4 q[AM_PT];
 #pragma unroll
-        for (int b = 0; b < AM_BATCH; ++b) q[b] = bload16(rr, (o0 + b * AM_NT) * 16);
+        for (int i = 0; i < AM_PT; ++i) q[i] = bload16(rr, (o0 + i * AM_NT) * 16);
 #pragma unroll
-        for (int b = 0; b < AM_BATCH; ++b) {
-            const int o = o0 + b * AM_NT;
-            if (o < noct) {
-                const uint32_t wd[4] = {q[b].x, q[b].y, q[b].z, q[b].w};
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float f = bf16f((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu);
-                    if (f > best) {
-                        best = f;
-                        idx = o * 8 + j;
-                    }
-                }
+        for (int i = 0; i < AM_PT; ++i) {
+            const int o = o0 + i * AM_NT;
+            const float m = octet_max(q[i]);
+            if (o < noct && m > best) {
+                best = m;
+                boct = o;
             }
         }
     }
+    // the first element of that octet equal to its maximum
+    int idx = 0;
+    if (boct >= 0) {
+        const u32x4 q = bload16(rr, boct * 16);
+        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+        idx = boct * 8 + 7;
+#pragma unroll
+        for (int j = 7; j >= 0; --j)
+            if (bf16f((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu) == best) idx = boct * 8 + j;
+    }
+    // elements past the last octet (or an unaligned row), one per lane
     for (int v = noct * 8 + tid; v < V; v += AM_NT) {
         const float f = bf16f(row[v]);
         if (f > best) {
@@ -159,8 +178,8 @@ argmax_bf16_kernel(const uint16_t* logits, int32_t* __restrict__ out, int V) {
             idx = v;
         }
     }
-    // The per-lane scans above visit indices in increasing order per lane but
-    // interleaved across lanes, so equal maxima resolve in the combine below.
+    // Indices increase per lane but interleave across lanes, so equal maxima
+    // resolve in the combine below (larger value, then smaller index).
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_xor(best, off, 64);
