@@ -141,6 +141,8 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip the M=16 and down-shape lines")
     ap.add_argument("--m16-only", action="store_true",
                     help="only time the M=16 verify (K=2560, N=10240) line (rocprofv3 counter runs)")
+    ap.add_argument("--verify-only", type=int, default=0, metavar="M",
+                    help="only time the M-row verify (K=2560, N=10240) line (rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -167,9 +169,10 @@ def main():
 
     N, K, M = 10240, 2560, 1
     qtype, G = int(va.QType.Q4_G64), 64
-    if args.m16_only:
-        us, gbs = time_linear(torch, L, gen, qtype, N, K, 16, steps=args.steps)
-        print(json.dumps({"workload": "Q4_G64 M=16 verify K=2560 N=10240", "us": us, "gbs": gbs}), flush=True)
+    if args.m16_only or args.verify_only:
+        Mv = 16 if args.m16_only else args.verify_only
+        us, gbs = time_linear(torch, L, gen, qtype, N, K, Mv, steps=args.steps)
+        print(json.dumps({"workload": f"Q4_G64 M={Mv} verify K=2560 N=10240", "us": us, "gbs": gbs}), flush=True)
         return
     copy_bytes = N * K // 2 + N * (K // G) * 2
     copies = max(2, -(-ROTATE_BYTES // copy_bytes) + 1)
