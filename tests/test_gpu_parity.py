@@ -388,3 +388,49 @@ def test_device_errors_are_codes(torch_dev):
     wbad = va.QuantizedWeight(va.QType.BF16, wd, sd, N, K)
     assert va.linear(wbad, x, y).code == va.StatusCode.UNIMPLEMENTED
     assert va.linear(w, x[:1], y[:1, :N - 1]).code == va.StatusCode.SHAPE_MISMATCH
+
+
+def crafted_act(M, K, G, seed):
+    """Rows whose groups hit the quantizer's special cases, rotated per row: an all-zero group
+    (scale 1e-8, q = 0), a group with amax 127 and exact .5 ties (scale 1: RNE to even), a group of
+    values near 1e-6, a x20 outlier group, random groups elsewhere."""
+    x = O.bf16_to_f32(O.gen_act(M, K, seed)).copy()
+    ties = np.array([127.0, 2.5, 3.5, -2.5, 0.5, -1.5, -0.5, 1.5], dtype=np.float32)
+    for m in range(M):
+        g0 = (m % 4) * G
+        x[m, g0:g0 + G] = 0.0
+        g1 = ((m + 1) % 4) * G
+        x[m, g1:g1 + G] = np.resize(ties, G)
+        g2 = ((m + 2) % 4) * G
+        x[m, g2:g2 + G] = np.linspace(-1e-6, 1e-6, G, dtype=np.float32)
+        g3 = ((m + 3) % 4) * G
+        x[m, g3:g3 + G] *= 20.0
+    return O.f32_to_bf16(x)
+
+
+# The quantize is fused into every GEMV path (the M = 1 prologue, M = 2 rows in
+# the M = 1 kernel, M = 3..8 into LDS in the matrix-core kernel, the fragment
+# quantize launch beyond): each must give the oracle's int8 values, so the
+# group dots are bit-exact on the quantizer's special cases.
+@pytest.mark.parametrize("qtype", [O.Q4_G64, O.Q6_G64, O.W8_G32])
+@pytest.mark.parametrize("M", [1, 2, 5, 12])
+def test_quantizer_edge_cases_every_path(torch_dev, qtype, M):
+    torch = torch_dev
+    N, K = 77, 2560
+    G = O.group_size(qtype)
+    note(f"case qtype={qtype} M={M} crafted activations")
+    packed, scales = O.gen_weights(qtype, N, K, 90 + M, O.SCALE_FP16)
+    x = crafted_act(M, K, G, 91 + M)
+    xq, _ = O.quantize_act(x, G)
+    assert list(xq[0, G:G + 8]) == [127, 2, 4, -2, 0, -2, 0, 2]   # the ties group of row 0
+    D_ref = O.group_dots(qtype, packed, N, K, xq)
+    y_ref, _, absterm = O.qlinear(qtype, packed, scales, O.SCALE_FP16, N, K, x)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G)
+    yd = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    pd = torch.full((M, N, K // G), -7, dtype=torch.int32, device="cuda")
+    nws = va.workspace_bytes(qtype, N, K, M)
+    wsd = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda") if nws else None
+    assert va.linear_partials(w, dev(torch, x), yd, pd, workspace=wsd).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(pd, np.int32), D_ref)
+    O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
