@@ -40,6 +40,15 @@
 // may share a launch (fused pair): workgroups [0, nb0) use (w, ws, y), the
 // rest (w1, ws1, y1).
 //
+// Arguments.  Only the first 14 argument dwords arrive preloaded in SGPRs;
+// a later argument is a scalar load from the argument buffer that the wave
+// waits for (the weight-scale encoding read after the weight loads cost
+// 0.17 us of the M = 16 verify, the residual pointer waited for before the
+// first load 0.3 us).  So everything the common path reads fits 14 dwords:
+// N, M - 1 and the encoding share one word (nm: N in bits 0..26, M - 1 in
+// 27..30, the encoding in bit 31) and the first matrix's workgroup count is
+// derived from N (both matrices of a pair have N rows).
+//
 // Activation modes (AM): RC_FRAG reads the fragments and [group][16] scales
 // the fragment quantize wrote; RC_NAT gathers them from the natural layout
 // ([M][K] int8, [M][K/G] fp32); RC_BF16 takes the bf16 rows themselves: every
@@ -88,7 +97,7 @@ struct RcSeg {
 template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART>
 __global__ void __launch_bounds__(64 * W)
 qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
-                int M, int N, int nb0, int senc, const uint16_t* res, int32_t* __restrict__ part,
+                unsigned nm, const uint16_t* res, int32_t* __restrict__ part,
                 const uint8_t* w1, const uint16_t* ws1, uint16_t* y1) {
     using FM = RcFmt<F>;
     using Seg = RcSeg<F, RB, QW>;
@@ -100,8 +109,13 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     const int n16 = L & 15, kb = L >> 4, qi = ((kb & 1) << 1) | (kb >> 1);
     const int NG = K / G, NQ = NG / 4;
     const int nseg = ONE ? 1 : (NQ + W * QW - 1) / (W * QW);
+    const int N = (int)(nm & ((1u << 27) - 1)), M = (int)((nm >> 27) & 15u) + 1;
+    const bool senc = (nm >> 31) != 0;
+    const int nb0 = (N + 8 * RB - 1) / (8 * RB);
     int bid = (int)blockIdx.x;
-    if (bid >= nb0) {
+    // the second matrix of a fused pair and the residual are the rare paths:
+    // marked unlikely, the common path is laid out and scheduled straight
+    if (__builtin_expect(bid >= nb0, 0)) {
         bid -= nb0;
         w = w1;
         ws = ws1;
@@ -208,6 +222,28 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
             const int Q = wave + W * (seg * QW + j);
             if (Q < NQ) {
                 i32x4 Av[4], C0[4];
+                // weight scales of the quad's groups for each tile, decoded
+                // once per quad under one uniform branch (a select per group
+                // inside the MFMA loop became a branch pair per group and
+                // tile, 0.4 us of the M = 16 verify)
+                float WSV[T][4];
+                if (senc) {
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        WSV[t][0] = bf16f(S.S[j][t].x & 0xffffu);
+                        WSV[t][1] = bf16f(S.S[j][t].x >> 16);
+                        WSV[t][2] = bf16f(S.S[j][t].y & 0xffffu);
+                        WSV[t][3] = bf16f(S.S[j][t].y >> 16);
+                    }
+                } else {
+#pragma unroll
+                    for (int t = 0; t < T; ++t) {
+                        WSV[t][0] = f16f(S.S[j][t].x & 0xffffu);
+                        WSV[t][1] = f16f(S.S[j][t].x >> 16);
+                        WSV[t][2] = f16f(S.S[j][t].y & 0xffffu);
+                        WSV[t][3] = f16f(S.S[j][t].y >> 16);
+                    }
+                }
 #pragma unroll
                 for (int h = 0; h < 4; ++h) {
                     u32x4 a;
@@ -276,9 +312,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                             C = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                                 Av[h], i32x4{(int)wd[0], (int)wd[1], (int)wd[2], (int)wd[3]}, C0[h], 0, 0, 0);
                         }
-                        const uint32_t sw = (h < 2) ? S.S[j][t].x : S.S[j][t].y;
-                        const uint32_t sh = (h & 1) ? (sw >> 16) : (sw & 0xffffu);
-                        const float wsf = senc ? bf16f(sh) : f16f(sh);
+                        const float wsf = WSV[t][h];
                         const float xf[4] = {__uint_as_float(S.XS[j][h].x), __uint_as_float(S.XS[j][h].y),
                                              __uint_as_float(S.XS[j][h].z), __uint_as_float(S.XS[j][h].w)};
 #pragma unroll
@@ -357,7 +391,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         const int m = 4 * kb + r, nl = 16 * t + n16;
         if (m < M && nl < nrows) {
             const size_t o = (size_t)m * N + row0 + nl;
-            if (res != nullptr) v += bf16f(res[o]);
+            if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
             y[o] = f2bf(v);
         }
     }
@@ -365,8 +399,8 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
 
 // ------------------------------------------------------------------ host side
 
-typedef void (*rc_fn)(const int8_t*, const float*, const uint8_t*, const uint16_t*, uint16_t*, int, int, int,
-                      int, int, const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*);
+typedef void (*rc_fn)(const int8_t*, const float*, const uint8_t*, const uint16_t*, uint16_t*, int, unsigned,
+                      const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*);
 
 // Launch shape: rows per workgroup (8 * rb), waves, quads per wave per
 // segment, single segment or double-buffered loop.

@@ -69,6 +69,7 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
               int am, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
               hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
     if (!rc_ok(qtype, K) || M < 2 || M > 16) return VIPER_INTERNAL;
+    if (N >= (1 << 27)) return VIPER_INVALID_ARGUMENT;  // N shares a word with M and the encoding
     if (am == RC_BF16 && !rc_bf16_ok(qtype, N, K, M, w1 != nullptr)) return VIPER_INTERNAL;
     const RcShape sh = rc_launch_shape(qtype, w1 != nullptr ? 2 * N : N, K);
     rc_fn fn;
@@ -91,7 +92,8 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     const uint8_t* b0 = (const uint8_t*)w1;
     const uint16_t* b1 = (const uint16_t*)s1;
     uint16_t* b2 = (uint16_t*)y1;
-    void* args[] = {&a0, &a1, &a2, &a3, &a4, &K, &M, &N, &nb0, &senc, &a5, &part, &b0, &b1, &b2};
+    unsigned nm = (unsigned)N | ((unsigned)(M - 1) << 27) | (senc ? 1u << 31 : 0u);  // see the kernel's arguments note
+    void* args[] = {&a0, &a1, &a2, &a3, &a4, &K, &nm, &a5, &part, &b0, &b1, &b2};
     launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args, ev0, ev1);
     return status_of(hipGetLastError());
 }

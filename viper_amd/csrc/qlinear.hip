@@ -50,15 +50,18 @@ quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
         if constexpr (MF) {
             // group g, k-slot kb of the octet's quarter, row m (matrix-core
             // fragment order: quarter qi of a group sits in k-slot
-            // kb = bit-swap(qi), Q bytes per fragment)
+            // kb = bit-swap(qi), Q bytes per fragment); written through like
+            // quantize_frag64_kernel's stores
             constexpr int Q = G == 64 ? 16 : 8;
             const int opr = K / 8;
             const int m = o / opr, og = o % opr;
             const int g = og / (G / 8), k0 = (og % (G / 8)) * 8;
             const int qi = k0 / Q;
             const int kb = ((qi & 1) << 1) | (qi >> 1);
-            *(u32x2*)(xq + ((size_t)(g * 4 + kb) * 16 + m) * Q + k0 % Q) = u32x2{d0, d1};
-            if ((o & (G / 8 - 1)) == 0) xs[g * 16 + m] = s;
+            const auto xw = buf(xq, (uint32_t)(K / G) * 64u * (uint32_t)Q);
+            const auto sw = buf(xs, (uint32_t)(K / G) * 64u);
+            bstore8<AUX_SC1>(xw, ((g * 4 + kb) * 16 + m) * Q + k0 % Q, u32x2{d0, d1});
+            if ((o & (G / 8 - 1)) == 0) bstore4<AUX_SC1>(sw, (g * 16 + m) * 4, __float_as_uint(s));
         } else {
             *(u32x2*)(xq + (size_t)o * 8) = u32x2{d0, d1};
             if ((o & (G / 8 - 1)) == 0) xs[(size_t)o * 8 / G] = s;
@@ -96,8 +99,12 @@ quantize_frag64_kernel(const uint16_t* x, int M, int K, int8_t* __restrict__ xq,
     for (int i = 0; i < 16; ++i) t[i] = qbits(f[i], s, r);
     const u32x4 o = {bytes4(t[0], t[2], t[4], t[6]), bytes4(t[1], t[3], t[5], t[7]), bytes4(t[8], t[10], t[12], t[14]),
                      bytes4(t[9], t[11], t[13], t[15])};
-    if (ok) *(u32x4*)(xq + ((size_t)g * 64 + L) * 16) = o;
-    if (ok && kb == 0) xs[g * 16 + m] = s;
+    // written through (the matrix-core kernel reads them right after this
+    // launch; 0.2 us of the M = 16 verify)
+    const auto xw = buf(xq, (uint32_t)(K / 64) * 1024u);
+    const auto sw = buf(xs, (uint32_t)(K / 64) * 64u);
+    bstore16<AUX_SC1>(xw, ok ? (g * 64 + L) * 16 : OOB, o);
+    bstore4<AUX_SC1>(sw, (ok && kb == 0) ? (g * 16 + m) * 4 : OOB, __float_as_uint(s));
 }
 
 // --------------------------------------------------- quantizer self-check

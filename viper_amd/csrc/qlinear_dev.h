@@ -272,11 +272,28 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 constexpr int BUF_CFG = 0x00020000;  // dword 3 of a raw buffer resource on gfx9
 constexpr int AUX_NT = 2;            // non-temporal (streamed once)
+constexpr int AUX_SC1 = 16;          // device scope: written through the XCD's L2 (no dirty line left)
 constexpr int OOB = 0x7ffffff0;      // an offset past any range used here
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, BUF_CFG);
 }
+// Buffer stores (out-of-range offsets are dropped by the resource bounds).
+// Written-through stores (AUX_SC1) leave no dirty L2 line for the end-of-kernel
+// write-back, which shortens small producer kernels whose consumer follows.
+template <int AUX = 0>
+__device__ __forceinline__ void bstore16(__amdgpu_buffer_rsrc_t r, int off, const u32x4& v) {
+    __builtin_amdgcn_raw_buffer_store_b128(i32x4{(int)v.x, (int)v.y, (int)v.z, (int)v.w}, r, off, 0, AUX);
+}
+template <int AUX = 0>
+__device__ __forceinline__ void bstore8(__amdgpu_buffer_rsrc_t r, int off, const u32x2& v) {
+    __builtin_amdgcn_raw_buffer_store_b64(i32x2{(int)v.x, (int)v.y}, r, off, 0, AUX);
+}
+template <int AUX = 0>
+__device__ __forceinline__ void bstore4(__amdgpu_buffer_rsrc_t r, int off, uint32_t v) {
+    __builtin_amdgcn_raw_buffer_store_b32((int)v, r, off, 0, AUX);
+}
+
 template <int AUX = 0>
 __device__ __forceinline__ u32x4 bload16(__amdgpu_buffer_rsrc_t r, int off) {
     const i32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX);
