@@ -267,17 +267,37 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         }
     };
     // rounds past the row are not issued (the bound is workgroup-uniform)
+    // The first input's octets go out first: the second input (int8 group
+    // scales, gamma, up) sits past the 14 preloaded argument dwords, and the
+    // wait for its argument load then follows these requests instead of
+    // preceding every load of the wave.
     u32x4 xv[XS], av[XS];
 #pragma unroll
     for (int i = 0; i < XS; ++i) {
         xv[i] = u32x4{0u, 0u, 0u, 0u};
         av[i] = xv[i];
         if (i == 0 || NTT * i < noct) {
-            xv[i] = load_x(tid + NTT * i);
-            if constexpr (TWO) av[i] = bload16(xsr, (tid + NTT * i) * 16);
+            if constexpr (PRE) {
+                const u32x2 q = bload8(xr, (tid + NTT * i) * 8);
+                xv[i] = u32x4{q.x, q.y, 0u, 0u};
+            } else {
+                xv[i] = bload16(xr, (tid + NTT * i) * 16);
+            }
         }
     }
     issue_fence();
+    if constexpr (PRE || TWO) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < XS; ++i) {
+            if (i == 0 || NTT * i < noct) {
+                const int o = tid + NTT * i;
+                if constexpr (PRE) xv[i].z = bload4(xsr, (o % OPC == 0) ? (o / OPG) * 4 : OOB);
+                else av[i] = bload16(xsr, o * 16);
+            }
+        }
+        issue_fence();
+    }
     const auto sr = buf(ws + (size_t)row0 * NGR, (uint32_t)(nrows * NGR) * 2);
     u32x4 sblk = {0u, 0u, 0u, 0u};
     if constexpr (EXACT) sblk = bload16(sr, ltid * 16);
