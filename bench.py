@@ -201,6 +201,24 @@ def main():
 
     extras = {}
     if not args.no_extras:
+        # the floor of one dispatch streaming the same weight bytes: a read-only kernel with the GEMV's
+        # launch shape over the same rotating copies (viper_hip_stream_read)
+        sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+        wbytes = N * K // 2
+
+        def launch_read(i):
+            rc = L.viper_hip_stream_read(wp[i % copies], wbytes, sink.data_ptr(),
+                                         torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"viper_hip_stream_read failed: {rc}")
+        for i in range(20):
+            launch_read(i)
+        gr, rr = capture(torch, launch_read, copies, args.steps)
+        read_us = time_graph(torch, gr, rr) * 1e3 / (rr * copies)
+        extras["stream_read_weights_us"] = round(read_us, 3)
+        extras["stream_read_weights_gbs"] = round(wbytes / (read_us * 1e-6) / 1e9, 1)
+        del gr
+
         # M=16 speculative verify (K=2560, N=10240): quantize kernel + GEMM
         M16 = 16
         x16 = torch.randn((M16, K), device="cuda", generator=gen).to(torch.bfloat16)

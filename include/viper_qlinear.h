@@ -50,6 +50,9 @@
  *                                   attached to the GEMV dispatch (benchmarking).
  *   viper_hip_check_quantizer       no counterpart: device self-check of the
  *                                   activation quantizer's rounding.
+ *   viper_hip_stream_read           no counterpart: reads a buffer once with the
+ *                                   M = 1 GEMV's launch shape (measurement: the
+ *                                   floor of one streaming dispatch).
  *
  * Formats (qtype values are viper::quant::QType, include/viper/quant.h:19-26):
  *   Q4_G64 (4)  packed [N][K/2]; k even in the low nibble; nibble = w + 8.
@@ -227,6 +230,14 @@ int viper_hip_qlinear_partials(int qtype, const void* w_packed, const void* w_sc
  * entries) receives the number of disagreements for amax bits
  * (exp_lo << 7) + i. */
 int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream);
+
+/* Measurement probe, no counterpart in the reference: reads `bytes` (a
+ * multiple of 16, 16-byte aligned buffer) once with the launch shape and load
+ * pattern of the north-star GEMV (320-thread workgroups, five 16-byte
+ * non-temporal loads per lane) and nothing else, so its duration is the
+ * floor of one dispatch streaming that many bytes.  sink (4 bytes) is
+ * written only if the folded data equals a fixed magic word. */
+int viper_hip_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

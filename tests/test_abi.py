@@ -78,6 +78,11 @@ def test_other_entry_validation():
     assert L.viper_hip_qlinear_partials(4, FAKE, FAKE, 0, 64, 8, 64, FAKE, 1, FAKE, None, None, 0, None, None) == 2
     assert L.viper_hip_check_quantizer(10, 5, FAKE, None) == 2
     assert L.viper_hip_check_quantizer(0, 255, FAKE, None) == 2
+    assert L.viper_hip_stream_read(None, 16, FAKE, None) == 2
+    assert L.viper_hip_stream_read(FAKE, 0, FAKE, None) == 2
+    assert L.viper_hip_stream_read(FAKE, 24, FAKE, None) == 2     # not a multiple of 16
+    assert L.viper_hip_stream_read(FAKE + 8, 16, FAKE, None) == 2  # buffer not 16-byte aligned
+    assert L.viper_hip_stream_read(FAKE, 16, None, None) == 2
 
 
 def test_registry_mirror():

@@ -434,3 +434,21 @@ def test_quantizer_edge_cases_every_path(torch_dev, qtype, M):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(pd, np.int32), D_ref)
     O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
+
+
+def test_stream_read_probe(torch_dev):
+    # the measurement probe reads every byte: a lane whose 16 bytes fold to the
+    # magic word writes it to the sink, zeros leave the sink alone
+    torch = torch_dev
+    L = va.lib()
+    buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), sink.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    assert int(sink[0]) == 0
+    words = buf.view(torch.int32)
+    words[(1 << 18) - 4] = np.int32(np.uint32(0x9E3779B9).view(np.int32))   # the last 16 bytes
+    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), sink.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    assert np.uint32(int(sink[0]) & 0xFFFFFFFF) == np.uint32(0x9E3779B9)

@@ -134,6 +134,27 @@ __global__ void __launch_bounds__(NT) check_quantizer_kernel(int ab0, int32_t* _
     if (threadIdx.x == 0) counts[blockIdx.x] = red[0];
 }
 
+// --------------------------------------------------- streaming-read probe
+
+// Reads a buffer once with the north-star GEMV's launch shape and load
+// pattern (320-thread workgroups, five 16-byte non-temporal loads per lane,
+// all issued at once) and does nothing else: its duration is what one
+// dispatch streaming those bytes costs here, the floor the GEMV is compared
+// with.  The loaded words are folded so the loads stay; the fold reaches
+// memory only in the (never expected) case that it equals the magic word.
+constexpr int SR_NT = 320, SR_LPT = 5;
+__global__ void __launch_bounds__(SR_NT) stream_read_kernel(const uint8_t* p, uint32_t bytes, uint32_t* sink) {
+    const auto r = buf(p, bytes);
+    const int base = (int)blockIdx.x * SR_NT * SR_LPT * 16;
+    u32x4 v[SR_LPT];
+#pragma unroll
+    for (int j = 0; j < SR_LPT; ++j) v[j] = bload16<AUX_NT>(r, base + (j * SR_NT + (int)threadIdx.x) * 16);
+    uint32_t f = 0u;
+#pragma unroll
+    for (int j = 0; j < SR_LPT; ++j) f ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    if (f == 0x9E3779B9u) sink[0] = f;
+}
+
 static int launch_quantize(int group, const void* x, int M, int K, void* xq, void* xs, bool mf,
                            hipStream_t st) {
     const int oct_total = M * K / 8;
@@ -397,6 +418,20 @@ extern "C" int viper_hip_qlinear_m1_swiglu(int qtype, int scale_enc, int group, 
     if (prologue == VIPER_PROLOGUE_RMSNORM && !vq::m1_folded_ok(qtype, K, N)) return VIPER_INVALID_ARGUMENT;
     return vq::launch_m1_swiglu(qtype, scale_enc, K, prologue, a, b, eps, norm_out, w_gate, s_gate, w_up, s_up, N,
                                 h_bf16, gate_bf16, up_bf16, (hipStream_t)stream);
+}
+
+extern "C" int viper_hip_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) {
+    if (buf == nullptr || sink == nullptr || bytes == 0 || bytes % 16 != 0 || bytes > (size_t)INT32_MAX)
+        return VIPER_INVALID_ARGUMENT;
+    if (vq::misaligned(buf, 16) || vq::misaligned(sink, 4)) return VIPER_INVALID_ARGUMENT;
+    constexpr size_t per_wg = (size_t)vq::SR_NT * vq::SR_LPT * 16;
+    const unsigned grid = (unsigned)((bytes + per_wg - 1) / per_wg);
+    const uint8_t* a0 = (const uint8_t*)buf;
+    uint32_t n = (uint32_t)bytes;
+    void* args[] = {&a0, &n, &sink};
+    vq::launch((const void*)vq::stream_read_kernel, grid, vq::SR_NT, 0, (hipStream_t)stream, args, nullptr,
+               nullptr);
+    return vq::status_of(hipGetLastError());
 }
 
 extern "C" int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream) {

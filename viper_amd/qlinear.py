@@ -121,6 +121,7 @@ _SYMBOLS = (
     "viper_hip_qlinear_partials",
     "viper_hip_qlinear_timed",
     "viper_hip_check_quantizer",
+    "viper_hip_stream_read",
     "viper_hip_qlinear_fused2",
     "viper_hip_qlinear_fused2_prequantized",
     "viper_hip_rmsnorm_quantize",
@@ -159,6 +160,8 @@ def lib():
     L.viper_hip_qlinear_timed.restype = i32
     L.viper_hip_check_quantizer.argtypes = [i32, i32, vp, vp]
     L.viper_hip_check_quantizer.restype = i32
+    L.viper_hip_stream_read.argtypes = [vp, sz, vp, vp]
+    L.viper_hip_stream_read.restype = i32
     L.viper_hip_qlinear_fused2.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     L.viper_hip_qlinear_fused2.restype = i32
     L.viper_hip_qlinear_fused2_prequantized.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, i32,
