@@ -54,14 +54,19 @@ ROW_BYTES = {4: lambda K: K // 2, 5: lambda K: K * 5 // 8, 6: lambda K: K * 6 //
 GROUP = {4: 64, 5: 64, 6: 64, 8: 32}
 
 
-def time_linear(torch, L, gen, qtype, N, K, M, steps=400):
-    """us per call of viper_hip_qlinear (bf16 x, fused or separate quantize) over rotating weights."""
+def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False):
+    """us per call of viper_hip_qlinear (bf16 x, fused or separate quantize) over rotating weights;
+    outliers: 5% of the activation channels (a fixed seeded set) scaled x20, as config 4 states."""
     G = GROUP[qtype]
     rb = ROW_BYTES[qtype](K)
     copy_bytes = N * rb + N * (K // G) * 2
     copies = max(2, -(-ROTATE_BYTES // copy_bytes) + 1)
     W, S = make_weights(torch, copies, N, K, gen, row_bytes=rb, G=G)
-    x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+    xf = torch.randn((M, K), device="cuda", generator=gen)
+    if outliers:
+        ch = torch.randperm(K, device="cuda", generator=gen)[: K // 20]
+        xf[:, ch] *= 20.0
+    x = xf.to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     nws = L.viper_hip_qlinear_workspace_bytes(qtype, N, K, M)
     ws = torch.empty(max(nws, 16), dtype=torch.uint8, device="cuda")
@@ -246,13 +251,18 @@ def main():
         for Mv in (2, 4, 8):
             us_v, gbs_v = time_linear(torch, L, gen, qtype, N, K, Mv)
             extras[f"verify_m{Mv}_us"], extras[f"verify_m{Mv}_gbs"] = us_v, gbs_v
-        us_v, gbs_v = time_linear(torch, L, gen, qtype, 2560, 10240, 16)
-        extras["verify_m16_down_us"], extras["verify_m16_down_gbs"] = us_v, gbs_v
+        for Mv in (2, 4, 8, 16):
+            us_v, gbs_v = time_linear(torch, L, gen, qtype, 2560, 10240, Mv)
+            extras[f"verify_m{Mv}_down_us"], extras[f"verify_m{Mv}_down_gbs"] = us_v, gbs_v
+
+        # config 0: the attention q/o projection, Q4_G64 M=1, K=N=2560
+        us_v, gbs_v = time_linear(torch, L, gen, qtype, 2560, 2560, 1)
+        extras["config0_us"], extras["config0_gbs"] = us_v, gbs_v
 
         # config 4: Q5_G64, Q6_G64 and W8_G32 at M=1 and M=8, K=2560, N=10240
         for qt, nm in ((5, "q5"), (6, "q6"), (8, "w8")):
             for Mv in (1, 8):
-                us_v, gbs_v = time_linear(torch, L, gen, qt, N, K, Mv)
+                us_v, gbs_v = time_linear(torch, L, gen, qt, N, K, Mv, outliers=True)
                 extras[f"{nm}_m{Mv}_us"], extras[f"{nm}_m{Mv}_gbs"] = us_v, gbs_v
 
         # down projection shape (K=10240, N=2560), M=1, fused quantize

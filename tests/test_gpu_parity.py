@@ -122,9 +122,11 @@ def test_multi_row(torch_dev, qtype, M):
     run_case(torch_dev, qtype, 77, K, M, seed=2000 + M, residual=(M % 2 == 0))
 
 
-# M = 2..4 at long K: rows staged in all eight rounds of a 640-thread
-# workgroup (M * K / 8 = 5120 octets), and past that bound (the matrix-core
-# path takes the call).
+# M = 2..4 at long K from bf16 x: 2 rows (and 3 rows, M * K <= 32768) staged
+# by every workgroup of the M = 1 kernel, 4 rows at K = 10240 and rows past
+# the staging bound on the matrix cores after the quantize launch.  (The
+# prequantized entry takes 4 rows at K = 10240 through all eight staging
+# rounds of a 640-thread workgroup: test_prequantized_entry.)
 @pytest.mark.parametrize("qtype", FORMATS)
 @pytest.mark.parametrize("M,K", [(2, 10240), (4, 10240), (3, 12288), (4, 16384)])
 def test_multi_row_long_k(torch_dev, qtype, M, K):
@@ -251,7 +253,7 @@ def test_bf16_rows_match_prequantized(torch_dev, qtype, N, K, M):
     O.assert_bf16_close(host(ya, np.uint16), y_ref, absterm, rel=REL_TOL)
 
 
-@pytest.mark.parametrize("N,K,M", [(200, 2560, 3), (70, 10240, 16), (40, 192, 2), (6001, 4096, 16)])
+@pytest.mark.parametrize("N,K,M", [(200, 2560, 3), (70, 10240, 16), (40, 192, 2), (6001, 4096, 16), (45, 10240, 4)])
 def test_prequantized_entry(torch_dev, N, K, M):
     # activations in viper_hip_quantize_act's layout ([M][K] int8, [M][K/G] fp32)
     torch = torch_dev
