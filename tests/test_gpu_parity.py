@@ -145,6 +145,8 @@ def test_multi_row_long_k(torch_dev, qtype, M, K):
     (33, 6144, 7, O.SCALE_BF16),
     (16400, 256, 3, O.SCALE_FP16),
     (29, 192, 4, O.SCALE_FP16),
+    (300, 384, 9, O.SCALE_BF16),     # 6 groups (W8: 12): the pair-wise matrix-core kernel
+    (70, 640, 12, O.SCALE_FP16),     # 10 groups (W8: 20)
 ])
 def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
     run_case(torch_dev, qtype, N, K, M, seed=3000 + N + M, scale_enc=senc, residual=(M % 2 == 1))

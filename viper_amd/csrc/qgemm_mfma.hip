@@ -104,12 +104,17 @@ __host__ __device__ constexpr size_t mf_lds_bytes(bool xnat, int W, int T, int N
 // ONE: every wave's pairs fit one segment (ceil(NP / W) <= MF_PS_ONE).
 // XNAT: natural activation layout (else fragment order, scales staged in LDS).
 // PART: also store every int32 group dot (test and debug entry point).
+// Arguments: what the common path reads fits the 14 preloaded argument
+// dwords (a later one is a scalar load the wave waits for): N, M - 1 and the
+// scale encoding share one word (nm: N in bits 0..26, M - 1 in 27..30, the
+// encoding in bit 31) and the first matrix's workgroup count is derived
+// from N (both matrices of a pair have N rows).
 template <int F, int T, int W, bool ONE, bool XNAT, bool PART>
 __global__ void __launch_bounds__(64 * W)
-qgemm_mfma_kernel(const int8_t* xq, const float* xs, int K, int M, int N, int nb0, int senc,
-                  const uint8_t* __restrict__ w, const uint16_t* __restrict__ ws, uint16_t* y,
-                  const uint16_t* res, int32_t* __restrict__ part, const uint8_t* __restrict__ w1,
-                  const uint16_t* __restrict__ ws1, uint16_t* y1) {
+qgemm_mfma_kernel(const int8_t* xq, const float* xs, const uint8_t* __restrict__ w,
+                  const uint16_t* __restrict__ ws, uint16_t* y, int K, unsigned nm, const uint16_t* res,
+                  int32_t* __restrict__ part, const uint8_t* __restrict__ w1, const uint16_t* __restrict__ ws1,
+                  uint16_t* y1) {
     using FT = Fmt<F>;
     constexpr int PS = ONE ? MF_PS_ONE : MF_PS_LOOP;
     constexpr bool NIB = F != 8;
@@ -128,8 +133,11 @@ qgemm_mfma_kernel(const int8_t* xq, const float* xs, int K, int M, int N, int nb
     const int CPR = K / FT::CK;
     const int cnt = (NP + W - 1) / W;
     const int nseg = ONE ? 1 : (cnt + PS - 1) / PS;
+    const int N = (int)(nm & ((1u << 27) - 1)), M = (int)((nm >> 27) & 15u) + 1;
+    const int senc = (int)(nm >> 31);
+    const int nb0 = (N + 16 * T - 1) / (16 * T);
     int bid = (int)blockIdx.x;
-    if (bid >= nb0) {  // second matrix of a fused pair
+    if (__builtin_expect(bid >= nb0, 0)) {  // second matrix of a fused pair
         bid -= nb0;
         w = w1;
         ws = ws1;
@@ -336,8 +344,8 @@ qgemm_mfma_kernel(const int8_t* xq, const float* xs, int K, int M, int N, int nb
 
 // ------------------------------------------------------------------ host side
 
-typedef void (*mf_fn)(const int8_t*, const float*, int, int, int, int, int, const uint8_t*, const uint16_t*,
-                      uint16_t*, const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*);
+typedef void (*mf_fn)(const int8_t*, const float*, const uint8_t*, const uint16_t*, uint16_t*, int, unsigned,
+                      const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*);
 
 struct MfShape {
     int t, w;
@@ -425,7 +433,9 @@ int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K,
     const uint8_t* b0 = (const uint8_t*)w1;
     const uint16_t* b1 = (const uint16_t*)s1;
     uint16_t* b2 = (uint16_t*)y1;
-    void* args[] = {&a3, &a4, &K, &M, &N, &nb0, &senc, &a0, &a1, &a5, &a6, &part, &b0, &b1, &b2};
+    if (N >= (1 << 27)) return VIPER_INVALID_ARGUMENT;  // N shares a word with M and the encoding
+    unsigned nm = (unsigned)N | ((unsigned)(M - 1) << 27) | (senc ? 1u << 31 : 0u);
+    void* args[] = {&a3, &a4, &a0, &a1, &a5, &K, &nm, &a6, &part, &b0, &b1, &b2};
     launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args, ev0, ev1);
     return status_of(hipGetLastError());
 }
