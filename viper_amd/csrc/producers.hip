@@ -22,14 +22,14 @@ constexpr int PR_NT = 256;  // threads per workgroup of the tiled (swiglu) kerne
 
 // Sum over the workgroup: DPP/permute butterfly in each wave, then the wave
 // sums in wave order.  Every thread gets the same value.
-__device__ __forceinline__ float block_sum(float v, float* red) {
+__device__ __forceinline__ float block_sum(float v, float* red, int nthreads) {
     v += dpp_f<DPP_SWAP1>(v);
     v += dpp_f<DPP_SWAP2>(v);
     v += dpp_f<DPP_HALF_MIRROR>(v);
     v += dpp_f<DPP_MIRROR>(v);
     v += __shfl_xor(v, 16, 64);
     v += __shfl_xor(v, 32, 64);
-    const int nw = (int)blockDim.x >> 6;
+    const int nw = nthreads >> 6;
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
     __syncthreads();
     float t = 0.0f;
@@ -68,15 +68,16 @@ __device__ __forceinline__ void quantize_store(const u32x4& v, bool ok, int o, i
     }
 }
 
-// One workgroup per row; blockDim a multiple of 64.
+// One workgroup per row; bd = the workgroup size, a multiple of 64 (an
+// argument rather than blockDim.x, which is a hidden argument the wave would
+// wait for before its first load).
 template <int G>
 __global__ void __launch_bounds__(1024)
 rmsnorm_quantize_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, float eps,
-                        int H, uint16_t* out, int8_t* __restrict__ xq, float* __restrict__ xs) {
+                        int H, uint16_t* out, int8_t* __restrict__ xq, float* __restrict__ xs, int bd) {
     __shared__ float red[16];
     const int row = (int)blockIdx.x;
     const int noct = H / 8;
-    const int bd = (int)blockDim.x;
     const int iters = (noct + bd - 1) / bd;
     const uint16_t* xr = x + (size_t)row * H;
 
@@ -90,7 +91,7 @@ rmsnorm_quantize_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
             for (int j = 0; j < 8; ++j) ss = __builtin_fmaf(f[j], f[j], ss);
         }
     }
-    ss = block_sum(ss, red);
+    ss = block_sum(ss, red, bd);
     const float inv = __builtin_amdgcn_rsqf(ss / (float)H + eps);
 
     int8_t* qr = xq + (size_t)row * H;
@@ -163,7 +164,8 @@ extern "C" int viper_hip_rmsnorm_quantize(const void* x_bf16, const void* gamma_
     uint16_t* a4 = (uint16_t*)out_bf16;
     int8_t* a5 = (int8_t*)xq;
     float* a6 = (float*)xs;
-    void* args[] = {&a0, &a1, &eps, &H, &a4, &a5, &a6};
+    int bdi = (int)bd;
+    void* args[] = {&a0, &a1, &eps, &H, &a4, &a5, &a6, &bdi};
     const void* fn = group == 64 ? (const void*)vq::rmsnorm_quantize_kernel<64>
                                  : (const void*)vq::rmsnorm_quantize_kernel<32>;
     (void)hipLaunchKernel(fn, dim3((unsigned)M), dim3(bd), args, 0, (hipStream_t)stream);
