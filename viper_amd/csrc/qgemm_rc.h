@@ -93,8 +93,11 @@ struct RcSeg {
     u32x2 S[QW][T];
 };
 
-// ONE: the quads of every wave fit one load segment.
-template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART>
+// ONE: the quads of every wave fit one load segment.  SE: the weight-scale
+// encoding, fp16 (0) or bf16 (1) as a constant for the production variants
+// (a run-time choice cost 0.1 us of the M = 16 verify), or read from nm (2)
+// for the partials and natural-layout variants.
+template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE>
 __global__ void __launch_bounds__(64 * W)
 qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
                 unsigned nm, const uint16_t* res, int32_t* __restrict__ part,
@@ -110,7 +113,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     const int NG = K / G, NQ = NG / 4;
     const int nseg = ONE ? 1 : (NQ + W * QW - 1) / (W * QW);
     const int N = (int)(nm & ((1u << 27) - 1)), M = (int)((nm >> 27) & 15u) + 1;
-    const bool senc = (nm >> 31) != 0;
+    const bool senc = SE == 2 ? (nm >> 31) != 0 : SE == 1;
     const int nb0 = (N + 8 * RB - 1) / (8 * RB);
     int bid = (int)blockIdx.x;
     // the second matrix of a fused pair and the residual are the rare paths:
@@ -414,42 +417,45 @@ __host__ __device__ constexpr int rc_rb_qw2(int F) { return F == 8 ? 6 : F == 6 
 constexpr int RC_RB_LOOP = 2;
 
 template <int F, int RB, int W, int QW, bool ONE>
-rc_fn rc_pick4(int am, bool part) {
+rc_fn rc_pick4(int am, bool part, int senc) {
     if (am == RC_NAT)
-        return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, true> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, false>;
+        return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, true, 2> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, false, 2>;
+    if (part)
+        return am == RC_BF16 ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, true, 2>
+                             : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, true, 2>;
     if (am == RC_BF16)
-        return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, true> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, false>;
-    return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, true> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, false>;
+        return senc ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, false, 1> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, false, 0>;
+    return senc ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, false, 1> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, false, 0>;
 }
 template <int F, int RB>
-rc_fn rc_pick3(const RcShape& s, int am, bool part) {
-    if (s.one && s.w == 4 && s.qw == 1) return rc_pick4<F, RB, 4, 1, true>(am, part);
-    if (s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, true>(am, part);
+rc_fn rc_pick3(const RcShape& s, int am, bool part, int senc) {
+    if (s.one && s.w == 4 && s.qw == 1) return rc_pick4<F, RB, 4, 1, true>(am, part, senc);
+    if (s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, true>(am, part, senc);
     if constexpr (RB <= rc_rb_qw2(F))
-        if (s.one && s.w == 10 && s.qw == 2) return rc_pick4<F, RB, 10, 2, true>(am, part);
+        if (s.one && s.w == 10 && s.qw == 2) return rc_pick4<F, RB, 10, 2, true>(am, part, senc);
     if constexpr (RB <= RC_RB_LOOP)
-        if (!s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, false>(am, part);
+        if (!s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, false>(am, part, senc);
     return nullptr;
 }
 template <int F>
-rc_fn rc_pick2(const RcShape& s, int am, bool part) {
+rc_fn rc_pick2(const RcShape& s, int am, bool part, int senc) {
     switch (s.rb) {
-        case 1: return rc_pick3<F, 1>(s, am, part);
-        case 2: return rc_pick3<F, 2>(s, am, part);
-        case 3: return rc_pick3<F, 3>(s, am, part);
-        case 4: return rc_pick3<F, 4>(s, am, part);
-        case 5: return rc_pick3<F, 5>(s, am, part);
-        case 6: return rc_pick3<F, 6>(s, am, part);
+        case 1: return rc_pick3<F, 1>(s, am, part, senc);
+        case 2: return rc_pick3<F, 2>(s, am, part, senc);
+        case 3: return rc_pick3<F, 3>(s, am, part, senc);
+        case 4: return rc_pick3<F, 4>(s, am, part, senc);
+        case 5: return rc_pick3<F, 5>(s, am, part, senc);
+        case 6: return rc_pick3<F, 6>(s, am, part, senc);
         default: return nullptr;
     }
 }
 
 // Kernels of format F (each defined in its own translation unit).
 template <int F>
-rc_fn rc_pick(const RcShape& s, int am, bool part);
+rc_fn rc_pick(const RcShape& s, int am, bool part, int senc);
 
 #define VQ_RC_PICK(F) \
     template <>       \
-    rc_fn rc_pick<F>(const RcShape& s, int am, bool part) { return rc_pick2<F>(s, am, part); }
+    rc_fn rc_pick<F>(const RcShape& s, int am, bool part, int senc) { return rc_pick2<F>(s, am, part, senc); }
 
 }  // namespace vq
