@@ -111,7 +111,11 @@ int viper_hip_abi_version(void);
 int viper_hip_group_size(int qtype);
 
 /* Bytes of caller workspace viper_hip_qlinear needs for this shape; 0 when
- * the activation quantize is fused into the GEMV (M == 1). */
+ * the activation quantize is fused into the GEMV (M == 1).  It holds the
+ * int8 activations and their scales, and for long K on the matrix cores
+ * (K of more than 20 quads of 4 groups) the K split's fp32 part sums and
+ * per-block counters.  Its contents need no initialisation; calls that use
+ * one workspace concurrently race. */
 size_t viper_hip_qlinear_workspace_bytes(int qtype, int N, int K, int M);
 
 /* y[M][N] = linear(w, x) with x[M][K] bf16 quantized per row and group.

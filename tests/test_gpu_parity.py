@@ -152,6 +152,42 @@ def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
     run_case(torch_dev, qtype, N, K, M, seed=3000 + N + M, scale_enc=senc, residual=(M % 2 == 1))
 
 
+# Long K on the matrix cores (K of 24..80 quads of 4 groups, a multiple of 4
+# quads) splits K in 4 parts, one workgroup each; the last part of a row block
+# to finish adds the parts' sums in part order.  The workspace starts as
+# garbage (the quantize launch clears the counters) and serves a second call
+# with another row count; a repeated call must give the same bits.
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("N,K,M,M2,senc", [
+    (2560, 10240, 16, 4, O.SCALE_FP16),   # down shape
+    (50, 10240, 7, 3, O.SCALE_BF16),      # ragged last row block
+    (1000, 6144, 12, 2, O.SCALE_FP16),    # 6 quads per part; M2 = 2 on the dot path
+    (333, 12288, 9, 16, O.SCALE_BF16),    # 12 quads per part (W8: 24, the segment loop)
+])
+def test_k_split(torch_dev, qtype, N, K, M, M2, senc):
+    torch = torch_dev
+    G = O.group_size(qtype)
+    packed, scales = O.gen_weights(qtype, N, K, 5100 + N, senc)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G,
+                           va.ScaleEnc(senc))
+    nws = max(va.workspace_bytes(qtype, N, K, m) for m in (M, M2))
+    ws = torch.full((nws,), 255, dtype=torch.uint8, device="cuda")
+    for m, residual in ((M, True), (M2, False)):
+        note(f"case qtype={qtype} N={N} K={K} M={m} senc={senc} res={residual}")
+        x = O.gen_act(m, K, 5200 + m)
+        res = O.gen_act(m, N, 5300 + m) if residual else None
+        y_ref, _, absterm = O.qlinear(qtype, packed, scales, senc, N, K, x, residual=res)
+        outs = []
+        for _ in range(2):
+            yd = torch.zeros((m, N), dtype=torch.int16, device="cuda")
+            rd = None if res is None else dev(torch, res)
+            assert va.linear(w, dev(torch, x), yd, residual=rd, workspace=ws).ok()
+            torch.cuda.synchronize()
+            outs.append(host(yd, np.uint16))
+        O.assert_bf16_close(outs[0], y_ref, absterm, rel=REL_TOL)
+        np.testing.assert_array_equal(outs[1], outs[0])
+
+
 # Q4 with K a multiple of 256 runs the row-contiguous matrix-core kernel: rows
 # per workgroup 8..48 (one workgroup per CU where N allows), one or two
 # 4-group quads per wave (K up to 2560, up to 5120), 4-wave workgroups for

@@ -403,11 +403,12 @@ bool mfma_staged(int qtype, int N, int K) {
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
                 const void* w1, const void* s1, void* y1, hipStream_t st, hipEvent_t ev0,
-                hipEvent_t ev1) {
+                hipEvent_t ev1, float* sp, unsigned* sc) {
     if (!mfma_ok(qtype, K, M, s)) return VIPER_INTERNAL;
     if (rc_ok(qtype, K))
         return launch_rc(qtype, w, s, senc, N, K, xq, xs, xnat ? RC_NAT : RC_FRAG, M, y, res, part, w1, s1, y1, st,
-                         ev0, ev1);
+                         ev0, ev1, sp, sc);
+    if (sp != nullptr) return VIPER_INTERNAL;
     const int NG = K / group_of(qtype);
     const int NP = NG / 2;
     const MfShape sh = mf_shape(N, NP, device_cus());

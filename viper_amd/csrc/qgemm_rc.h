@@ -96,26 +96,38 @@ struct RcSeg {
 // ONE: the quads of every wave fit one load segment.  SE: the weight-scale
 // encoding, fp16 (0) or bf16 (1) as a constant for the production variants
 // (a run-time choice cost 0.1 us of the M = 16 verify), or read from nm (2)
-// for the partials and natural-layout variants.
-template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE>
+// for the partials and natural-layout variants.  SK > 1 (fragment input
+// only): K split into SK equal parts, one workgroup per (row block, part),
+// blockIdx = SK * block + part; each part stores its fp32 sums to sp
+// [SK][M][N], and the last part of a block to arrive (counter sc[block],
+// zeroed by the fragment quantize launch) adds the SK sums in part order, so
+// the result does not depend on which part finishes last.
+template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, int SK = 1>
 __global__ void __launch_bounds__(64 * W)
 qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
                 unsigned nm, const uint16_t* res, int32_t* __restrict__ part,
-                const uint8_t* w1, const uint16_t* ws1, uint16_t* y1) {
+                const uint8_t* w1, const uint16_t* ws1, uint16_t* y1, float* __restrict__ sp,
+                unsigned* __restrict__ sc) {
     using FM = RcFmt<F>;
     using Seg = RcSeg<F, RB, QW>;
     constexpr int T = Seg::T;
     constexpr bool XNAT = AM == RC_NAT, XBF = AM == RC_BF16;
+    static_assert(SK == 1 || (AM == RC_FRAG && !PART), "the K split reads fragments and writes no partials");
     constexpr int G = F == 8 ? 32 : 64;
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = (int)threadIdx.x, L = tid & 63, wave = tid >> 6;
     const int n16 = L & 15, kb = L >> 4, qi = ((kb & 1) << 1) | (kb >> 1);
-    const int NG = K / G, NQ = NG / 4;
+    const int NG = K / G, NQ = NG / 4 / SK;  // quads of this workgroup's part of K
     const int nseg = ONE ? 1 : (NQ + W * QW - 1) / (W * QW);
     const int N = (int)(nm & ((1u << 27) - 1)), M = (int)((nm >> 27) & 15u) + 1;
     const bool senc = SE == 2 ? (nm >> 31) != 0 : SE == 1;
     const int nb0 = (N + 8 * RB - 1) / (8 * RB);
     int bid = (int)blockIdx.x;
+    int q0 = 0;  // first quad of the part
+    if constexpr (SK > 1) {
+        q0 = (int)(blockIdx.x % SK) * NQ;
+        bid = (int)(blockIdx.x / SK);
+    }
     // the second matrix of a fused pair and the residual are the rare paths:
     // marked unlikely, the common path is laid out and scheduled straight
     if (__builtin_expect(bid >= nb0, 0)) {
@@ -129,11 +141,14 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     const int nrows = min(8 * RB, N - row0);
     const int rbytes = NG * 32;              // main plane: 32 bytes per group
     const int hrb = NG * (FM::HQ / 4);       // high plane: HQ / 4 bytes per group
-    const auto wr = buf(w + (size_t)row0 * rbytes, (uint32_t)(nrows * rbytes));
-    const auto hr = buf(w + (size_t)N * rbytes + (size_t)row0 * hrb, (uint32_t)(nrows * hrb));
-    const auto sr = buf(ws + (size_t)row0 * NG, (uint32_t)(nrows * NG * 2));
-    const auto xr = buf(xq, XNAT ? (uint32_t)(M * K) : XBF ? (uint32_t)(M * K) * 2 : (uint32_t)NG * 64 * FM::QB);
-    const auto xsr = buf(xs, XNAT ? (uint32_t)(M * NG * 4) : XBF ? 0u : (uint32_t)NG * 64);
+    // (with a K split the resources start at the part's first quad: the
+    // offsets below stay those of an unsplit launch with NQ quads)
+    const auto wr = buf(w + (size_t)row0 * rbytes + q0 * 128, (uint32_t)(nrows * rbytes - q0 * 128));
+    const auto hr = buf(w + (size_t)N * rbytes + (size_t)row0 * hrb + q0 * FM::HQ, (uint32_t)(nrows * hrb - q0 * FM::HQ));
+    const auto sr = buf(ws + (size_t)row0 * NG + 4 * q0, (uint32_t)(nrows * NG - 4 * q0) * 2);
+    const auto xr = buf(xq + (size_t)q0 * 4 * 64 * FM::QB,
+                        XNAT ? (uint32_t)(M * K) : XBF ? (uint32_t)(M * K) * 2 : (uint32_t)(NG - 4 * q0) * 64 * FM::QB);
+    const auto xsr = buf(xs + (size_t)q0 * 4 * 16, XNAT ? (uint32_t)(M * NG * 4) : XBF ? 0u : (uint32_t)(NG - 4 * q0) * 64);
     const bool m_ok = n16 < M;  // A row of this lane
     // RC_BF16: the LDS fragments and scales (after the transpose buffers and
     // the cross-wave sums)
@@ -394,8 +409,40 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         const int m = 4 * kb + r, nl = 16 * t + n16;
         if (m < M && nl < nrows) {
             const size_t o = (size_t)m * N + row0 + nl;
-            if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
-            y[o] = f2bf(v);
+            if constexpr (SK > 1) {
+                __hip_atomic_store(sp + (size_t)(blockIdx.x % SK) * M * N + o, v, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
+                y[o] = f2bf(v);
+            }
+        }
+    }
+    if constexpr (SK > 1) {
+        // The parts' sums are device-coherent stores (sc1, through the
+        // XCD's L2); once every thread's stores have completed (vmcnt 0) the
+        // block's counter is incremented, and the last part reads the sums
+        // with device-coherent loads.  No device-scope fence: its L2
+        // write-back and invalidate per workgroup cost 70 us of the
+        // down-shape verify.
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        int* last = (int*)red;
+        if (tid == 0) last[0] = atomicAdd(sc + bid, 1u) == (unsigned)(SK - 1);
+        __syncthreads();
+        if (!last[0]) return;
+        for (int sl = wave; sl < 4 * T; sl += W) {
+            const int t = sl >> 2, r = sl & 3;
+            const int m = 4 * kb + r, nl = 16 * t + n16;
+            if (m < M && nl < nrows) {
+                const size_t o = (size_t)m * N + row0 + nl;
+                float v = 0.0f;
+#pragma unroll
+                for (int p = 0; p < SK; ++p)
+                    v += __hip_atomic_load(sp + (size_t)p * M * N + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
+                y[o] = f2bf(v);
+            }
         }
     }
 }
@@ -403,13 +450,14 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
 // ------------------------------------------------------------------ host side
 
 typedef void (*rc_fn)(const int8_t*, const float*, const uint8_t*, const uint16_t*, uint16_t*, int, unsigned,
-                      const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*);
+                      const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*, float*, unsigned*);
 
 // Launch shape: rows per workgroup (8 * rb), waves, quads per wave per
 // segment, single segment or double-buffered loop.
 struct RcShape {
     int rb, w, qw;
     bool one;
+    int sk = 1;  // parts of K (1: no split, else RC_SK)
 };
 // Most 8-row blocks per workgroup that two quads per wave, or the
 // double-buffered segment loop, hold in registers without spilling.
@@ -427,8 +475,20 @@ rc_fn rc_pick4(int am, bool part, int senc) {
         return senc ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, false, 1> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, false, 0>;
     return senc ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, false, 1> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, false, 0>;
 }
+template <int F, int RB, int QW>
+rc_fn rc_pick_split(int senc) {
+    return senc ? qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 1, RC_SK>
+                : qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 0, RC_SK>;
+}
 template <int F, int RB>
 rc_fn rc_pick3(const RcShape& s, int am, bool part, int senc) {
+    if (s.sk != 1) {  // K split: fragment input, one segment of 10 waves
+        if (s.sk != RC_SK || am != RC_FRAG || part || !s.one || s.w != 10) return nullptr;
+        if (s.qw == 1) return rc_pick_split<F, RB, 1>(senc);
+        if constexpr (RB <= rc_rb_qw2(F))
+            if (s.qw == 2) return rc_pick_split<F, RB, 2>(senc);
+        return nullptr;
+    }
     if (s.one && s.w == 4 && s.qw == 1) return rc_pick4<F, RB, 4, 1, true>(am, part, senc);
     if (s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, true>(am, part, senc);
     if constexpr (RB <= rc_rb_qw2(F))

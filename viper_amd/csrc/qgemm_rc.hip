@@ -32,6 +32,34 @@ static RcShape rc_shape(int F, int rows_total, int NQ, int cus) {
     return s;
 }
 
+// K split (fragment input): K whose unsplit shape is the segment loop, in
+// RC_SK parts that each fit one segment of 10 waves (one or two quads per
+// wave); rows per workgroup spread the RC_SK * N (row, part) pairs over one
+// workgroup per CU.  Down shape K = 10240, N = 2560: 64 blocks of 40 rows x 4
+// parts instead of 160 blocks of 16 rows that each read all of K's
+// activation.
+static bool rc_split_fits(int NQ) { return NQ > 20 && NQ % RC_SK == 0 && NQ / RC_SK <= 20; }
+
+static bool rc_split_shape(int F, int N, int NQ, int cus, RcShape& s) {
+    if (!rc_split_fits(NQ)) return false;
+    s.w = 10;
+    s.one = true;
+    s.qw = NQ / RC_SK <= 10 ? 1 : 2;
+    s.sk = RC_SK;
+    const int rb = (RC_SK * N + 8 * cus - 1) / (8 * cus), rbmax = s.qw == 2 ? rc_rb_qw2(F) : 6;
+    s.rb = rb < 1 ? 1 : (rb > rbmax ? rbmax : rb);
+    return true;
+}
+
+bool rc_split_ok(int qtype, int K) {
+    const int G = group_of(qtype);
+    return G != 0 && K % (4 * G) == 0 && rc_split_fits(K / G / 4);
+}
+
+size_t rc_split_bytes(int N, int M) {
+    return align16((size_t)RC_SK * M * N * 4) + align16((size_t)rc_split_counters(N) * 4);
+}
+
 bool rc_ok(int qtype, int K) {
     const int G = group_of(qtype);
     return G != 0 && K % (4 * G) == 0;
@@ -67,11 +95,17 @@ bool rc_bf16_ok(int qtype, int N, int K, int M, bool pair) {
 
 int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq, const void* xs,
               int am, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
-              hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+              hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, float* sp, unsigned* sc) {
     if (!rc_ok(qtype, K) || M < 2 || M > 16) return VIPER_INTERNAL;
     if (N >= (1 << 27)) return VIPER_INVALID_ARGUMENT;  // N shares a word with M and the encoding
     if (am == RC_BF16 && !rc_bf16_ok(qtype, N, K, M, w1 != nullptr)) return VIPER_INTERNAL;
-    const RcShape sh = rc_launch_shape(qtype, w1 != nullptr ? 2 * N : N, K);
+    RcShape sh = rc_launch_shape(qtype, w1 != nullptr ? 2 * N : N, K);
+    if (sp != nullptr) {
+        const int F = qtype == VIPER_QTYPE_W8_G32 ? 8 : qtype;
+        if (am != RC_FRAG || part != nullptr || w1 != nullptr || sc == nullptr ||
+            !rc_split_shape(F, N, K / group_of(qtype) / 4, device_cus(), sh))
+            return VIPER_INTERNAL;
+    }
     rc_fn fn;
     switch (qtype) {
         case VIPER_QTYPE_Q4_G64: fn = rc_pick<4>(sh, am, part != nullptr, senc); break;
@@ -81,7 +115,8 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     }
     if (fn == nullptr) return VIPER_INTERNAL;
     int nb0 = (N + 8 * sh.rb - 1) / (8 * sh.rb);
-    const unsigned grid = (unsigned)(w1 != nullptr ? 2 * nb0 : nb0);
+    const unsigned grid = (unsigned)(w1 != nullptr ? 2 * nb0 : nb0 * sh.sk);
+    if (sh.sk > 1 && nb0 > rc_split_counters(N)) return VIPER_INTERNAL;
     const size_t lds = rc_launch_lds(qtype, sh, K, am);
     const int8_t* a0 = (const int8_t*)xq;
     const float* a1 = (const float*)xs;
@@ -93,7 +128,7 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     const uint16_t* b1 = (const uint16_t*)s1;
     uint16_t* b2 = (uint16_t*)y1;
     unsigned nm = (unsigned)N | ((unsigned)(M - 1) << 27) | (senc ? 1u << 31 : 0u);  // see the kernel's arguments note
-    void* args[] = {&a0, &a1, &a2, &a3, &a4, &K, &nm, &a5, &part, &b0, &b1, &b2};
+    void* args[] = {&a0, &a1, &a2, &a3, &a4, &K, &nm, &a5, &part, &b0, &b1, &b2, &sp, &sc};
     launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args, ev0, ev1);
     return status_of(hipGetLastError());
 }

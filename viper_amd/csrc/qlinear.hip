@@ -35,11 +35,18 @@ namespace vq {
 // MF: the fragment order the matrix-core kernels read (xs transposed to
 // [K/G][16]; 64-groups use quantize_frag64_kernel); else xq [M][K] in k order
 // and xs [M][K/G].
+// Both fragment-order quantizers also clear the ncnt counters of a K-split
+// matrix-core launch that follows (written through, like their outputs).
 template <int G, bool MF>
 __global__ void __launch_bounds__(NT)
 quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
-                    float* __restrict__ xs, int oct_total, int K) {
+                    float* __restrict__ xs, int oct_total, int K, unsigned* __restrict__ cnt, int ncnt) {
     const int o = (int)blockIdx.x * NT + (int)threadIdx.x;
+    if constexpr (MF) {
+        const int stride = (oct_total + NT - 1) / NT * NT;
+        const auto cw = buf(cnt, (uint32_t)ncnt * 4u);
+        for (int i = o; i < ncnt; i += stride) bstore4<AUX_SC1>(cw, i * 4, 0u);
+    }
     const bool ok = o < oct_total;
     u32x4 v = {0u, 0u, 0u, 0u};
     if (ok) v = *(const u32x4*)(x + (size_t)o * 8);
@@ -75,8 +82,13 @@ quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
 // group amax is the max over the 4 lanes of row m (lanes m, m + 16, m + 32,
 // m + 48).  Rows m >= M are neither read nor written.
 __global__ void __launch_bounds__(64)
-quantize_frag64_kernel(const uint16_t* x, int M, int K, int8_t* __restrict__ xq, float* __restrict__ xs) {
+quantize_frag64_kernel(const uint16_t* x, int M, int K, int8_t* __restrict__ xq, float* __restrict__ xs,
+                       unsigned* __restrict__ cnt, int ncnt) {
     const int L = (int)threadIdx.x, g = (int)blockIdx.x;
+    {
+        const auto cw = buf(cnt, (uint32_t)ncnt * 4u);
+        for (int i = g * 64 + L; i < ncnt; i += K) bstore4<AUX_SC1>(cw, i * 4, 0u);  // K threads in the grid
+    }
     const int m = L & 15, kb = L >> 4, qi = ((kb & 1) << 1) | (kb >> 1);
     const bool ok = m < M;
     const auto xr = buf(x, (uint32_t)M * (uint32_t)K * 2u);
@@ -156,18 +168,19 @@ __global__ void __launch_bounds__(SR_NT) stream_read_kernel(const uint8_t* p, ui
 }
 
 static int launch_quantize(int group, const void* x, int M, int K, void* xq, void* xs, bool mf,
-                           hipStream_t st) {
+                           hipStream_t st, unsigned* cnt = nullptr, int ncnt = 0) {
     const int oct_total = M * K / 8;
     const unsigned grid = (unsigned)((oct_total + NT - 1) / NT);
     const uint16_t* a0 = (const uint16_t*)x;
     int8_t* a1 = (int8_t*)xq;
     float* a2 = (float*)xs;
+    if (ncnt > 0 && !mf) return VIPER_INTERNAL;
     if (mf && group == 64) {
-        void* fargs[] = {&a0, &M, &K, &a1, &a2};
+        void* fargs[] = {&a0, &M, &K, &a1, &a2, &cnt, &ncnt};
         launch((const void*)quantize_frag64_kernel, (unsigned)(K / 64), 64, 0, st, fargs, nullptr, nullptr);
         return status_of(hipGetLastError());
     }
-    void* args[] = {&a0, &a1, &a2, (void*)&oct_total, &K};
+    void* args[] = {&a0, &a1, &a2, (void*)&oct_total, &K, &cnt, &ncnt};
     const void* fn;
     if (group == 64) fn = (const void*)quantize_act_kernel<64, false>;
     else fn = mf ? (const void*)quantize_act_kernel<32, true> : (const void*)quantize_act_kernel<32, false>;
@@ -181,13 +194,19 @@ static bool fused_ok(int qtype, int M, int K) {
     return M == 1 && lds_m1(qtype, K) <= (size_t)LDS_MAX;
 }
 
-static size_t workspace_need(int qtype, int K, int M) {
+// xq ([M][K], or fragment order with room for 16 rows), then xs ([M][K/G],
+// or [K/G][16]) fp32, then (long K on the matrix cores) the K split's part
+// sums and counters.
+static size_t workspace_xq(int K) { return align16((size_t)16 * K); }
+static size_t workspace_xs(int qtype, int K) { return align16((size_t)(K / group_of(qtype)) * 16 * 4); }
+
+static size_t workspace_need(int qtype, int N, int K, int M) {
     const int G = group_of(qtype);
-    if (G == 0 || M <= 0 || K <= 0) return 0;
+    if (G == 0 || M <= 0 || K <= 0 || N <= 0) return 0;
     if (fused_ok(qtype, M, K)) return 0;
-    // xq ([M][K], or fragment order with room for 16 rows), then xs ([M][K/G],
-    // or [K/G][16]) fp32
-    return align16((size_t)16 * K) + (size_t)(K / G) * 16 * 4;
+    size_t need = workspace_xq(K) + workspace_xs(qtype, K);
+    if (M >= 2 && M <= 16 && rc_split_ok(qtype, K)) need += rc_split_bytes(N, M);
+    return need;
 }
 
 // Optional second matrix of the same shape applied to the same activation in
@@ -223,7 +242,7 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
         return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, b.w ? 2 : 1, res, part, st,
                          ev0, ev1);
     }
-    const size_t need = workspace_need(qtype, K, M);
+    const size_t need = workspace_need(qtype, N, K, M);
     if (wsp == nullptr || wsp_bytes < need || misaligned(wsp, 16)) return VIPER_INVALID_ARGUMENT;
     // Few rows: every workgroup quantizes the rows itself, one launch (the
     // workspace stays required for M > 1 whichever kernel runs).  Two rows of
@@ -237,11 +256,15 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
         const M1Out outs[1] = {{w, s, y, N}};
         return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, ev0, ev1, M);
     }
-    if (mf && M >= 3 && M <= 8 && rc_bf16_ok(qtype, N, K, M, b.w != nullptr))
+    // (long K splits over workgroups in the two-launch path instead: down
+    // shape K = 10240, 4 rows 9.9 us against 10.3 us)
+    const bool split_ok = mf && b.w == nullptr && part == nullptr && rc_split_ok(qtype, K);
+    if (mf && M >= 3 && M <= 8 && !split_ok && rc_bf16_ok(qtype, N, K, M, b.w != nullptr))
         return launch_rc(qtype, w, s, senc, N, K, x, nullptr, RC_BF16, M, y, res, part, b.w, b.s, b.y, st, ev0, ev1);
     // (3 or 4 rows here where the LDS copy does not fit: while every
     // workgroup's share of the rows' quantize stays small; down shape
-    // K = 10240: 3 rows 8.8 us against 10.1 us for two launches, 4 rows 10.4 us)
+    // K = 10240: 3 rows 8.8 us against 9.9 us for two launches with the K
+    // split)
     if (b.w == nullptr && m1_rows_ok(qtype, K, M) && (long)M * K <= 32768) {
         const M1Out outs[1] = {{w, s, y, N}};
         return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, ev0, ev1, M);
@@ -249,12 +272,16 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     const bool staged = mf && mfma_staged(qtype, N, K);
     if (!mf && lds_pre(qtype, M, K) > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
     uint8_t* xq = (uint8_t*)wsp;
-    float* xs = (float*)(xq + align16((size_t)16 * K));
-    rc = launch_quantize(group, x, M, K, xq, xs, staged, st);
+    float* xs = (float*)(xq + workspace_xq(K));
+    // long K on the matrix cores: the K split (parts' sums and counters after xs)
+    const bool split = split_ok;
+    float* sp = split ? (float*)((uint8_t*)xs + workspace_xs(qtype, K)) : nullptr;
+    unsigned* sc = split ? (unsigned*)((uint8_t*)sp + align16((size_t)RC_SK * M * N * 4)) : nullptr;
+    rc = launch_quantize(group, x, M, K, xq, xs, staged, st, sc, split ? rc_split_counters(N) : 0);
     if (rc != VIPER_OK) return rc;
     if (mf)
         return launch_mfma(qtype, w, s, senc, N, K, xq, xs, !staged, M, y, res, part, b.w, b.s, b.y,
-                           st, ev0, ev1);
+                           st, ev0, ev1, sp, sc);
     rc = launch_pre(qtype, w, s, senc, N, K, xq, xs, M, y, res, part, st, ev0, ev1);
     if (rc == VIPER_OK && b.w != nullptr)
         rc = launch_pre(qtype, b.w, b.s, senc, N, K, xq, xs, M, b.y, nullptr, nullptr, st, nullptr, nullptr);
@@ -301,7 +328,7 @@ extern "C" int viper_hip_group_size(int qtype) { return vq::group_of(qtype); }
 
 extern "C" size_t viper_hip_qlinear_workspace_bytes(int qtype, int N, int K, int M) {
     (void)N;
-    return vq::workspace_need(qtype, K, M);
+    return vq::workspace_need(qtype, N, K, M);
 }
 
 extern "C" int viper_hip_qlinear(int qtype, const void* w_packed, const void* w_scales,

@@ -128,13 +128,21 @@ bool mfma_ok(int qtype, int K, int M, const void* s);
 enum { RC_FRAG = 0, RC_NAT = 1, RC_BF16 = 2 };
 bool rc_ok(int qtype, int K);
 bool rc_bf16_ok(int qtype, int N, int K, int M, bool pair);
+// K split of the fragment-input launch (long K): sp = fp32 part sums
+// [4][M][N], sc = one counter per row block, at most rc_split_counters(N),
+// zero when the launch starts (the fragment quantize clears them); both in
+// the caller's workspace, rc_split_bytes(N, M) bytes.
+constexpr int RC_SK = 4;  // parts of the K split
+bool rc_split_ok(int qtype, int K);
+inline int rc_split_counters(int N) { return (N + 7) / 8; }
+size_t rc_split_bytes(int N, int M);
 int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq, const void* xs,
               int am, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
-              hipStream_t st, hipEvent_t ev0, hipEvent_t ev1);
+              hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, float* sp = nullptr, unsigned* sc = nullptr);
 bool mfma_staged(int qtype, int N, int K);
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
                 const void* w1, const void* s1, void* y1, hipStream_t st, hipEvent_t ev0,
-                hipEvent_t ev1);
+                hipEvent_t ev1, float* sp = nullptr, unsigned* sc = nullptr);
 
 }  // namespace vq
