@@ -259,7 +259,14 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     // (long K splits over workgroups in the two-launch path instead: down
     // shape K = 10240, 4 rows 9.9 us against 10.3 us)
     const bool split_ok = mf && b.w == nullptr && part == nullptr && rc_split_ok(qtype, K);
-    if (mf && M >= 3 && M <= 8 && !split_ok && rc_bf16_ok(qtype, N, K, M, b.w != nullptr))
+    // Q5/Q6/W8 (K = 2560, N = 10240, 5% outlier channels): 3 or 4 rows run
+    // faster on the dot kernel below (Q5 4 rows 7.86 against 8.10 us) or in
+    // two launches (W8 3 rows 8.37 against 9.23 us), and Q5/Q6 8 rows in two
+    // launches (8.65 / 8.89 against 9.01 / 9.10 us); 6 rows of every format
+    // and 8 of W8 stay here.
+    const bool hi = qtype == VIPER_QTYPE_Q5_G64 || qtype == VIPER_QTYPE_Q6_G64;
+    const bool bf_ok = mf && M >= 3 && M <= (hi ? 7 : 8) && !split_ok && rc_bf16_ok(qtype, N, K, M, b.w != nullptr);
+    if (bf_ok && (qtype == VIPER_QTYPE_Q4_G64 || M > 4))
         return launch_rc(qtype, w, s, senc, N, K, x, nullptr, RC_BF16, M, y, res, part, b.w, b.s, b.y, st, ev0, ev1);
     // (3 or 4 rows here where the LDS copy does not fit: while every
     // workgroup's share of the rows' quantize stays small; down shape
