@@ -101,8 +101,9 @@ struct RcSeg {
 // blockIdx = SK * block + part; each part stores its fp32 sums to sp
 // [SK][M][N], and the last part of a block to arrive (counter sc[block],
 // zeroed by the fragment quantize launch) adds the SK sums in part order, so
-// the result does not depend on which part finishes last.
-template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, int SK = 1>
+// the result does not depend on which part finishes last.  PR: the launch
+// may carry a fused pair (without it the matrix select is not compiled).
+template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, int SK = 1, bool PR = true>
 __global__ void __launch_bounds__(64 * W)
 qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
                 unsigned nm, const uint16_t* res, int32_t* __restrict__ part,
@@ -130,7 +131,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     }
     // the second matrix of a fused pair and the residual are the rare paths:
     // marked unlikely, the common path is laid out and scheduled straight
-    if (__builtin_expect(bid >= nb0, 0)) {
+    if (PR && __builtin_expect(bid >= nb0, 0)) {
         bid -= nb0;
         w = w1;
         ws = ws1;
@@ -464,24 +465,29 @@ struct RcShape {
 __host__ __device__ constexpr int rc_rb_qw2(int F) { return F == 8 ? 6 : F == 6 ? 3 : 4; }
 constexpr int RC_RB_LOOP = 2;
 
+template <int F, int RB, int W, int QW, bool ONE, int AM, int SE>
+rc_fn rc_pick5(bool pair) {
+    return pair ? qgemm_rc_kernel<F, RB, W, QW, ONE, AM, false, SE, 1, true>
+                : qgemm_rc_kernel<F, RB, W, QW, ONE, AM, false, SE, 1, false>;
+}
 template <int F, int RB, int W, int QW, bool ONE>
-rc_fn rc_pick4(int am, bool part, int senc) {
+rc_fn rc_pick4(int am, bool part, int senc, bool pair) {
     if (am == RC_NAT)
         return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, true, 2> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, false, 2>;
     if (part)
         return am == RC_BF16 ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, true, 2>
                              : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, true, 2>;
     if (am == RC_BF16)
-        return senc ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, false, 1> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, false, 0>;
-    return senc ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, false, 1> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, false, 0>;
+        return senc ? rc_pick5<F, RB, W, QW, ONE, RC_BF16, 1>(pair) : rc_pick5<F, RB, W, QW, ONE, RC_BF16, 0>(pair);
+    return senc ? rc_pick5<F, RB, W, QW, ONE, RC_FRAG, 1>(pair) : rc_pick5<F, RB, W, QW, ONE, RC_FRAG, 0>(pair);
 }
 template <int F, int RB, int QW>
 rc_fn rc_pick_split(int senc) {
-    return senc ? qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 1, RC_SK>
-                : qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 0, RC_SK>;
+    return senc ? qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 1, RC_SK, false>
+                : qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 0, RC_SK, false>;
 }
 template <int F, int RB>
-rc_fn rc_pick3(const RcShape& s, int am, bool part, int senc) {
+rc_fn rc_pick3(const RcShape& s, int am, bool part, int senc, bool pair) {
     if (s.sk != 1) {  // K split: fragment input, one segment of 10 waves
         if (s.sk != RC_SK || am != RC_FRAG || part || !s.one || s.w != 10) return nullptr;
         if (s.qw == 1) return rc_pick_split<F, RB, 1>(senc);
@@ -489,33 +495,33 @@ rc_fn rc_pick3(const RcShape& s, int am, bool part, int senc) {
             if (s.qw == 2) return rc_pick_split<F, RB, 2>(senc);
         return nullptr;
     }
-    if (s.one && s.w == 4 && s.qw == 1) return rc_pick4<F, RB, 4, 1, true>(am, part, senc);
-    if (s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, true>(am, part, senc);
+    if (s.one && s.w == 4 && s.qw == 1) return rc_pick4<F, RB, 4, 1, true>(am, part, senc, pair);
+    if (s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, true>(am, part, senc, pair);
     if constexpr (RB <= rc_rb_qw2(F))
-        if (s.one && s.w == 10 && s.qw == 2) return rc_pick4<F, RB, 10, 2, true>(am, part, senc);
+        if (s.one && s.w == 10 && s.qw == 2) return rc_pick4<F, RB, 10, 2, true>(am, part, senc, pair);
     if constexpr (RB <= RC_RB_LOOP)
-        if (!s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, false>(am, part, senc);
+        if (!s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, false>(am, part, senc, pair);
     return nullptr;
 }
 template <int F>
-rc_fn rc_pick2(const RcShape& s, int am, bool part, int senc) {
+rc_fn rc_pick2(const RcShape& s, int am, bool part, int senc, bool pair) {
     switch (s.rb) {
-        case 1: return rc_pick3<F, 1>(s, am, part, senc);
-        case 2: return rc_pick3<F, 2>(s, am, part, senc);
-        case 3: return rc_pick3<F, 3>(s, am, part, senc);
-        case 4: return rc_pick3<F, 4>(s, am, part, senc);
-        case 5: return rc_pick3<F, 5>(s, am, part, senc);
-        case 6: return rc_pick3<F, 6>(s, am, part, senc);
+        case 1: return rc_pick3<F, 1>(s, am, part, senc, pair);
+        case 2: return rc_pick3<F, 2>(s, am, part, senc, pair);
+        case 3: return rc_pick3<F, 3>(s, am, part, senc, pair);
+        case 4: return rc_pick3<F, 4>(s, am, part, senc, pair);
+        case 5: return rc_pick3<F, 5>(s, am, part, senc, pair);
+        case 6: return rc_pick3<F, 6>(s, am, part, senc, pair);
         default: return nullptr;
     }
 }
 
 // Kernels of format F (each defined in its own translation unit).
 template <int F>
-rc_fn rc_pick(const RcShape& s, int am, bool part, int senc);
+rc_fn rc_pick(const RcShape& s, int am, bool part, int senc, bool pair);
 
 #define VQ_RC_PICK(F) \
     template <>       \
-    rc_fn rc_pick<F>(const RcShape& s, int am, bool part, int senc) { return rc_pick2<F>(s, am, part, senc); }
+    rc_fn rc_pick<F>(const RcShape& s, int am, bool part, int senc, bool pair) { return rc_pick2<F>(s, am, part, senc, pair); }
 
 }  // namespace vq

@@ -108,10 +108,10 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     }
     rc_fn fn;
     switch (qtype) {
-        case VIPER_QTYPE_Q4_G64: fn = rc_pick<4>(sh, am, part != nullptr, senc); break;
-        case VIPER_QTYPE_Q5_G64: fn = rc_pick<5>(sh, am, part != nullptr, senc); break;
-        case VIPER_QTYPE_Q6_G64: fn = rc_pick<6>(sh, am, part != nullptr, senc); break;
-        default: fn = rc_pick<8>(sh, am, part != nullptr, senc); break;
+        case VIPER_QTYPE_Q4_G64: fn = rc_pick<4>(sh, am, part != nullptr, senc, w1 != nullptr); break;
+        case VIPER_QTYPE_Q5_G64: fn = rc_pick<5>(sh, am, part != nullptr, senc, w1 != nullptr); break;
+        case VIPER_QTYPE_Q6_G64: fn = rc_pick<6>(sh, am, part != nullptr, senc, w1 != nullptr); break;
+        default: fn = rc_pick<8>(sh, am, part != nullptr, senc, w1 != nullptr); break;
     }
     if (fn == nullptr) return VIPER_INTERNAL;
     int nb0 = (N + 8 * sh.rb - 1) / (8 * sh.rb);
