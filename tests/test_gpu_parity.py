@@ -188,6 +188,49 @@ def test_k_split(torch_dev, qtype, N, K, M, M2, senc):
         np.testing.assert_array_equal(outs[1], outs[0])
 
 
+# The K split captured in a HIP graph (its counters are cleared by the
+# quantize launch inside the graph, no memset node): every replay, with an
+# eager call of another row count on the same workspace between replays,
+# equals the eager result bit for bit.
+def test_k_split_graph_replays(torch_dev):
+    torch = torch_dev
+    qtype, N, K, M, M2 = O.Q4_G64, 2560, 10240, 8, 5
+    packed, scales = O.gen_weights(qtype, N, K, 5400, O.SCALE_FP16)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, 64,
+                           va.ScaleEnc(O.SCALE_FP16))
+    x, x2 = O.gen_act(M, K, 5401), O.gen_act(M2, K, 5402)
+    res = O.gen_act(M, N, 5403)
+    xd, x2d, rd = dev(torch, x), dev(torch, x2), dev(torch, res)
+    ws = torch.full((max(va.workspace_bytes(qtype, N, K, m) for m in (M, M2)),), 255, dtype=torch.uint8,
+                    device="cuda")
+    ye = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    assert va.linear(w, xd, ye, residual=rd, workspace=ws).ok()
+    torch.cuda.synchronize()
+    y_eager = host(ye, np.uint16)
+    y_ref, _, absterm = O.qlinear(qtype, packed, scales, O.SCALE_FP16, N, K, x, residual=res)
+    O.assert_bf16_close(y_eager, y_ref, absterm, rel=REL_TOL)
+    yg = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    y2 = torch.zeros((M2, N), dtype=torch.int16, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        assert va.linear(w, xd, yg, residual=rd, workspace=ws).ok()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = va.linear(w, xd, yg, residual=rd, workspace=ws)
+    assert st.ok()
+    for i in range(3):
+        note(f"replay {i}")
+        yg.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(yg, np.uint16), y_eager)
+        assert va.linear(w, x2d, y2, workspace=ws).ok()   # eager, same workspace
+        torch.cuda.synchronize()
+
+
 # Q4 with K a multiple of 256 runs the row-contiguous matrix-core kernel: rows
 # per workgroup 8..48 (one workgroup per CU where N allows), one or two
 # 4-group quads per wave (K up to 2560, up to 5120), 4-wave workgroups for
