@@ -188,6 +188,29 @@ def test_k_split(torch_dev, qtype, N, K, M, M2, senc):
         np.testing.assert_array_equal(outs[1], outs[0])
 
 
+# Seeded random shapes on the K split: K of 24..80 quads (every multiple of
+# 4 quads the split takes: one or two quads per wave and part), ragged N,
+# rows past the multi-row bound, both scale encodings, residual on odd M.
+def _k_split_shapes(n=12, seed=0x5EED5):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        qtype = FORMATS[i % len(FORMATS)]
+        G = O.group_size(qtype)
+        nq = int(rng.choice([24, 28, 32, 36, 40, 48, 56, 64, 72, 80]))
+        K = nq * 4 * G
+        M = int(rng.integers(max(4, 32768 // K + 1), 17))
+        N = int(rng.integers(1, 3000))
+        out.append((qtype, N, K, M, int(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("qtype,N,K,M,senc", _k_split_shapes())
+def test_k_split_random_shapes(torch_dev, qtype, N, K, M, senc):
+    run_case(torch_dev, qtype, N, K, M, seed=5500 + N, scale_enc=senc, residual=(M % 2 == 1),
+             check_partials=False)
+
+
 # The K split captured in a HIP graph (its counters are cleared by the
 # quantize launch inside the graph, no memset node): every replay, with an
 # eager call of another row count on the same workspace between replays,
