@@ -34,10 +34,11 @@ static RcShape rc_shape(int F, int rows_total, int NQ, int cus) {
 
 // K split (fragment input): K whose unsplit shape is the segment loop, in
 // RC_SK parts that each fit one segment of 10 waves (one or two quads per
-// wave); rows per workgroup spread the RC_SK * N (row, part) pairs over one
-// workgroup per CU.  Down shape K = 10240, N = 2560: 64 blocks of 40 rows x 4
-// parts instead of 160 blocks of 16 rows that each read all of K's
-// activation.
+// wave); rows per workgroup spread the RC_SK * N (row, part) pairs over two
+// workgroups per CU.  Down shape K = 10240, N = 2560: 107 blocks of 24 rows x
+// 4 parts instead of 160 blocks of 16 rows that each read all of K's
+// activation (M = 4 / 8 / 16: 9.47 / 9.45 / 9.87 us; 40 rows, one workgroup
+// per CU: 9.9 / 9.8 / 10.0 us; 16 rows 11.3 / 11.6 / 11.9 us).
 static bool rc_split_fits(int NQ) { return NQ > 20 && NQ % RC_SK == 0 && NQ / RC_SK <= 20; }
 
 static bool rc_split_shape(int F, int N, int NQ, int cus, RcShape& s) {
@@ -46,7 +47,7 @@ static bool rc_split_shape(int F, int N, int NQ, int cus, RcShape& s) {
     s.one = true;
     s.qw = NQ / RC_SK <= 10 ? 1 : 2;
     s.sk = RC_SK;
-    const int rb = (RC_SK * N + 8 * cus - 1) / (8 * cus), rbmax = s.qw == 2 ? rc_rb_qw2(F) : 6;
+    const int rb = (RC_SK * N + 16 * cus - 1) / (16 * cus), rbmax = s.qw == 2 ? rc_rb_qw2(F) : 6;
     s.rb = rb < 1 ? 1 : (rb > rbmax ? rbmax : rb);
     return true;
 }
