@@ -257,7 +257,7 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
         return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, ev0, ev1, M);
     }
     // (long K splits over workgroups in the two-launch path instead: down
-    // shape K = 10240, 4 rows 9.9 us against 10.3 us)
+    // shape K = 10240, 4 rows 9.5 us against 10.3 us)
     const bool split_ok = mf && b.w == nullptr && part == nullptr && rc_split_ok(qtype, K);
     // Q5/Q6/W8 (K = 2560, N = 10240, 5% outlier channels): 3 or 4 rows run
     // faster on the dot kernel below (Q5 4 rows 7.86 against 8.10 us) or in
@@ -270,7 +270,7 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
         return launch_rc(qtype, w, s, senc, N, K, x, nullptr, RC_BF16, M, y, res, part, b.w, b.s, b.y, st, ev0, ev1);
     // (3 or 4 rows here where the LDS copy does not fit: while every
     // workgroup's share of the rows' quantize stays small; down shape
-    // K = 10240: 3 rows 8.8 us against 9.9 us for two launches with the K
+    // K = 10240: 3 rows 8.8 us against about 9.5 us for two launches with the K
     // split)
     if (b.w == nullptr && m1_rows_ok(qtype, K, M) && (long)M * K <= 32768) {
         const M1Out outs[1] = {{w, s, y, N}};
