@@ -49,7 +49,11 @@ usize packed_bytes(QType q, i64 rows, i64 cols) noexcept;
 DType dtype_of(QType q) noexcept;
 
 // Device view of one quantized matrix (reference quant.h:34-41) plus the
-// scale encoding, which the reference leaves implicit.
+// scale encoding, which the reference leaves implicit.  The encoding defaults
+// to bf16, what the reference's converter writes (convert.cpp:109-113) and
+// its engine decodes (dp4a_smem_kernel.cu:27,61), so a caller that fills only
+// the reference's six fields over reference-converted weights decodes them
+// correctly; fp16 scales (BASELINE's synthetic weights) must be stated.
 struct QuantizedWeight {
     QType qtype = QType::BF16;
     void* data = nullptr;    // device pointer to packed weights
@@ -57,7 +61,7 @@ struct QuantizedWeight {
     i32 rows = 0;            // output channels (N)
     i32 cols = 0;            // input channels (K)
     i32 group_size = 64;     // 64 for Q*_G64, 32 for W8_G32
-    ScaleEnc scale_enc = ScaleEnc::FP16;
+    ScaleEnc scale_enc = ScaleEnc::BF16;
 };
 
 // Lossy-vs-lossless delta report (reference quant.h:44-50).

@@ -46,8 +46,6 @@
  *   viper_hip_sampling_greedy       sampling_greedy_bf16 (kernels/ops/sampling_kernel.cu:66-80).
  *   viper_hip_qlinear_partials      no counterpart: the same kernels, also writing
  *                                   the exact per-group int32 dots for parity tests.
- *   viper_hip_qlinear_timed         no counterpart: viper_hip_qlinear with events
- *                                   attached to the GEMV dispatch (benchmarking).
  *   viper_hip_check_quantizer       no counterpart: device self-check of the
  *                                   activation quantizer's rounding.
  *   viper_hip_stream_read           no counterpart: reads a buffer once with the
@@ -103,7 +101,7 @@ extern "C" {
 #define VIPER_SCALE_BF16 1
 
 #define VIPER_QLINEAR_MAX_M 16
-#define VIPER_QLINEAR_ABI_VERSION 2
+#define VIPER_QLINEAR_ABI_VERSION 3
 
 int viper_hip_abi_version(void);
 
@@ -212,14 +210,6 @@ int viper_hip_linear_bf16(const void* w_bf16, const void* x_bf16, void* y_bf16, 
 /* out_token[b] = the smallest index of the largest logits[b][V] (bf16); NaN
  * never wins; a row with nothing above -inf gives 0. */
 int viper_hip_sampling_greedy(const void* logits_bf16, int32_t* out_token, int B, int V, void* stream);
-
-/* viper_hip_qlinear with two caller-created hipEvent_t attached to the GEMV
- * dispatch (measurement use: they bracket the kernel's own execution, not
- * the host launch).  No counterpart in the reference. */
-int viper_hip_qlinear_timed(int qtype, const void* w_packed, const void* w_scales, int scale_enc,
-                            int group, int N, int K, const void* x_bf16, int M, void* y_bf16,
-                            const void* residual_bf16, void* workspace, size_t workspace_bytes,
-                            void* start_event, void* stop_event, void* stream);
 
 /* viper_hip_qlinear, also writing D[M][N][K/group] int32 (test use). */
 int viper_hip_qlinear_partials(int qtype, const void* w_packed, const void* w_scales,

@@ -84,8 +84,18 @@ int main() {
     EXPECT(ops::linear_workspace_bytes(w, 4) == 16 * 128 + 2 * 16 * 4);  // xq, xs for 16 rows
     Tensor misaligned(reinterpret_cast<void*>(0x10008), DType::BF16, {128});
     EXPECT(code(w, misaligned, y) == StatusCode::INVALID_ARGUMENT);
-    Tensor wt(fake, DType::Q4_G64, {64, 128});
-    EXPECT(ops::linear_forward(wt, Tensor(), x, y).code() == StatusCode::INVALID_ARGUMENT);
+    // lossy dtypes through the Tensor overload: UNIMPLEMENTED, as the
+    // reference's switch returns (src/viper/linear.cpp:26-32)
+    for (DType dt : {DType::Q4_G64, DType::Q5_G64, DType::Q6_G64, DType::W8_G32}) {
+        Tensor wt(fake, dt, {64, 128});
+        EXPECT(ops::linear_forward(wt, Tensor(), x, y).code() == StatusCode::UNIMPLEMENTED);
+    }
+    // the six fields of the reference's QuantizedWeight leave the encoding at
+    // bf16, what its converter writes
+    {
+        quant::QuantizedWeight r;
+        EXPECT(r.scale_enc == quant::ScaleEnc::BF16);
+    }
     Tensor wbf(fake, DType::BF16, {64, 128});
     EXPECT(ops::linear_forward(wbf, Tensor(), x, y).code() == StatusCode::UNIMPLEMENTED);
     Tensor wi(fake, DType::INT32, {64, 128});
@@ -133,6 +143,19 @@ int main() {
         };
         g = write_artifact(d, short_fill);
         EXPECT(A::parse(g.data(), g.size(), &idx).code() == StatusCode::INVALID_ARGUMENT);
+        // header products past INT32_MAX (n_heads * head_dim here): a wrapped
+        // section size would let a few-KB file parse into views ~137 GB past
+        // its end; the parser rejects the header instead
+        {
+            std::vector<uint8_t> bad(A::kHeaderBytes + 8192, 0);
+            std::memcpy(bad.data(), "VIPER", 5);
+            const uint32_t hdr[10] = {1, 1, 1, 192, 64, 1596634768u, 1596634768u, 3851171736u, 64, 16};
+            std::memcpy(bad.data() + 16, hdr, sizeof hdr);
+            EXPECT(A::parse(bad.data(), bad.size(), &idx).code() == StatusCode::INVALID_ARGUMENT);
+            const uint32_t big[10] = {1, 1, 1, 0x80000000u, 64, 1, 1, 64, 64, 16};  // hidden > INT32_MAX
+            std::memcpy(bad.data() + 16, big, sizeof big);
+            EXPECT(A::parse(bad.data(), bad.size(), &idx).code() == StatusCode::INVALID_ARGUMENT);
+        }
         ArtifactDims odd = d;
         odd.hidden = 96;  // not a multiple of the 64-group
         g = write_artifact(odd, hash_fill);

@@ -241,8 +241,58 @@ static int artifact_case() {
     return fails;
 }
 
+// A weight described by the reference's six fields only (quant.h:34-41:
+// qtype, data, scales, rows, cols, group_size) over bf16 scales, the
+// converter's encoding (convert.cpp:109-113): the default encoding must
+// decode them, for every format and both the fused M = 1 and multi-row paths.
+int reference_fields_case(int qt, int M) {
+    const int N = 257, K = 2560, G = vo_group_size(qt);
+    std::vector<uint8_t> packed(vo_packed_bytes(qt, N, K));
+    std::vector<uint16_t> scales((size_t)N * (K / G));
+    vo_gen_weights(qt, N, K, 0xB16u + qt, VO_SCALE_BF16, packed.data(), scales.data());
+    std::vector<uint16_t> x((size_t)M * K), yref((size_t)M * N);
+    vo_gen_act(M, K, 0xB17u + qt, 0.0, 1.0f, x.data());
+    std::vector<float> yf((size_t)M * N);
+    std::vector<double> ya((size_t)M * N);
+    vo_qlinear(qt, packed.data(), scales.data(), VO_SCALE_BF16, N, K, x.data(), M, nullptr, yref.data(), yf.data(),
+               ya.data());
+    uint8_t* dw = upload(packed);
+    uint16_t* ds = upload(scales);
+    uint16_t* dx = upload(x);
+    uint16_t* dy = nullptr;
+    CHECK_HIP(hipMalloc(&dy, (size_t)M * N * 2));
+    quant::QuantizedWeight w;
+    w.qtype = static_cast<quant::QType>(qt);
+    w.data = dw;
+    w.scales = ds;
+    w.rows = N;
+    w.cols = K;
+    w.group_size = G;
+    Tensor tx(dx, DType::BF16, {M, K}), ty(dy, DType::BF16, {M, N});
+    ops::LinearOptions opt;
+    opt.workspace_bytes = ops::linear_workspace_bytes(w, M);
+    if (opt.workspace_bytes) CHECK_HIP(hipMalloc(&opt.workspace, opt.workspace_bytes));
+    char what[96];
+    std::snprintf(what, sizeof what, "reference fields q%d M%d (bf16 scales)", qt, M);
+    std::printf("case %s\n", what);
+    std::fflush(stdout);
+    if (!ops::linear(w, tx, ty, opt).ok()) return 1;
+    CHECK_HIP(hipDeviceSynchronize());
+    std::vector<uint16_t> yg((size_t)M * N);
+    CHECK_HIP(hipMemcpy(yg.data(), dy, yg.size() * 2, hipMemcpyDeviceToHost));
+    const int fails = close_bf16(yg, yref, ya, what) ? 0 : 1;
+    (void)hipFree(dw);
+    (void)hipFree(ds);
+    (void)hipFree(dx);
+    (void)hipFree(dy);
+    if (opt.workspace) (void)hipFree(opt.workspace);
+    return fails;
+}
+
 int main() {
     failures += artifact_case();
+    for (int qt : {VO_Q4_G64, VO_Q5_G64, VO_Q6_G64, VO_W8_G32})
+        for (int M : {1, 8}) failures += reference_fields_case(qt, M);
     const int qts[] = {VO_Q4_G64, VO_Q5_G64, VO_Q6_G64, VO_W8_G32};
     for (int qt : qts)
         for (int senc : {0, 1})

@@ -28,7 +28,7 @@ def test_header_symbols_exported():
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(ql._SYMBOLS)
-    assert L.viper_hip_abi_version() == 2
+    assert L.viper_hip_abi_version() == 3
 
 
 def test_group_sizes_and_workspace():
@@ -39,10 +39,11 @@ def test_group_sizes_and_workspace():
     assert va.workspace_bytes(4, 10240, 2560, 4) == 16 * 2560 + 40 * 16 * 4
     assert va.workspace_bytes(8, 10, 2560, 3) == 16 * 2560 + 80 * 16 * 4
     assert va.workspace_bytes(6, 10, 2496, 3) == 16 * 2496 + 39 * 16 * 4
-    # long K (the K split in 4 parts): then fp32 part sums [4][M][N] and one
-    # counter per 8 rows
-    assert va.workspace_bytes(4, 2560, 10240, 16) == 16 * 10240 + 160 * 16 * 4 + 4 * 16 * 2560 * 4 + 320 * 4
-    assert va.workspace_bytes(8, 2560, 10240, 3) == 16 * 10240 + 320 * 16 * 4 + 4 * 3 * 2560 * 4 + 320 * 4
+    # long K (the K split in 4 parts): then the part sums [4][M][N] as 64-bit
+    # {generation, fp32} slots, one counter per 8 rows and the generation word
+    # (16-byte aligned)
+    assert va.workspace_bytes(4, 2560, 10240, 16) == 16 * 10240 + 160 * 16 * 4 + 4 * 16 * 2560 * 8 + 1296
+    assert va.workspace_bytes(8, 2560, 10240, 3) == 16 * 10240 + 320 * 16 * 4 + 4 * 3 * 2560 * 8 + 1296
     assert va.workspace_bytes(4, 2560, 5120, 16) == 16 * 5120 + 80 * 16 * 4   # one segment: no split
 
 

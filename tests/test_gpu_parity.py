@@ -207,8 +207,102 @@ def _k_split_shapes(n=12, seed=0x5EED5):
 
 @pytest.mark.parametrize("qtype,N,K,M,senc", _k_split_shapes())
 def test_k_split_random_shapes(torch_dev, qtype, N, K, M, senc):
-    run_case(torch_dev, qtype, N, K, M, seed=5500 + N, scale_enc=senc, residual=(M % 2 == 1),
-             check_partials=False)
+    # every part writes the int32 dots of its own groups: D bit-exact
+    run_case(torch_dev, qtype, N, K, M, seed=5500 + N, scale_enc=senc, residual=(M % 2 == 1))
+
+
+# Two different activations at the same row count alternating on one
+# workspace: each result must be the oracle's for its own x (a part that
+# consumed the previous call's sums would give the other x's output).
+def test_k_split_alternating_inputs(torch_dev):
+    torch = torch_dev
+    qtype, N, K, M = O.Q4_G64, 2560, 10240, 8
+    packed, scales = O.gen_weights(qtype, N, K, 5600, O.SCALE_FP16)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, 64,
+                           va.ScaleEnc(O.SCALE_FP16))
+    xs = [O.gen_act(M, K, 5601), O.gen_act(M, K, 5602)]
+    refs = [O.qlinear(qtype, packed, scales, O.SCALE_FP16, N, K, x) for x in xs]
+    ws = torch.full((va.workspace_bytes(qtype, N, K, M),), 255, dtype=torch.uint8, device="cuda")
+    xds = [dev(torch, x) for x in xs]
+    for i in range(6):
+        note(f"alternating call {i}")
+        yd = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+        assert va.linear(w, xds[i % 2], yd, workspace=ws).ok()
+        torch.cuda.synchronize()
+        y_ref, _, absterm = refs[i % 2]
+        O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
+
+
+# BASELINE config 2 as stated: M in {2, 4, 8, 16} at both shapes, full size,
+# int32 group dots bit-exact and bf16 within the bar.
+@pytest.mark.parametrize("M", [2, 4, 8, 16])
+@pytest.mark.parametrize("N,K", [(10240, 2560), (2560, 10240)])
+def test_config2_grid_full_size(torch_dev, N, K, M):
+    run_case(torch_dev, O.Q4_G64, N, K, M, seed=0x5EED0002 + M, residual=(K == 10240))
+
+
+# Output rounding (A8) pinned exactly: one non-zero group whose weight scale
+# (2^-4) and activation scale (amax 15.875 -> 2^-3) are powers of two, so the
+# fp32 sum ws*xs*D is exact and the bf16 output must equal RNE(D * 2^-7) bit
+# for bit: ties to even both ways (257 -> 256, 259 -> 260, 383 -> 384), a
+# round up past a truncation (515 -> 516) and exact values.  Every other
+# group holds zeros (its term is exactly 0).  Runs the M = 1 kernel, the
+# multi-row and matrix-core paths and the K split.
+A8_CODES = [(2, 0, 1), (2, 2, 1), (4, 7, 0), (3, 0, 0), (-2, -2, -1), (1, 1, 0), (7, 7, 7), (-8, -8, -8),
+            (5, 3, 2), (0, 1, 0), (0, 0, 0), (6, -3, 7), (3, 5, -1), (-3, -5, 1), (-4, -7, 0), (7, -8, 5)]
+
+
+def _rne_bf16_exact(D):
+    # D * 2^-7 rounded to 8 significant bits, ties to even, from the integer
+    from fractions import Fraction
+    out = []
+    for d in D:
+        v = Fraction(int(d), 128)
+        if v == 0:
+            out.append(0)
+            continue
+        sign = 0x8000 if v < 0 else 0
+        a = abs(v)
+        e = a.numerator.bit_length() - a.denominator.bit_length()
+        if Fraction(2) ** e > a:
+            e -= 1
+        q = a / Fraction(2) ** (e - 7)          # in [128, 256)
+        fl = q.numerator // q.denominator
+        rem = q - fl
+        if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+            fl += 1
+        if fl == 256:
+            fl, e = 128, e + 1
+        out.append(sign | ((e + 127) << 7) | (fl - 128))
+    return np.array(out, dtype=np.uint16)
+
+
+@pytest.mark.parametrize("senc", [O.SCALE_FP16, O.SCALE_BF16])
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("M,K", [(1, 256), (2, 256), (4, 256), (16, 256), (1, 10240), (16, 10240)])
+def test_bf16_rounding_exact(torch_dev, qtype, M, K, senc):
+    torch = torch_dev
+    G = O.group_size(qtype)
+    N = len(A8_CODES)
+    w = np.zeros((N, K), dtype=np.int8)
+    for n, (a, b, c) in enumerate(A8_CODES):
+        w[n, :3] = (a, b, c)
+    packed = O.pack(qtype, w)
+    scales = np.full(N * (K // G), 0x2C00 if senc == O.SCALE_FP16 else 0x3D80, dtype=np.uint16)
+    x = np.zeros((M, K), dtype=np.uint16)
+    x[:, 0], x[:, 1], x[:, 2] = 0x417E, 0x3E00, 0x3EC0   # 15.875 (q = 127), 0.125 (1), 0.375 (3)
+    D = w[:, 0].astype(np.int64) * 127 + w[:, 1] + 3 * w[:, 2]
+    expect = np.tile(_rne_bf16_exact(D), (M, 1))
+    y_ref, _, _ = O.qlinear(qtype, packed, scales, senc, N, K, x)
+    np.testing.assert_array_equal(y_ref, expect)         # the oracle's rounding
+    wq = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, va.ScaleEnc(senc))
+    nws = va.workspace_bytes(qtype, N, K, M)
+    ws = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda") if nws else None
+    note(f"case qtype={qtype} M={M} K={K} senc={senc}")
+    yd = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    assert va.linear(wq, dev(torch, x), yd, workspace=ws).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(yd, np.uint16), expect)
 
 
 # The K split captured in a HIP graph (its counters are cleared by the
@@ -303,7 +397,7 @@ def test_down_shape_full_size(torch_dev):
 @pytest.mark.parametrize("qtype", FORMATS)
 def test_format_sweep_full_size(torch_dev, qtype):
     # config 4: K=2560, N=10240 with 5% x20 outlier channels
-    run_case(torch_dev, qtype, 10240, 2560, 1, seed=0x5EED0004, outlier=0.05, check_partials=False)
+    run_case(torch_dev, qtype, 10240, 2560, 1, seed=0x5EED0004, outlier=0.05)
 
 
 @pytest.mark.parametrize("qtype", FORMATS)
@@ -319,7 +413,7 @@ def test_row_matches_single_row_call(torch_dev):
     N, K, M = 300, 2560, 4
     packed, scales = O.gen_weights(O.Q4_G64, N, K, 5, O.SCALE_FP16)
     x = O.gen_act(M, K, 6)
-    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K)
+    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K, scale_enc=va.ScaleEnc.FP16)
     ws = torch.zeros(va.workspace_bytes(4, N, K, M), dtype=torch.uint8, device="cuda")
     pm = torch.zeros((M, N, K // 64), dtype=torch.int32, device="cuda")
     ym = torch.zeros((M, N), dtype=torch.int16, device="cuda")
@@ -386,7 +480,7 @@ def test_prequantized_m1(torch_dev, qtype, N, K):
     xq, xs = O.quantize_act(O.gen_act(1, K, 51, outlier_frac=0.05, outlier_mul=20.0), G)
     res = O.gen_act(1, N, 52)
     y_ref, _, absterm = O.qlinear_prequant(qtype, packed, scales, O.SCALE_FP16, N, K, xq, xs, residual=res)
-    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, scale_enc=va.ScaleEnc.FP16)
     yd = torch.zeros((1, N), dtype=torch.int16, device="cuda")
     assert va.linear_prequantized(w, dev(torch, xq), dev(torch, xs), yd, residual=dev(torch, res)).ok()
     torch.cuda.synchronize()
@@ -429,7 +523,7 @@ def test_fused2_matches_two_calls(torch_dev):
     torch = torch_dev
     N, K, M = 512, 2560, 1
     mats = [O.gen_weights(O.Q4_G64, N, K, s, O.SCALE_FP16) for s in (81, 82)]
-    ws = [va.QuantizedWeight(va.QType.Q4_G64, dev(torch, p), dev(torch, sc), N, K) for p, sc in mats]
+    ws = [va.QuantizedWeight(va.QType.Q4_G64, dev(torch, p), dev(torch, sc), N, K, scale_enc=va.ScaleEnc.FP16) for p, sc in mats]
     x = dev(torch, O.gen_act(M, K, 83))
     ya = [torch.zeros((M, N), dtype=torch.int16, device="cuda") for _ in range(2)]
     yb = [torch.zeros((M, N), dtype=torch.int16, device="cuda") for _ in range(2)]
@@ -451,7 +545,7 @@ def test_residual_in_place(torch_dev, M):
     x = O.gen_act(M, K, 72)
     res = O.gen_act(M, N, 73)
     y_ref, _, absterm = O.qlinear(O.Q4_G64, packed, scales, O.SCALE_FP16, N, K, x, residual=res)
-    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K)
+    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K, scale_enc=va.ScaleEnc.FP16)
     yd = dev(torch, res)
     ws = torch.zeros(max(16, va.workspace_bytes(4, N, K, M)), dtype=torch.uint8, device="cuda") if M > 1 else None
     assert va.linear(w, dev(torch, x), yd, residual=yd, workspace=ws).ok()
@@ -467,7 +561,7 @@ def test_zero_weight_kat(torch_dev):
     scales = np.full(N * K // 64, 0x3C00, np.uint16)
     x = O.gen_act(1, K, 3)
     res = O.gen_act(1, N, 4)
-    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K)
+    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K, scale_enc=va.ScaleEnc.FP16)
     yd = torch.zeros((1, N), dtype=torch.int16, device="cuda")
     assert va.linear(w, dev(torch, x), yd, residual=dev(torch, res)).ok()
     torch.cuda.synchronize()
@@ -487,11 +581,11 @@ def test_device_errors_are_codes(torch_dev):
     wd, sd = dev(torch, packed), dev(torch, scales)
     x = dev(torch, O.gen_act(2, K, 1))
     y = torch.zeros((2, N), dtype=torch.int16, device="cuda")
-    w = va.QuantizedWeight(va.QType.Q4_G64, wd, sd, N, K)
+    w = va.QuantizedWeight(va.QType.Q4_G64, wd, sd, N, K, scale_enc=va.ScaleEnc.FP16)
     assert va.linear(w, x, y).code == va.StatusCode.INVALID_ARGUMENT        # M=2 without workspace
     small = torch.zeros(16, dtype=torch.uint8, device="cuda")
     assert va.linear(w, x, y, workspace=small).code == va.StatusCode.INVALID_ARGUMENT
-    wbad = va.QuantizedWeight(va.QType.BF16, wd, sd, N, K)
+    wbad = va.QuantizedWeight(va.QType.BF16, wd, sd, N, K, scale_enc=va.ScaleEnc.FP16)
     assert va.linear(wbad, x, y).code == va.StatusCode.UNIMPLEMENTED
     assert va.linear(w, x[:1], y[:1, :N - 1]).code == va.StatusCode.SHAPE_MISMATCH
 
@@ -531,7 +625,7 @@ def test_quantizer_edge_cases_every_path(torch_dev, qtype, M):
     assert list(xq[0, G:G + 8]) == [127, 2, 4, -2, 0, -2, 0, 2]   # the ties group of row 0
     D_ref = O.group_dots(qtype, packed, N, K, xq)
     y_ref, _, absterm = O.qlinear(qtype, packed, scales, O.SCALE_FP16, N, K, x)
-    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, scale_enc=va.ScaleEnc.FP16)
     yd = torch.zeros((M, N), dtype=torch.int16, device="cuda")
     pd = torch.full((M, N, K // G), -7, dtype=torch.int32, device="cuda")
     nws = va.workspace_bytes(qtype, N, K, M)

@@ -112,9 +112,9 @@ def test_mlp_pipeline(torch_dev):
     pd, sd = O.gen_weights(O.Q4_G64, H, I, 0x5EED0021, O.SCALE_FP16)
     x = O.gen_act(1, H, 0x5EED0031)
     res = O.gen_act(1, H, 0x5EED0041)
-    wg = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, pg), dev(torch, sg), I, H)
-    wu = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, pu), dev(torch, su), I, H)
-    wd = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, pd), dev(torch, sd), H, I)
+    wg = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, pg), dev(torch, sg), I, H, scale_enc=va.ScaleEnc.FP16)
+    wu = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, pu), dev(torch, su), I, H, scale_enc=va.ScaleEnc.FP16)
+    wd = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, pd), dev(torch, sd), H, I, scale_enc=va.ScaleEnc.FP16)
     g = torch.zeros((1, I), dtype=torch.int16, device="cuda")
     u = torch.zeros((1, I), dtype=torch.int16, device="cuda")
     xq = torch.zeros((1, I), dtype=torch.int8, device="cuda")

@@ -106,6 +106,45 @@ def test_q4_weight_quantizer_matches_reference_convert(shape, seed):
     np.testing.assert_array_equal(s, s_ref)
 
 
+@pytest.mark.parametrize("scale_enc", [O.SCALE_BF16, O.SCALE_FP16])
+@pytest.mark.parametrize("qtype", O.QTYPES)
+def test_weight_quantizer_roundtrip_every_format(qtype, scale_enc):
+    """vo_quantize_weights on representable weights w = c * 2^e: each group's
+    largest |c| is the format's top code wmax, so scale = wmax*2^e / wmax =
+    2^e exactly (both 16-bit encodings hold it) and every code comes back.
+    Half-way values (c + 1/2) * 2^e round half away from zero, as
+    convert.cpp:115-117's std::round; the low end -wmax-1 (Q5/Q6: -16/-32)
+    is reached by a tie only.  No reference pins the Q5/Q6/W8 branches, so
+    the closed form does."""
+    rng = np.random.default_rng(100 + qtype)
+    G = O.group_size(qtype)
+    wmin, wmax = O.wrange(qtype)
+    N, K = 6, 4 * G
+    codes = rng.integers(-wmax, wmax + 1, size=(N, K))
+    e = rng.integers(-12, 3, size=(N, K // G))
+    for n in range(N):
+        for g in range(K // G):
+            codes[n, g * G + int(rng.integers(0, G))] = wmax if rng.random() < 0.5 else -wmax
+    expo = np.repeat(e, G, axis=1).astype(np.float64)
+    w = codes * 2.0 ** expo
+    p, s = O.quantize_weights(qtype, _bf16(w), scale_enc)
+    np.testing.assert_array_equal(O.unpack(qtype, p, N, K), codes)
+    if scale_enc == O.SCALE_BF16:
+        got = O.bf16_to_f32(s).reshape(N, K // G)
+    else:
+        got = s.view(np.float16).astype(np.float32).reshape(N, K // G)
+    np.testing.assert_array_equal(got, (2.0 ** e).astype(np.float32))
+    # ties: (c + 1/2) * 2^e -> c + 1 for c >= 0, c - 1 ... away from zero, in range
+    wt = np.zeros((1, G))
+    wt[0, 0] = wmax                                   # scale 1
+    half = np.arange(-(wmax - 1), wmax - 1) + 0.5     # every tie whose result is a valid code
+    wt[0, 1:1 + min(len(half), G - 1)] = half[:G - 1]
+    p, s = O.quantize_weights(qtype, _bf16(wt), scale_enc)
+    got = O.unpack(qtype, p, 1, G)[0, 1:1 + min(len(half), G - 1)]
+    h = half[:G - 1]
+    np.testing.assert_array_equal(got, np.where(h > 0, np.floor(h) + 1, np.ceil(h) - 1))
+
+
 def test_reference_ties_round_half_away():
     _ref_or_skip()
     # max 1.75 -> scale 0.25 exactly; 0.625/0.25 = 2.5 -> 3 (away from zero)

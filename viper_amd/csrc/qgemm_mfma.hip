@@ -402,12 +402,10 @@ bool mfma_staged(int qtype, int N, int K) {
 
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
-                const void* w1, const void* s1, void* y1, hipStream_t st, hipEvent_t ev0,
-                hipEvent_t ev1, float* sp, unsigned* sc) {
+                const void* w1, const void* s1, void* y1, hipStream_t st, uint64_t* sp, unsigned* sc) {
     if (!mfma_ok(qtype, K, M, s)) return VIPER_INTERNAL;
     if (rc_ok(qtype, K))
-        return launch_rc(qtype, w, s, senc, N, K, xq, xs, xnat ? RC_NAT : RC_FRAG, M, y, res, part, w1, s1, y1, st,
-                         ev0, ev1, sp, sc);
+        return launch_rc(qtype, w, s, senc, N, K, xq, xs, xnat ? RC_NAT : RC_FRAG, M, y, res, part, w1, s1, y1, st, sp, sc);
     if (sp != nullptr) return VIPER_INTERNAL;
     const int NG = K / group_of(qtype);
     const int NP = NG / 2;
@@ -437,7 +435,7 @@ int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K,
     if (N >= (1 << 27)) return VIPER_INVALID_ARGUMENT;  // N shares a word with M and the encoding
     unsigned nm = (unsigned)N | ((unsigned)(M - 1) << 27) | (senc ? 1u << 31 : 0u);
     void* args[] = {&a3, &a4, &a0, &a1, &a5, &K, &nm, &a6, &part, &b0, &b1, &b2};
-    launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args, ev0, ev1);
+    launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args);
     return status_of(hipGetLastError());
 }
 

@@ -167,7 +167,7 @@ static pre_fn pick_pre(int mt, int ts) {
 
 int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K,
                       const void* xq, const void* xs, int M, void* y, const void* res,
-                      int32_t* part, hipStream_t st, hipEvent_t ev0, hipEvent_t ev1) {
+                      int32_t* part, hipStream_t st) {
     const size_t lds = lds_pre(qtype, M, K);
     if (lds > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
     const int cpr = K / (qtype == VIPER_QTYPE_W8_G32 ? 16 : 32);
@@ -189,7 +189,7 @@ int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K,
     uint16_t* a5 = (uint16_t*)y;
     const uint16_t* a6 = (const uint16_t*)res;
     void* args[] = {&a0, &a1, &senc, &a3, &a4, &a5, &a6, &part, &N, &K, &M};
-    launch((const void*)fn, grid, NT, lds, st, args, ev0, ev1);
+    launch((const void*)fn, grid, NT, lds, st, args);
     return status_of(hipGetLastError());
 }
 

@@ -74,6 +74,7 @@ template <> struct RcFmt<6> { static constexpr int QB = 16, HQ = 64, HSTR = 72, 
 template <> struct RcFmt<8> { static constexpr int QB = 8, HQ = 0, HSTR = 0, OFF = 0; };
 
 constexpr int RC_LSTR = 136;  // main-plane transpose row stride (bytes): 128 + 8 spreads banks
+constexpr int RC_SPIN = 4096; // K split: re-reads of a slot that still holds an earlier call's sum
 constexpr int RC_XR = 8;      // RC_BF16: octets per thread held in registers (all rows in one pass)
 
 __host__ __device__ constexpr size_t rc_wave_lds(int hstr) { return (size_t)16 * (RC_LSTR + hstr); }
@@ -101,19 +102,34 @@ struct RcSeg {
 // blockIdx = SK * block + part; each part stores its fp32 sums to sp
 // [SK][M][N], and the last part of a block to arrive (counter sc[block],
 // zeroed by the fragment quantize launch) adds the SK sums in part order, so
-// the result does not depend on which part finishes last.  PR: the launch
-// may carry a fused pair (without it the matrix select is not compiled).
+// the result does not depend on which part finishes last.  Partials (PART)
+// are written by each part for its own groups.  PR: the launch may carry a
+// fused pair (without it the matrix select is not compiled).
+//
+// The exchange between the parts of a block.  Each sum travels in a 64-bit
+// slot {generation, fp32 bits}, written and read as agent-scope relaxed
+// atomics; the generation is the word after the counters, which the fragment
+// quantize launch increments once per call.  The last part accepts a slot
+// only when it carries the current generation and re-reads it otherwise
+// (bounded by RC_SPIN, then NaN).  So a sum from an earlier call on the same
+// workspace can never be consumed: the result depends only on the coherence
+// of the atomic accesses to each slot, not on any ordering between the
+// slots and the counter.  (An agent-scope release/acquire pair would order
+// them but costs a write-back and an invalidate of the XCD's L2 per
+// workgroup: 70 us on the down shape.)  Each part also waits for its own
+// slot stores to complete before it counts (vmcnt 0), so in practice the
+// first read already holds the current generation.
 template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, int SK = 1, bool PR = true>
 __global__ void __launch_bounds__(64 * W)
 qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
                 unsigned nm, const uint16_t* res, int32_t* __restrict__ part,
-                const uint8_t* w1, const uint16_t* ws1, uint16_t* y1, float* __restrict__ sp,
+                const uint8_t* w1, const uint16_t* ws1, uint16_t* y1, uint64_t* __restrict__ sp,
                 unsigned* __restrict__ sc) {
     using FM = RcFmt<F>;
     using Seg = RcSeg<F, RB, QW>;
     constexpr int T = Seg::T;
     constexpr bool XNAT = AM == RC_NAT, XBF = AM == RC_BF16;
-    static_assert(SK == 1 || (AM == RC_FRAG && !PART), "the K split reads fragments and writes no partials");
+    static_assert(SK == 1 || AM == RC_FRAG, "the K split reads fragments");
     constexpr int G = F == 8 ? 32 : 64;
     extern __shared__ __align__(16) uint8_t smem[];
     const int tid = (int)threadIdx.x, L = tid & 63, wave = tid >> 6;
@@ -340,7 +356,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                             if (16 * t + n16 < nrows) {
 #pragma unroll
                                 for (int r = 0; r < 4; ++r)
-                                    if (4 * kb + r < M) part[((size_t)(4 * kb + r) * N + n) * NG + 4 * Q + h] = C[r];
+                                    if (4 * kb + r < M) part[((size_t)(4 * kb + r) * N + n) * NG + 4 * (q0 + Q) + h] = C[r];
                             }
                         }
                     }
@@ -395,24 +411,34 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         }
     }
 
-    // cross-wave sum in wave order, residual, bf16 store
+    // cross-wave sum in wave order, residual, bf16 store (K split: the part's
+    // sums to its slots, kept in registers too: at most MINE per thread)
     float* red = (float*)(smem + (size_t)W * rc_wave_lds(FM::HSTR));
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
         for (int r = 0; r < 4; ++r) red[((wave * T + t) * 4 + r) * 64 + L] = acc[t][r];
     __syncthreads();
-    for (int sl = wave; sl < 4 * T; sl += W) {
+    constexpr int MINE = (4 * T + W - 1) / W;
+    float mine[MINE];
+    const int kpart = SK > 1 ? (int)(blockIdx.x % SK) : 0;
+    unsigned gen = 0;
+    if constexpr (SK > 1) gen = sc[(N + 7) / 8];  // written by the previous launch
+#pragma unroll
+    for (int i = 0; i < MINE; ++i) {
+        const int sl = wave + i * W;
+        if (sl >= 4 * T) break;
         const int t = sl >> 2, r = sl & 3;
         float v = 0.0f;
 #pragma unroll
         for (int u = 0; u < W; ++u) v += red[((u * T + t) * 4 + r) * 64 + L];
+        mine[i] = v;
         const int m = 4 * kb + r, nl = 16 * t + n16;
         if (m < M && nl < nrows) {
             const size_t o = (size_t)m * N + row0 + nl;
             if constexpr (SK > 1) {
-                __hip_atomic_store(sp + (size_t)(blockIdx.x % SK) * M * N + o, v, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(sp + (size_t)kpart * M * N + o, ((uint64_t)gen << 32) | __float_as_uint(v),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
                 y[o] = f2bf(v);
@@ -420,27 +446,33 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         }
     }
     if constexpr (SK > 1) {
-        // The parts' sums are device-coherent stores (sc1, through the
-        // XCD's L2); once every thread's stores have completed (vmcnt 0) the
-        // block's counter is incremented, and the last part reads the sums
-        // with device-coherent loads.  No device-scope fence: its L2
-        // write-back and invalidate per workgroup cost 70 us of the
-        // down-shape verify.
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         int* last = (int*)red;
         if (tid == 0) last[0] = atomicAdd(sc + bid, 1u) == (unsigned)(SK - 1);
         __syncthreads();
         if (!last[0]) return;
-        for (int sl = wave; sl < 4 * T; sl += W) {
+#pragma unroll
+        for (int i = 0; i < MINE; ++i) {
+            const int sl = wave + i * W;
+            if (sl >= 4 * T) break;
             const int t = sl >> 2, r = sl & 3;
             const int m = 4 * kb + r, nl = 16 * t + n16;
             if (m < M && nl < nrows) {
                 const size_t o = (size_t)m * N + row0 + nl;
                 float v = 0.0f;
 #pragma unroll
-                for (int p = 0; p < SK; ++p)
-                    v += __hip_atomic_load(sp + (size_t)p * M * N + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int p = 0; p < SK; ++p) {
+                    float vp = mine[i];
+                    if (p != kpart) {
+                        uint64_t* a = sp + (size_t)p * M * N + o;
+                        uint64_t u = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        for (int it = 0; (unsigned)(u >> 32) != gen && it < RC_SPIN; ++it)
+                            u = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        vp = (unsigned)(u >> 32) == gen ? __uint_as_float((unsigned)u) : __builtin_nanf("");
+                    }
+                    v += vp;
+                }
                 if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
                 y[o] = f2bf(v);
             }
@@ -451,7 +483,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
 // ------------------------------------------------------------------ host side
 
 typedef void (*rc_fn)(const int8_t*, const float*, const uint8_t*, const uint16_t*, uint16_t*, int, unsigned,
-                      const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*, float*, unsigned*);
+                      const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*, uint64_t*, unsigned*);
 
 // Launch shape: rows per workgroup (8 * rb), waves, quads per wave per
 // segment, single segment or double-buffered loop.
@@ -472,8 +504,8 @@ rc_fn rc_pick5(bool pair) {
 }
 template <int F, int RB, int W, int QW, bool ONE>
 rc_fn rc_pick4(int am, bool part, int senc, bool pair) {
-    if (am == RC_NAT)
-        return part ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, true, 2> : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, false, 2>;
+    if (am == RC_NAT)  // the prequantized entry points, which write no partials
+        return part ? nullptr : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_NAT, false, 2>;
     if (part)
         return am == RC_BF16 ? qgemm_rc_kernel<F, RB, W, QW, ONE, RC_BF16, true, 2>
                              : qgemm_rc_kernel<F, RB, W, QW, ONE, RC_FRAG, true, 2>;
@@ -482,17 +514,18 @@ rc_fn rc_pick4(int am, bool part, int senc, bool pair) {
     return senc ? rc_pick5<F, RB, W, QW, ONE, RC_FRAG, 1>(pair) : rc_pick5<F, RB, W, QW, ONE, RC_FRAG, 0>(pair);
 }
 template <int F, int RB, int QW>
-rc_fn rc_pick_split(int senc) {
+rc_fn rc_pick_split(int senc, bool part) {
+    if (part) return qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, true, 2, RC_SK, false>;
     return senc ? qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 1, RC_SK, false>
                 : qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 0, RC_SK, false>;
 }
 template <int F, int RB>
 rc_fn rc_pick3(const RcShape& s, int am, bool part, int senc, bool pair) {
     if (s.sk != 1) {  // K split: fragment input, one segment of 10 waves
-        if (s.sk != RC_SK || am != RC_FRAG || part || !s.one || s.w != 10) return nullptr;
-        if (s.qw == 1) return rc_pick_split<F, RB, 1>(senc);
+        if (s.sk != RC_SK || am != RC_FRAG || !s.one || s.w != 10) return nullptr;
+        if (s.qw == 1) return rc_pick_split<F, RB, 1>(senc, part);
         if constexpr (RB <= rc_rb_qw2(F))
-            if (s.qw == 2) return rc_pick_split<F, RB, 2>(senc);
+            if (s.qw == 2) return rc_pick_split<F, RB, 2>(senc, part);
         return nullptr;
     }
     if (s.one && s.w == 4 && s.qw == 1) return rc_pick4<F, RB, 4, 1, true>(am, part, senc, pair);

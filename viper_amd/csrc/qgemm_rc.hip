@@ -58,7 +58,7 @@ bool rc_split_ok(int qtype, int K) {
 }
 
 size_t rc_split_bytes(int N, int M) {
-    return align16((size_t)RC_SK * M * N * 4) + align16((size_t)rc_split_counters(N) * 4);
+    return align16((size_t)RC_SK * M * N * 8) + align16((size_t)(rc_split_counters(N) + 1) * 4);
 }
 
 bool rc_ok(int qtype, int K) {
@@ -96,14 +96,14 @@ bool rc_bf16_ok(int qtype, int N, int K, int M, bool pair) {
 
 int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq, const void* xs,
               int am, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
-              hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, float* sp, unsigned* sc) {
+              hipStream_t st, uint64_t* sp, unsigned* sc) {
     if (!rc_ok(qtype, K) || M < 2 || M > 16) return VIPER_INTERNAL;
     if (N >= (1 << 27)) return VIPER_INVALID_ARGUMENT;  // N shares a word with M and the encoding
     if (am == RC_BF16 && !rc_bf16_ok(qtype, N, K, M, w1 != nullptr)) return VIPER_INTERNAL;
     RcShape sh = rc_launch_shape(qtype, w1 != nullptr ? 2 * N : N, K);
     if (sp != nullptr) {
         const int F = qtype == VIPER_QTYPE_W8_G32 ? 8 : qtype;
-        if (am != RC_FRAG || part != nullptr || w1 != nullptr || sc == nullptr ||
+        if (am != RC_FRAG || w1 != nullptr || sc == nullptr ||
             !rc_split_shape(F, N, K / group_of(qtype) / 4, device_cus(), sh))
             return VIPER_INTERNAL;
     }
@@ -130,7 +130,7 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     uint16_t* b2 = (uint16_t*)y1;
     unsigned nm = (unsigned)N | ((unsigned)(M - 1) << 27) | (senc ? 1u << 31 : 0u);  // see the kernel's arguments note
     void* args[] = {&a0, &a1, &a2, &a3, &a4, &K, &nm, &a5, &part, &b0, &b1, &b2, &sp, &sc};
-    launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args, ev0, ev1);
+    launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args);
     return status_of(hipGetLastError());
 }
 

@@ -38,7 +38,26 @@ namespace vq {
 
 constexpr int M1_XS = 4;    // activation octets per thread loaded before the weights
 constexpr int M1_XS_MR = 8; // the same for MR > 1 rows (all of them: no later rounds)
-constexpr int M1_DELAY = 8; // weight-issue delay, s_sleep units
+constexpr int M1_DELAY = 6; // weight-issue delay, s_sleep units
+
+// Row length of an exact tiling (TS lanes x CPL chunks of CK weights): an
+// exact launch's K is this constant, so its load rounds and offsets are
+// compile-time (the run-time round guards of the general path cost 0.1 us of
+// the north-star launch, placed before the weight loads).
+template <int F>
+__host__ __device__ constexpr int m1_exact_k(int ts, int cpl) { return Fmt<F>::CK * ts * cpl; }
+
+// Logical block of workgroup b in a grid of g: the dispatcher deals
+// workgroups to the 8 XCDs in turn (b -> XCD b % 8), so numbering the
+// blocks XCD by XCD gives each XCD one contiguous range of output rows.  Its
+// y stores then fill whole cache lines of one L2 instead of sharing lines
+// with the neighbouring XCDs (north star 4.07 -> 4.03 us).  Any g works: XCD
+// k holds g / 8 blocks, one more when k < g % 8.  The mapping only permutes
+// blocks, so results do not depend on how the hardware deals them.
+__device__ __forceinline__ int xcd_block(int b, int g) {
+    const int k = b & 7;
+    return k * (g >> 3) + min(k, g & 7) + (b >> 3);
+}
 
 // Kernel modes: plain, with the int32 group dots (test entry point), or the
 // gate/up pair with the swiglu epilogue (M1_SWIGLU): the first NTT/2 threads
@@ -159,8 +178,10 @@ __device__ __forceinline__ void m1_dots_rows(u32x4 (&wv)[CPL], uint32_t (&h0)[CP
 // chunks) and a row's scales fill whole 16-byte words (groups % 8 == 0), so no
 // chunk needs masking and the workgroup's scale block is loaded with one
 // 16-byte load per thread into LDS instead of one 2-byte load per chunk (those
-// small loads slow the weight issue several-fold).  CPL: chunk slots per lane
-// per row segment.
+// small loads slow the weight issue several-fold).  K is then the constant
+// m1_exact_k and its argument carries the number of workgroups of the launch
+// (the XCD-aware block order needs it, and every preloaded dword is taken).
+// CPL: chunk slots per lane per row segment.
 // DELAY: s_sleep units (64 clocks) between issuing the activation loads and
 // the weight loads.  The activation is a few KB read by every workgroup; a
 // short head start lets its requests through the memory pipeline before the
@@ -183,7 +204,13 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     constexpr bool SWI = MODE == M1_SWIGLU;
     constexpr bool PRE = PRO == PRO_INT8;
     constexpr bool TWO = PRO == PRO_RMSNORM || PRO == PRO_SWIGLU;  // two bf16 inputs
-    constexpr int XS = MR == 1 ? M1_XS : M1_XS_MR;
+    // exact tilings: K is the tiling's row length and the argument slot
+    // carries the grid size instead (for the XCD-aware block order); the
+    // load rounds of one row are then exact
+    constexpr int KX = EXACT ? m1_exact_k<F>(TS, CPL) : 0;
+    const int grid = K;
+    if constexpr (EXACT) K = KX;
+    constexpr int XS = MR > 1 ? M1_XS_MR : EXACT ? (KX / 8 + NTT - 1) / NTT : M1_XS;
     constexpr int ROWS = NTT / TS;
     const int M = MR == 1 ? 1 : e1;  // activation rows
     constexpr int HB = FT::HIW * 4;  // high-plane bytes per chunk: Q5 4, Q6 8
@@ -209,7 +236,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // 0.05 us off the north-star launch; MR > 1 launches are single-matrix and
     // stage their rows in XS rounds, so those paths are not compiled there
     // (0.5 us of an M = 2 launch).
-    int bid = (int)blockIdx.x;
+    int bid = EXACT ? xcd_block((int)blockIdx.x, grid) : (int)blockIdx.x;
     const uint8_t* w = w0;
     const uint16_t* ws = s0;
     uint16_t* y = y0;
@@ -539,24 +566,29 @@ m1_fn m1_pick_mode(int ts, int ntt, int cpl, int senc, bool exact) {
     return senc ? m1_kernel_v<F, 1, MODE, false, PRO, MR>(ts, ntt, cpl) : m1_kernel_v<F, 0, MODE, false, PRO, MR>(ts, ntt, cpl);
 }
 // The swiglu pair is built for the BF16 and RMSNORM prologues (the inputs of
-// the engine's gate/up projection); MR > 1 rows for BF16 and INT8, plain or
-// with partials.
+// the engine's gate/up projection); MR > 1 rows for BF16 and INT8; the
+// partials (test entry point viper_hip_qlinear_partials) for BF16 only, the
+// one prologue that entry point takes.
 template <int F, int PRO>
 m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, int mode, bool exact, int mr) {
+    constexpr bool PART_OK = PRO == PRO_BF16;
     if constexpr (PRO == PRO_BF16 || PRO == PRO_INT8) {
         if (mr == 2) {
-            if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 2>(ts, ntt, cpl, senc, exact);
+            if constexpr (PART_OK)
+                if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 2>(ts, ntt, cpl, senc, exact);
             if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 2>(ts, ntt, cpl, senc, exact);
             return nullptr;
         }
         if (mr == 4) {
-            if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 4>(ts, ntt, cpl, senc, exact);
+            if constexpr (PART_OK)
+                if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 4>(ts, ntt, cpl, senc, exact);
             if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 4>(ts, ntt, cpl, senc, exact);
             return nullptr;
         }
     }
     if (mr != 1) return nullptr;
-    if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 1>(ts, ntt, cpl, senc, exact);
+    if constexpr (PART_OK)
+        if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 1>(ts, ntt, cpl, senc, exact);
     if constexpr (PRO == PRO_BF16 || PRO == PRO_RMSNORM)
         if (mode == M1_SWIGLU) return m1_pick_mode<F, PRO, M1_SWIGLU, 1>(ts, ntt, cpl, senc, exact);
     if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 1>(ts, ntt, cpl, senc, exact);

@@ -133,8 +133,7 @@ bool m1_folded_ok(int qtype, int K, int N) {
 }
 
 int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
-              const M1Out* outs, int nouts, const void* res, int32_t* part, hipStream_t st,
-              hipEvent_t ev0, hipEvent_t ev1, int M) {
+              const M1Out* outs, int nouts, const void* res, int32_t* part, hipStream_t st, int M) {
     if (nouts < 1 || nouts > 3) return VIPER_INVALID_ARGUMENT;
     const int mr = m1_mr(M);
     if (mr > 1 && (nouts != 1 || (pro != PRO_BF16 && pro != PRO_INT8) || !m1_rows_ok(qtype, K, M)))
@@ -174,9 +173,11 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     if (mr > 1) e1 = M;  // one matrix: e1 carries the activation rows
     const unsigned grid = (unsigned)(nb[0] + nb[1] + nb[2]);
     const uint16_t* r = (const uint16_t*)res;
-    void* args[] = {&x, &w0, &s0, &y0, &K, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,
+    // an exact tiling's K is a kernel constant: the slot carries the grid size
+    int kg = exact ? (int)grid : K;
+    void* args[] = {&x, &w0, &s0, &y0, &kg, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,
                     &w1, &s1, &y1, &n1, &w2, &s2, &y2, &n2};
-    launch((const void*)fn, grid, (unsigned)sh.ntt, lds, st, args, ev0, ev1);
+    launch((const void*)fn, grid, (unsigned)sh.ntt, lds, st, args);
     return status_of(hipGetLastError());
 }
 
@@ -207,9 +208,10 @@ int launch_m1_swiglu(int qtype, int senc, int K, int pro, const void* x, const v
     uint16_t *y0 = (uint16_t*)g_out, *y1 = (uint16_t*)u_out, *y2 = (uint16_t*)h;
     const uint16_t* r = nullptr;
     int32_t* part = nullptr;
-    void* args[] = {&x, &w0, &s0, &y0, &K, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,
+    int kg = exact ? (int)grid : K;  // as in launch_m1
+    void* args[] = {&x, &w0, &s0, &y0, &kg, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,
                     &w1, &s1, &y1, &n1, &w2, &s2, &y2, &n2};
-    launch((const void*)fn, grid, (unsigned)sh.ntt, lds, st, args, nullptr, nullptr);
+    launch((const void*)fn, grid, (unsigned)sh.ntt, lds, st, args);
     return status_of(hipGetLastError());
 }
 

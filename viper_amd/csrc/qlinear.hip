@@ -32,6 +32,15 @@ namespace vq {
 
 // ------------------------------------------------ standalone activation quantize
 
+// The K split's generation word (after its counters): one increment per
+// call, by one thread of the quantize launch that precedes the split launch
+// on the stream (so the split launch sees it).  Written through like the
+// counters.
+__device__ __forceinline__ void bump_generation(unsigned* gen) {
+    const unsigned v = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(gen, v + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // MF: the fragment order the matrix-core kernels read (xs transposed to
 // [K/G][16]; 64-groups use quantize_frag64_kernel); else xq [M][K] in k order
 // and xs [M][K/G].
@@ -46,6 +55,7 @@ quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
         const int stride = (oct_total + NT - 1) / NT * NT;
         const auto cw = buf(cnt, (uint32_t)ncnt * 4u);
         for (int i = o; i < ncnt; i += stride) bstore4<AUX_SC1>(cw, i * 4, 0u);
+        if (ncnt > 0 && o == 0) bump_generation(cnt + ncnt);
     }
     const bool ok = o < oct_total;
     u32x4 v = {0u, 0u, 0u, 0u};
@@ -88,6 +98,7 @@ quantize_frag64_kernel(const uint16_t* x, int M, int K, int8_t* __restrict__ xq,
     {
         const auto cw = buf(cnt, (uint32_t)ncnt * 4u);
         for (int i = g * 64 + L; i < ncnt; i += K) bstore4<AUX_SC1>(cw, i * 4, 0u);  // K threads in the grid
+        if (ncnt > 0 && g == 0 && L == 0) bump_generation(cnt + ncnt);
     }
     const int m = L & 15, kb = L >> 4, qi = ((kb & 1) << 1) | (kb >> 1);
     const bool ok = m < M;
@@ -177,14 +188,14 @@ static int launch_quantize(int group, const void* x, int M, int K, void* xq, voi
     if (ncnt > 0 && !mf) return VIPER_INTERNAL;
     if (mf && group == 64) {
         void* fargs[] = {&a0, &M, &K, &a1, &a2, &cnt, &ncnt};
-        launch((const void*)quantize_frag64_kernel, (unsigned)(K / 64), 64, 0, st, fargs, nullptr, nullptr);
+        launch((const void*)quantize_frag64_kernel, (unsigned)(K / 64), 64, 0, st, fargs);
         return status_of(hipGetLastError());
     }
     void* args[] = {&a0, &a1, &a2, (void*)&oct_total, &K, &cnt, &ncnt};
     const void* fn;
     if (group == 64) fn = (const void*)quantize_act_kernel<64, false>;
     else fn = mf ? (const void*)quantize_act_kernel<32, true> : (const void*)quantize_act_kernel<32, false>;
-    launch(fn, grid, NT, 0, st, args, nullptr, nullptr);
+    launch(fn, grid, NT, 0, st, args);
     return status_of(hipGetLastError());
 }
 
@@ -227,8 +238,7 @@ static int validate_second(const Second& b, int qtype, int senc, int group, int 
 
 static int qlinear_common(int qtype, const void* w, const void* s, int senc, int group, int N,
                           int K, const void* x, int M, void* y, const void* res, void* wsp,
-                          size_t wsp_bytes, int32_t* part, void* stream,
-                          hipEvent_t ev0 = nullptr, hipEvent_t ev1 = nullptr, Second b = Second()) {
+                          size_t wsp_bytes, int32_t* part, void* stream, Second b = Second()) {
     int rc = validate_weights(qtype, w, s, senc, group, N, K, M);
     if (rc != VIPER_OK) return rc;
     if (x == nullptr || y == nullptr) return VIPER_INVALID_ARGUMENT;
@@ -239,8 +249,7 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     hipStream_t st = (hipStream_t)stream;
     if (fused_ok(qtype, M, K)) {
         const M1Out outs[2] = {{w, s, y, N}, {b.w, b.s, b.y, N}};
-        return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, b.w ? 2 : 1, res, part, st,
-                         ev0, ev1);
+        return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, b.w ? 2 : 1, res, part, st);
     }
     const size_t need = workspace_need(qtype, N, K, M);
     if (wsp == nullptr || wsp_bytes < need || misaligned(wsp, 16)) return VIPER_INVALID_ARGUMENT;
@@ -254,11 +263,11 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     const bool mf = mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s));
     if (b.w == nullptr && M == 2 && m1_rows_ok(qtype, K, M)) {
         const M1Out outs[1] = {{w, s, y, N}};
-        return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, ev0, ev1, M);
+        return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, M);
     }
     // (long K splits over workgroups in the two-launch path instead: down
     // shape K = 10240, 4 rows 9.5 us against 10.3 us)
-    const bool split_ok = mf && b.w == nullptr && part == nullptr && rc_split_ok(qtype, K);
+    const bool split_ok = mf && b.w == nullptr && rc_split_ok(qtype, K);
     // Q5/Q6/W8 (K = 2560, N = 10240, 5% outlier channels): 3 or 4 rows run
     // faster on the dot kernel below (Q5 4 rows 7.86 against 8.10 us) or in
     // two launches (W8 3 rows 8.37 against 9.23 us), and Q5/Q6 8 rows in two
@@ -267,14 +276,14 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     const bool hi = qtype == VIPER_QTYPE_Q5_G64 || qtype == VIPER_QTYPE_Q6_G64;
     const bool bf_ok = mf && M >= 3 && M <= (hi ? 7 : 8) && !split_ok && rc_bf16_ok(qtype, N, K, M, b.w != nullptr);
     if (bf_ok && (qtype == VIPER_QTYPE_Q4_G64 || M > 4))
-        return launch_rc(qtype, w, s, senc, N, K, x, nullptr, RC_BF16, M, y, res, part, b.w, b.s, b.y, st, ev0, ev1);
+        return launch_rc(qtype, w, s, senc, N, K, x, nullptr, RC_BF16, M, y, res, part, b.w, b.s, b.y, st);
     // (3 or 4 rows here where the LDS copy does not fit: while every
     // workgroup's share of the rows' quantize stays small; down shape
     // K = 10240: 3 rows 8.8 us against about 9.5 us for two launches with the K
     // split)
     if (b.w == nullptr && m1_rows_ok(qtype, K, M) && (long)M * K <= 32768) {
         const M1Out outs[1] = {{w, s, y, N}};
-        return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, ev0, ev1, M);
+        return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, M);
     }
     const bool staged = mf && mfma_staged(qtype, N, K);
     if (!mf && lds_pre(qtype, M, K) > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
@@ -282,16 +291,16 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     float* xs = (float*)(xq + workspace_xq(K));
     // long K on the matrix cores: the K split (parts' sums and counters after xs)
     const bool split = split_ok;
-    float* sp = split ? (float*)((uint8_t*)xs + workspace_xs(qtype, K)) : nullptr;
-    unsigned* sc = split ? (unsigned*)((uint8_t*)sp + align16((size_t)RC_SK * M * N * 4)) : nullptr;
+    uint64_t* sp = split ? (uint64_t*)((uint8_t*)xs + workspace_xs(qtype, K)) : nullptr;
+    unsigned* sc = split ? (unsigned*)((uint8_t*)sp + align16((size_t)RC_SK * M * N * 8)) : nullptr;
     rc = launch_quantize(group, x, M, K, xq, xs, staged, st, sc, split ? rc_split_counters(N) : 0);
     if (rc != VIPER_OK) return rc;
     if (mf)
         return launch_mfma(qtype, w, s, senc, N, K, xq, xs, !staged, M, y, res, part, b.w, b.s, b.y,
-                           st, ev0, ev1, sp, sc);
-    rc = launch_pre(qtype, w, s, senc, N, K, xq, xs, M, y, res, part, st, ev0, ev1);
+                           st, sp, sc);
+    rc = launch_pre(qtype, w, s, senc, N, K, xq, xs, M, y, res, part, st);
     if (rc == VIPER_OK && b.w != nullptr)
-        rc = launch_pre(qtype, b.w, b.s, senc, N, K, xq, xs, M, b.y, nullptr, nullptr, st, nullptr, nullptr);
+        rc = launch_pre(qtype, b.w, b.s, senc, N, K, xq, xs, M, b.y, nullptr, nullptr, st);
     return rc;
 }
 
@@ -308,20 +317,17 @@ static int prequant_common(int qtype, const void* w, const void* s, int senc, in
     hipStream_t st = (hipStream_t)stream;
     if (fused_ok(qtype, M, K)) {
         const M1Out outs[2] = {{w, s, y, N}, {b.w, b.s, b.y, N}};
-        return launch_m1(qtype, senc, K, PRO_INT8, xq, xs, 0.0f, nullptr, outs, b.w ? 2 : 1, res, nullptr, st,
-                         nullptr, nullptr);
+        return launch_m1(qtype, senc, K, PRO_INT8, xq, xs, 0.0f, nullptr, outs, b.w ? 2 : 1, res, nullptr, st);
     }
     if (b.w == nullptr && m1_rows_ok(qtype, K, M)) {
         const M1Out outs[1] = {{w, s, y, N}};
-        return launch_m1(qtype, senc, K, PRO_INT8, xq, xs, 0.0f, nullptr, outs, 1, res, nullptr, st, nullptr,
-                         nullptr, M);
+        return launch_m1(qtype, senc, K, PRO_INT8, xq, xs, 0.0f, nullptr, outs, 1, res, nullptr, st, M);
     }
     if (mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s)))
-        return launch_mfma(qtype, w, s, senc, N, K, xq, xs, true, M, y, res, nullptr, b.w, b.s, b.y, st,
-                           nullptr, nullptr);
-    rc = launch_pre(qtype, w, s, senc, N, K, xq, xs, M, y, res, nullptr, st, nullptr, nullptr);
+        return launch_mfma(qtype, w, s, senc, N, K, xq, xs, true, M, y, res, nullptr, b.w, b.s, b.y, st);
+    rc = launch_pre(qtype, w, s, senc, N, K, xq, xs, M, y, res, nullptr, st);
     if (rc == VIPER_OK && b.w != nullptr)
-        rc = launch_pre(qtype, b.w, b.s, senc, N, K, xq, xs, M, b.y, nullptr, nullptr, st, nullptr, nullptr);
+        rc = launch_pre(qtype, b.w, b.s, senc, N, K, xq, xs, M, b.y, nullptr, nullptr, st);
     return rc;
 }
 
@@ -344,16 +350,6 @@ extern "C" int viper_hip_qlinear(int qtype, const void* w_packed, const void* w_
                                  size_t workspace_bytes, void* stream) {
     return vq::qlinear_common(qtype, w_packed, w_scales, scale_enc, group, N, K, x_bf16, M, y_bf16,
                               residual_bf16, workspace, workspace_bytes, nullptr, stream);
-}
-
-extern "C" int viper_hip_qlinear_timed(int qtype, const void* w_packed, const void* w_scales,
-                                       int scale_enc, int group, int N, int K, const void* x_bf16,
-                                       int M, void* y_bf16, const void* residual_bf16,
-                                       void* workspace, size_t workspace_bytes, void* start_event,
-                                       void* stop_event, void* stream) {
-    return vq::qlinear_common(qtype, w_packed, w_scales, scale_enc, group, N, K, x_bf16, M, y_bf16,
-                              residual_bf16, workspace, workspace_bytes, nullptr, stream,
-                              (hipEvent_t)start_event, (hipEvent_t)stop_event);
 }
 
 extern "C" int viper_hip_qlinear_partials(int qtype, const void* w_packed, const void* w_scales,
@@ -394,7 +390,7 @@ extern "C" int viper_hip_qlinear_fused2(int qtype, const void* w0_packed, const 
                                         size_t workspace_bytes, void* stream) {
     if (w1_packed == nullptr || w1_scales == nullptr || y1_bf16 == nullptr) return VIPER_INVALID_ARGUMENT;
     return vq::qlinear_common(qtype, w0_packed, w0_scales, scale_enc, group, N, K, x_bf16, M, y0_bf16,
-                              nullptr, workspace, workspace_bytes, nullptr, stream, nullptr, nullptr,
+                              nullptr, workspace, workspace_bytes, nullptr, stream,
                               vq::Second{w1_packed, w1_scales, y1_bf16});
 }
 
@@ -434,7 +430,7 @@ extern "C" int viper_hip_qlinear_m1(int qtype, int scale_enc, int group, int K, 
     if ((prologue == VIPER_PROLOGUE_RMSNORM || prologue == VIPER_PROLOGUE_SWIGLU) && !vq::m1_folded_ok(qtype, K, N[0]))
         return VIPER_INVALID_ARGUMENT;
     return vq::launch_m1(qtype, scale_enc, K, prologue, a, b, eps, norm_out, outs, n_out, residual_bf16, nullptr,
-                         (hipStream_t)stream, nullptr, nullptr);
+                         (hipStream_t)stream);
 }
 
 extern "C" int viper_hip_qlinear_m1_swiglu(int qtype, int scale_enc, int group, int K, int prologue, const void* a,
@@ -466,8 +462,7 @@ extern "C" int viper_hip_stream_read(const void* buf, size_t bytes, uint32_t* si
     const uint8_t* a0 = (const uint8_t*)buf;
     uint32_t n = (uint32_t)bytes;
     void* args[] = {&a0, &n, &sink};
-    vq::launch((const void*)vq::stream_read_kernel, grid, vq::SR_NT, 0, (hipStream_t)stream, args, nullptr,
-               nullptr);
+    vq::launch((const void*)vq::stream_read_kernel, grid, vq::SR_NT, 0, (hipStream_t)stream, args);
     return vq::status_of(hipGetLastError());
 }
 
@@ -479,7 +474,6 @@ extern "C" int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts
     int32_t* c = counts;
     void* args[] = {&ab0, &c};
     const unsigned grid = (unsigned)((exp_hi - exp_lo + 1) << 7);
-    vq::launch((const void*)vq::check_quantizer_kernel, grid, vq::NT, 0, (hipStream_t)stream, args,
-               nullptr, nullptr);
+    vq::launch((const void*)vq::check_quantizer_kernel, grid, vq::NT, 0, (hipStream_t)stream, args);
     return vq::status_of(hipGetLastError());
 }

@@ -1,7 +1,7 @@
 // Host-side helpers and the launchers each kernel translation unit provides.
 #pragma once
 
-#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
 
 #include "qlinear_dev.h"
 
@@ -52,14 +52,8 @@ inline int validate_weights(int qtype, const void* w, const void* s, int senc, i
     return VIPER_OK;
 }
 
-inline void launch(const void* fn, unsigned grid, unsigned block, size_t lds, hipStream_t st,
-                   void** args, hipEvent_t ev0, hipEvent_t ev1) {
-    // Events (when given) are attached to this dispatch, so they time the
-    // kernel itself rather than the host-side launch.
-    if (ev0 == nullptr && ev1 == nullptr)
-        (void)hipLaunchKernel(fn, dim3(grid), dim3(block), args, lds, st);
-    else
-        (void)hipExtLaunchKernel(fn, dim3(grid), dim3(block), args, lds, st, ev0, ev1, 0);
+inline void launch(const void* fn, unsigned grid, unsigned block, size_t lds, hipStream_t st, void** args) {
+    (void)hipLaunchKernel(fn, dim3(grid), dim3(block), args, lds, st);
 }
 
 inline int device_cus() {
@@ -99,8 +93,7 @@ bool m1_folded_ok(int qtype, int K, int N);
 // M (1..4) activation rows: M > 1 needs one matrix, PRO_BF16 or PRO_INT8 and
 // m1_rows_ok (x, y, res and part hold M rows).
 int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
-              const M1Out* outs, int nouts, const void* res, int32_t* part, hipStream_t st,
-              hipEvent_t ev0, hipEvent_t ev1, int M = 1);
+              const M1Out* outs, int nouts, const void* res, int32_t* part, hipStream_t st, int M = 1);
 bool m1_rows_ok(int qtype, int K, int M);
 // M = 1 gate/up pair (one shape) with the swiglu epilogue: h = bf16(silu(g)
 // * u) from the bf16-rounded outputs; g_out / u_out may be null.  Prologue
@@ -111,8 +104,7 @@ int launch_m1_swiglu(int qtype, int senc, int K, int pro, const void* x, const v
 
 // M <= 16 over prequantized activations, v_dot4 (qgemm_pre.hip).
 int launch_pre(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
-               const void* xs, int M, void* y, const void* res, int32_t* part, hipStream_t st,
-               hipEvent_t ev0, hipEvent_t ev1);
+               const void* xs, int M, void* y, const void* res, int32_t* part, hipStream_t st);
 
 // M = 2..16 on the i8 matrix cores (qgemm_mfma.hip): needs K a multiple of
 // two groups and 4-byte aligned scales.  xnat: activations in the layout of
@@ -128,21 +120,22 @@ bool mfma_ok(int qtype, int K, int M, const void* s);
 enum { RC_FRAG = 0, RC_NAT = 1, RC_BF16 = 2 };
 bool rc_ok(int qtype, int K);
 bool rc_bf16_ok(int qtype, int N, int K, int M, bool pair);
-// K split of the fragment-input launch (long K): sp = fp32 part sums
-// [4][M][N], sc = one counter per row block, at most rc_split_counters(N),
-// zero when the launch starts (the fragment quantize clears them); both in
-// the caller's workspace, rc_split_bytes(N, M) bytes.
+// K split of the fragment-input launch (long K): sp = the parts' sums
+// [4][M][N] as 64-bit {generation, fp32} slots, sc = one counter per row
+// block (rc_split_counters(N) of them, zero when the launch starts) followed
+// by the generation word; the fragment quantize launch clears the counters
+// and increments the generation.  All in the caller's workspace,
+// rc_split_bytes(N, M) bytes.
 constexpr int RC_SK = 4;  // parts of the K split
 bool rc_split_ok(int qtype, int K);
 inline int rc_split_counters(int N) { return (N + 7) / 8; }
 size_t rc_split_bytes(int N, int M);
 int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq, const void* xs,
               int am, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
-              hipStream_t st, hipEvent_t ev0, hipEvent_t ev1, float* sp = nullptr, unsigned* sc = nullptr);
+              hipStream_t st, uint64_t* sp = nullptr, unsigned* sc = nullptr);
 bool mfma_staged(int qtype, int N, int K);
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
-                const void* w1, const void* s1, void* y1, hipStream_t st, hipEvent_t ev0,
-                hipEvent_t ev1, float* sp = nullptr, unsigned* sc = nullptr);
+                const void* w1, const void* s1, void* y1, hipStream_t st, uint64_t* sp = nullptr, unsigned* sc = nullptr);
 
 }  // namespace vq

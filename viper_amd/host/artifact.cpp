@@ -13,6 +13,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <climits>
 #include <cstring>
 
 #include <hip/hip_runtime_api.h>
@@ -47,8 +48,13 @@ struct Reader {
     }
 };
 
-u64 q4_packed(i64 rows, i64 cols) { return (u64)rows * (u64)cols / 2; }
-u64 q4_scales(i64 rows, i64 cols) { return (u64)rows * (u64)(cols / 64) * 2; }
+// Section sizes of a rows x cols Q4_G64 matrix.  The callers pass dimensions
+// of at most INT32_MAX, so the products stay below 2^62; the checked
+// multiply keeps that an invariant rather than an assumption (a wrapped size
+// could match a short file and give views past its end).
+bool mul_ok(u64 a, u64 b, u64* out) { return !__builtin_mul_overflow(a, b, out); }
+bool q4_packed(u64 rows, u64 cols, u64* out) { return mul_ok(rows, cols / 2, out); }
+bool q4_scales(u64 rows, u64 cols, u64* out) { return mul_ok(rows, (cols / 64) * 2, out); }
 
 const char* kLinearName[N_LINEAR] = {"q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"};
 
@@ -71,11 +77,15 @@ Status parse(const u8* data, usize size, Index* out) {
     if (hd.n_layers == 0 || hd.n_passes == 0 || hd.hidden == 0 || hd.intermediate == 0 || hd.n_heads == 0 ||
         hd.n_kv_heads == 0 || hd.head_dim == 0 || hd.vocab == 0)
         return invalid("zero dimension in the header");
-    const i64 H = hd.hidden, I = hd.intermediate, nQ = (i64)hd.n_heads * hd.head_dim,
-              nKV = (i64)hd.n_kv_heads * hd.head_dim;
+    // Every dimension must fit the i32 rows/cols of a weight view (and the
+    // C ABI's int shapes); products of two u32 fields cannot overflow u64.
+    const u64 H = hd.hidden, I = hd.intermediate, nQ = (u64)hd.n_heads * hd.head_dim,
+              nKV = (u64)hd.n_kv_heads * hd.head_dim, V = hd.vocab;
+    for (const u64 dim : {H, I, nQ, nKV, V})
+        if (dim > (u64)INT32_MAX) return invalid("a dimension (or n_heads*head_dim) exceeds INT32_MAX");
     if (H % 64 || I % 64 || nQ % 64) return invalid("hidden, intermediate and n_heads*head_dim must be multiples of 64");
-    const i64 rows[N_LINEAR] = {nQ, nKV, nKV, H, I, I, H};
-    const i64 cols[N_LINEAR] = {H, H, H, nQ, H, H, I};
+    const u64 rows[N_LINEAR] = {nQ, nKV, nKV, H, I, I, H};
+    const u64 cols[N_LINEAR] = {H, H, H, nQ, H, H, I};
 
     Reader r{data, size, kHeaderBytes};
     out->layers.resize(hd.n_layers);
@@ -87,21 +97,27 @@ Status parse(const u8* data, usize size, Index* out) {
                 LinearBlob lb;
                 lb.rows = (i32)rows[i];
                 lb.cols = (i32)cols[i];
-                Status s = r.next(&lb.packed, q4_packed(rows[i], cols[i]), name + " packed");
+                u64 np = 0, ns = 0;
+                if (!q4_packed(rows[i], cols[i], &np) || !q4_scales(rows[i], cols[i], &ns))
+                    return invalid(name + ": size overflows");
+                Status s = r.next(&lb.packed, np, name + " packed");
                 if (!s.ok()) return s;
-                s = r.next(&lb.scales, q4_scales(rows[i], cols[i]), name + " scales");
+                s = r.next(&lb.scales, ns, name + " scales");
                 if (!s.ok()) return s;
                 if (pass == 0) out->layers[l][i] = lb;
             }
         }
     }
-    Status s = r.next(&out->embed, (u64)hd.vocab * (u64)H * 2, "embed_tokens");
+    u64 ne = 0, nhp = 0, nhs = 0;
+    if (!mul_ok(V, H * 2, &ne) || !q4_packed(V, H, &nhp) || !q4_scales(V, H, &nhs))
+        return invalid("embedding / lm_head size overflows");
+    Status s = r.next(&out->embed, ne, "embed_tokens");
     if (!s.ok()) return s;
-    out->lm_head.rows = (i32)hd.vocab;
+    out->lm_head.rows = (i32)V;
     out->lm_head.cols = (i32)H;
-    s = r.next(&out->lm_head.packed, q4_packed(hd.vocab, H), "lm_head packed");
+    s = r.next(&out->lm_head.packed, nhp, "lm_head packed");
     if (!s.ok()) return s;
-    s = r.next(&out->lm_head.scales, q4_scales(hd.vocab, H), "lm_head scales");
+    s = r.next(&out->lm_head.scales, nhs, "lm_head scales");
     if (!s.ok()) return s;
     s = r.next(&out->final_norm, (u64)H * 2, "final norm");
     if (!s.ok()) return s;

@@ -160,13 +160,20 @@ Status linear_forward(const Tensor& w, const Tensor& b, const Tensor& x, Tensor&
             return Status::Unimplemented("linear_forward BF16: lossless weights are not on the quantized path");
         case DType::FP32:
             return Status::Unimplemented("linear_forward FP32: lossless weights are not on the quantized path");
+        // The reference returns UNIMPLEMENTED for every lossy case
+        // (src/viper/linear.cpp:26-32); so does this overload, since a Tensor
+        // cannot carry the group scales: the quantized path is
+        // ops::linear(quant::QuantizedWeight, x, y).
         case DType::Q4_G64:
+            return Status::Unimplemented(
+                "linear_forward Q4_G64: a Tensor cannot carry the group scales; use ops::linear(QuantizedWeight, x, y)");
         case DType::Q5_G64:
         case DType::Q6_G64:
+            return Status::Unimplemented(
+                "linear_forward Q5/Q6: a Tensor cannot carry the group scales; use ops::linear(QuantizedWeight, x, y)");
         case DType::W8_G32:
-            return Status(StatusCode::INVALID_ARGUMENT,
-                          "linear_forward: a Tensor cannot carry the group scales; pass a "
-                          "quant::QuantizedWeight to ops::linear(w, x, y)");
+            return Status::Unimplemented(
+                "linear_forward W8_G32: a Tensor cannot carry the group scales; use ops::linear(QuantizedWeight, x, y)");
         default: return Status(StatusCode::INVALID_ARGUMENT, "linear_forward: bad weight dtype");
     }
 }

@@ -106,7 +106,7 @@ class QuantizedWeight:
     rows: int
     cols: int
     group_size: int = 64
-    scale_enc: ScaleEnc = ScaleEnc.FP16
+    scale_enc: ScaleEnc = ScaleEnc.BF16
 
 
 _lib = None
@@ -119,7 +119,6 @@ _SYMBOLS = (
     "viper_hip_quantize_act",
     "viper_hip_qlinear_prequantized",
     "viper_hip_qlinear_partials",
-    "viper_hip_qlinear_timed",
     "viper_hip_check_quantizer",
     "viper_hip_stream_read",
     "viper_hip_qlinear_fused2",
@@ -156,8 +155,6 @@ def lib():
     L.viper_hip_qlinear_prequantized.restype = i32
     L.viper_hip_qlinear_partials.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp, vp]
     L.viper_hip_qlinear_partials.restype = i32
-    L.viper_hip_qlinear_timed.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp, vp, vp]
-    L.viper_hip_qlinear_timed.restype = i32
     L.viper_hip_check_quantizer.argtypes = [i32, i32, vp, vp]
     L.viper_hip_check_quantizer.restype = i32
     L.viper_hip_stream_read.argtypes = [vp, sz, vp, vp]
