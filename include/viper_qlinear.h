@@ -211,6 +211,22 @@ int viper_hip_linear_bf16(const void* w_bf16, const void* x_bf16, void* y_bf16, 
  * never wins; a row with nothing above -inf gives 0. */
 int viper_hip_sampling_greedy(const void* logits_bf16, int32_t* out_token, int B, int V, void* stream);
 
+/* viper_hip_qlinear without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference (whose
+ * multi-row path hides a lazily cudaMalloc'd static buffer,
+ * kernels/ops/linear_multim.cu:133-146).  The workspace is a static device
+ * array of VIPER_QLINEAR_STATIC_SCRATCH_BYTES per GPU, held until the process
+ * ends; the call allocates nothing.  Shapes whose
+ * viper_hip_qlinear_workspace_bytes() exceeds it return INVALID_ARGUMENT.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one
+ * GPU (concurrent streams or host threads) race; calls ordered on one stream
+ * do not.  Results equal viper_hip_qlinear's bit for bit. */
+#define VIPER_QLINEAR_STATIC_SCRATCH_BYTES (8u << 20)
+int viper_hip_qlinear_static(int qtype, const void* w_packed, const void* w_scales, int scale_enc,
+                             int group, int N, int K, const void* x_bf16, int M, void* y_bf16,
+                             const void* residual_bf16, void* stream);
+
 /* viper_hip_qlinear, also writing D[M][N][K/group] int32 (test use). */
 int viper_hip_qlinear_partials(int qtype, const void* w_packed, const void* w_scales,
                                int scale_enc, int group, int N, int K, const void* x_bf16, int M,

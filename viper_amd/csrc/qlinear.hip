@@ -28,7 +28,39 @@
 
 #include "qlinear_host.h"
 
+#include <mutex>
+
 namespace vq {
+
+// ------------------------------------------------ allocation-free entry point
+
+// The workspace of viper_hip_qlinear_static: a file-scope device array, one
+// copy on every device the library runs on, held until the process ends.  In
+// host code `scratch` names a host-side stand-in, never device memory: the
+// device address comes from hipGetSymbolAddress, taken once per device with
+// that device current and kept in scratch_dev.
+constexpr size_t STATIC_SCRATCH_BYTES = VIPER_QLINEAR_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) uint8_t scratch[STATIC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+static std::mutex scratch_mu;
+static void* scratch_dev[MAX_DEVICES];
+
+// Device address of the current device's scratch (looked up on its first use).
+static int scratch_address(void** out) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return VIPER_DEVICE_ERROR;
+    if (dev < 0 || dev >= MAX_DEVICES) return VIPER_INTERNAL;
+    std::lock_guard<std::mutex> lock(scratch_mu);
+    if (scratch_dev[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || p == nullptr) return VIPER_DEVICE_ERROR;
+        scratch_dev[dev] = p;
+    }
+    *out = scratch_dev[dev];
+    return VIPER_OK;
+}
 
 // ------------------------------------------------ standalone activation quantize
 
@@ -350,6 +382,20 @@ extern "C" int viper_hip_qlinear(int qtype, const void* w_packed, const void* w_
                                  size_t workspace_bytes, void* stream) {
     return vq::qlinear_common(qtype, w_packed, w_scales, scale_enc, group, N, K, x_bf16, M, y_bf16,
                               residual_bf16, workspace, workspace_bytes, nullptr, stream);
+}
+
+extern "C" int viper_hip_qlinear_static(int qtype, const void* w_packed, const void* w_scales, int scale_enc,
+                                        int group, int N, int K, const void* x_bf16, int M, void* y_bf16,
+                                        const void* residual_bf16, void* stream) {
+    const size_t need = vq::workspace_need(qtype, N, K, M);
+    if (need > vq::STATIC_SCRATCH_BYTES) return VIPER_INVALID_ARGUMENT;
+    void* wsp = nullptr;
+    if (need > 0) {
+        const int rc = vq::scratch_address(&wsp);
+        if (rc != VIPER_OK) return rc;
+    }
+    return vq::qlinear_common(qtype, w_packed, w_scales, scale_enc, group, N, K, x_bf16, M, y_bf16, residual_bf16,
+                              wsp, need > 0 ? vq::STATIC_SCRATCH_BYTES : 0, nullptr, stream);
 }
 
 extern "C" int viper_hip_qlinear_partials(int qtype, const void* w_packed, const void* w_scales,

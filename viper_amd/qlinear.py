@@ -129,6 +129,7 @@ _SYMBOLS = (
     "viper_hip_sampling_greedy",
     "viper_hip_qlinear_m1",
     "viper_hip_qlinear_m1_swiglu",
+    "viper_hip_qlinear_static",
 )
 
 
@@ -155,6 +156,8 @@ def lib():
     L.viper_hip_qlinear_prequantized.restype = i32
     L.viper_hip_qlinear_partials.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp, vp]
     L.viper_hip_qlinear_partials.restype = i32
+    L.viper_hip_qlinear_static.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp]
+    L.viper_hip_qlinear_static.restype = i32
     L.viper_hip_check_quantizer.argtypes = [i32, i32, vp, vp]
     L.viper_hip_check_quantizer.restype = i32
     L.viper_hip_stream_read.argtypes = [vp, sz, vp, vp]
