@@ -116,9 +116,9 @@ struct RcSeg {
 // of the atomic accesses to each slot, not on any ordering between the
 // slots and the counter.  (An agent-scope release/acquire pair would order
 // them but costs a write-back and an invalidate of the XCD's L2 per
-// workgroup: 70 us on the down shape.)  Each part also waits for its own
-// slot stores to complete before it counts (vmcnt 0), so in practice the
-// first read already holds the current generation.
+// workgroup: 70 us on the down shape.)  A part counts as soon as its slot
+// stores are issued; the last part requests every slot at once, then
+// re-reads any that still holds an earlier generation.
 template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, int SK = 1, bool PR = true>
 __global__ void __launch_bounds__(64 * W)
 qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
@@ -420,10 +420,14 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         for (int r = 0; r < 4; ++r) red[((wave * T + t) * 4 + r) * 64 + L] = acc[t][r];
     __syncthreads();
     constexpr int MINE = (4 * T + W - 1) / W;
-    float mine[MINE];
+    float mine[MINE] = {};
     const int kpart = SK > 1 ? (int)(blockIdx.x % SK) : 0;
+    // K split: this call's generation (the word after the counters, written by
+    // the preceding quantize launch), read once the sums are formed: issued
+    // earlier as a vector load among the weights it cost 2 us of the
+    // down-shape launch
     unsigned gen = 0;
-    if constexpr (SK > 1) gen = sc[(N + 7) / 8];  // written by the previous launch
+    if constexpr (SK > 1) gen = sc[(N + 7) / 8];
 #pragma unroll
     for (int i = 0; i < MINE; ++i) {
         const int sl = wave + i * W;
@@ -446,12 +450,33 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         }
     }
     if constexpr (SK > 1) {
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        // count once every wave's slot stores are issued; a slot whose store
+        // is still in flight when the last part reads it is re-read (waiting
+        // for the stores to complete before counting measured 0.4 us slower)
+        lds_barrier();
         int* last = (int*)red;
         if (tid == 0) last[0] = atomicAdd(sc + bid, 1u) == (unsigned)(SK - 1);
-        __syncthreads();
+        lds_barrier();
         if (!last[0]) return;
+        // every slot of the other parts is requested at once (a load that
+        // waited for the previous one's tag would serialise the round trips:
+        // 0.4 us of the down-shape launch), then the tags are checked and a
+        // slot still holding an earlier generation is re-read
+        uint64_t u[MINE][SK];
+#pragma unroll
+        for (int i = 0; i < MINE; ++i) {
+            const int sl = wave + i * W;
+            const int t = sl >> 2, r = sl & 3;
+            const int m = 4 * kb + r, nl = 16 * t + n16;
+            const bool ok = sl < 4 * T && m < M && nl < nrows;
+            const size_t o = (size_t)m * N + row0 + nl;
+#pragma unroll
+            for (int p = 0; p < SK; ++p) {
+                u[i][p] = ((uint64_t)gen << 32) | __float_as_uint(mine[i]);
+                if (ok && p != kpart)
+                    u[i][p] = __hip_atomic_load(sp + (size_t)p * M * N + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
 #pragma unroll
         for (int i = 0; i < MINE; ++i) {
             const int sl = wave + i * W;
@@ -463,15 +488,13 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                 float v = 0.0f;
 #pragma unroll
                 for (int p = 0; p < SK; ++p) {
-                    float vp = mine[i];
-                    if (p != kpart) {
+                    uint64_t w = u[i][p];
+                    if (__builtin_expect((unsigned)(w >> 32) != gen, 0)) {
                         uint64_t* a = sp + (size_t)p * M * N + o;
-                        uint64_t u = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        for (int it = 0; (unsigned)(u >> 32) != gen && it < RC_SPIN; ++it)
-                            u = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        vp = (unsigned)(u >> 32) == gen ? __uint_as_float((unsigned)u) : __builtin_nanf("");
+                        for (int it = 0; (unsigned)(w >> 32) != gen && it < RC_SPIN; ++it)
+                            w = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
-                    v += vp;
+                    v += (unsigned)(w >> 32) == gen ? __uint_as_float((unsigned)w) : __builtin_nanf("");
                 }
                 if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
                 y[o] = f2bf(v);

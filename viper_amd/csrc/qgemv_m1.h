@@ -38,7 +38,8 @@ namespace vq {
 
 constexpr int M1_XS = 4;    // activation octets per thread loaded before the weights
 constexpr int M1_XS_MR = 8; // the same for MR > 1 rows (all of them: no later rounds)
-constexpr int M1_DELAY = 6; // weight-issue delay, s_sleep units
+constexpr int M1_DELAY = 6; // weight-issue delay, s_sleep units (one activation row)
+constexpr int M1_DELAY_MR = 8; // the same for MR > 1 rows (MR rows of activation ahead of the weights)
 
 // Row length of an exact tiling (TS lanes x CPL chunks of CK weights): an
 // exact launch's K is this constant, so its load rounds and offsets are
@@ -210,7 +211,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     constexpr int KX = EXACT ? m1_exact_k<F>(TS, CPL) : 0;
     const int grid = K;
     if constexpr (EXACT) K = KX;
-    constexpr int XS = MR > 1 ? M1_XS_MR : EXACT ? (KX / 8 + NTT - 1) / NTT : M1_XS;
+    constexpr int XS = EXACT ? (MR * (KX / 8) + NTT - 1) / NTT : MR > 1 ? M1_XS_MR : M1_XS;
     constexpr int ROWS = NTT / TS;
     const int M = MR == 1 ? 1 : e1;  // activation rows
     constexpr int HB = FT::HIW * 4;  // high-plane bytes per chunk: Q5 4, Q6 8
@@ -551,7 +552,7 @@ m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
 #define VQ_M1(TS_, NTT_, CPL_)                                                                      \
     if constexpr ((MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_)) && (MR == 1 || m1_mr_shape_ok(TS_, NTT_, CPL_))) \
         if (ts == TS_ && ntt == NTT_ && cpl == CPL_)                                                \
-            return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, MR, M1_DELAY>;
+            return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, MR, MR == 1 ? M1_DELAY : M1_DELAY_MR>;
     VQ_M1(8, 128, 10) VQ_M1(8, 192, 10) VQ_M1(8, 320, 10) VQ_M1(16, 256, 10) VQ_M1(16, 640, 10)
     VQ_M1(32, 320, 10) VQ_M1(32, 640, 10) VQ_M1(64, 640, 10) VQ_M1(16, 256, 5) VQ_M1(16, 320, 5)
     VQ_M1(16, 640, 5) VQ_M1(32, 640, 5) VQ_M1(64, 640, 5)
