@@ -19,6 +19,7 @@ semantics, seeded inputs), timed on this host with 1 and all threads.
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
 import argparse
+import ctypes as C
 import json
 import math
 import os
@@ -31,6 +32,7 @@ sys.path.insert(0, ROOT)
 METRIC = "Q4_G64 GEMV µs + achieved HBM GB/s (% of peak) at M=1; M=16 verify µs"
 PEAK_GBS = 8000.0
 ROTATE_BYTES = 512 * 1024 * 1024
+MIN_STEPS, MIN_WARMUP = 200, 20
 
 
 def algorithmic_bytes(qtype_bytes_per_row, N, K, M, G=64):
@@ -87,6 +89,18 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False):
     return round(us, 3), round(alg / (us * 1e-6) / 1e9, 1)
 
 
+def capture_n(torch, launch, n):
+    """One HIP graph holding exactly n launches (launch(i) for i < n, i picks the weight copy)."""
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(n):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    return graph
+
+
 def capture(torch, launch, copies, steps):
     """One HIP graph holding one launch per weight copy; replays to cover steps."""
     torch.cuda.synchronize()
@@ -135,6 +149,114 @@ def cpu_baseline(N, K, reps_1t, reps_mt):
     return t1, tm, nthreads
 
 
+# ---- the streaming-read floor -----------------------------------------------------------
+
+SWEEP_SHAPES = [(64, 16), (128, 10), (256, 5), (256, 10), (320, 5), (320, 10), (512, 5), (512, 8), (640, 5),
+                (640, 10), (1024, 4), (1024, 8)]
+SWEEP_MB = [13.1072, 28, 56, 112, 557]
+
+
+def _time_probe(torch, L, pool, nbytes, threads, loads, y=None, launches=200):
+    """us per dispatch of viper_hip_stream_read over rotating slices of pool (>= 512 MB of distinct
+    data, or >= 2 slices for large sizes)."""
+    stride = (nbytes + 65535) // 65536 * 65536
+    copies = max(2, min(40, pool.numel() // stride))
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    base = pool.data_ptr()
+    yp = None if y is None else y.data_ptr()
+
+    def launch(i):
+        st = torch.cuda.current_stream().cuda_stream   # the capture stream while a graph is captured
+        rc = L.viper_hip_stream_read(base + (i % copies) * stride, nbytes, threads, loads, yp, sink.data_ptr(), st)
+        if rc != 0:
+            raise RuntimeError(f"stream_read {threads}x{loads} {nbytes} failed: {rc}")
+    n = max(launches, 2 * copies)
+    for i in range(2 * copies):
+        launch(i)
+    g = capture_n(torch, launch, n)
+    us = time_graph(torch, g, 1) * 1e3 / n
+    del g
+    return us
+
+
+def read_sweep(torch, L, gen):
+    """Launch shapes x sizes of the GEMV-pattern streaming read; per shape a least-squares fit
+    t = fixed + bytes / bandwidth over the sizes; then the north-star I/O ladder at the GEMV's shape."""
+    pool = torch.randint(0, 256, (1200 << 20,), dtype=torch.uint8, device="cuda", generator=gen)
+    best13 = None
+    for threads, loads in SWEEP_SHAPES:
+        per_wg = threads * loads * 16
+        pts = []
+        for mb in SWEEP_MB:
+            nbytes = max(1, round(mb * 1e6 / per_wg)) * per_wg
+            us = _time_probe(torch, L, pool, nbytes, threads, loads, launches=200 if mb < 100 else 40)
+            pts.append((nbytes, us))
+        xs = [b / 1e6 for b, _ in pts]
+        ys = [u for _, u in pts]
+        n = len(xs)
+        mx, my = sum(xs) / n, sum(ys) / n
+        slope = sum((a - mx) * (b - my) for a, b in zip(xs, ys)) / sum((a - mx) ** 2 for a in xs)
+        fixed = my - slope * mx
+        line = {"probe": "stream_read", "threads": threads, "loads_per_lane": loads,
+                "points_bytes_us": [[b, round(u, 3)] for b, u in pts],
+                "fit_fixed_us": round(fixed, 3), "fit_gbs": round(1e3 / slope, 1)}
+        print(json.dumps(line), flush=True)
+        if best13 is None or pts[0][1] < best13[1]:
+            best13 = ((threads, loads), pts[0][1], pts[0][0])
+    print(json.dumps({"probe": "best_13MB_shape", "threads": best13[0][0], "loads_per_lane": best13[0][1],
+                      "bytes": best13[2], "us": round(best13[1], 3)}), flush=True)
+    # the north-star GEMV's I/O at its own launch shape (320 threads, 5 loads per lane): weights only,
+    # weights + scales (13,952,000 bytes = 545 workgroups), and the same with one bf16 store per row
+    y = torch.empty(545 * 20, dtype=torch.int16, device="cuda")
+    ladder = {"probe": "north_star_io_ladder"}
+    ladder["read_13107200_us"] = round(_time_probe(torch, L, pool, 13107200, 320, 5), 3)
+    ladder["read_13952000_us"] = round(_time_probe(torch, L, pool, 13952000, 320, 5), 3)
+    ladder["read_13952000_store_rows_us"] = round(_time_probe(torch, L, pool, 13952000, 320, 5, y=y), 3)
+    print(json.dumps(ladder), flush=True)
+    del pool
+
+
+def timeline(torch, L, gen, N, K):
+    """Per-wave timeline of the north-star GEMV: percentiles of each stamp over all waves of one
+    dispatch (the last of a back-to-back sequence over rotating weights), in us from the first wave's
+    start."""
+    copy_bytes = N * K // 2 + N * (K // 64) * 2
+    copies = max(2, -(-ROTATE_BYTES // copy_bytes) + 1)
+    W, S = make_weights(torch, copies, N, K, gen)
+    x = torch.randn((1, K), device="cuda", generator=gen).to(torch.bfloat16)
+    y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+    stamps = torch.zeros(1 << 20, dtype=torch.int64, device="cuda")
+    grid, waves = C.c_int(0), C.c_int(0)
+
+    def launch(i):
+        c = i % copies
+        st = torch.cuda.current_stream().cuda_stream   # the capture stream while a graph is captured
+        rc = L.viper_hip_qlinear_timeline(4, W[c].data_ptr(), S[c].data_ptr(), 0, 64, N, K, x.data_ptr(),
+                                          y.data_ptr(), stamps.data_ptr(), stamps.numel() * 8, C.byref(grid),
+                                          C.byref(waves), st)
+        if rc != 0:
+            raise RuntimeError(f"timeline failed: {rc}")
+    for i in range(50):
+        launch(i)
+    g = capture_n(torch, launch, 400)
+    us = time_graph(torch, g, 1) * 1e3 / 400
+    g.replay()
+    torch.cuda.synchronize()
+    nw = grid.value * waves.value
+    t = stamps[: nw * 8].view(nw, 8).cpu().numpy()
+    t = (t - t[:, 0].min()) * 0.01       # 100 MHz ticks -> us
+    names = ["wave start", "activation + scale loads issued", "weight loads issued", "activation quantized",
+             "barrier passed", "first chunk dotted", "last chunk dotted", "output stored"]
+    import numpy as np
+    rows = {}
+    for i, nm in enumerate(names):
+        v = np.sort(t[:, i])
+        rows[nm] = [round(float(np.percentile(v, p)), 3) for p in (10, 50, 90)] + [round(float(v[-1]), 3)]
+    print(json.dumps({"timeline": "qgemv_m1 Q4_G64 K=2560 N=10240", "workgroups": grid.value,
+                      "waves_per_workgroup": waves.value, "us_per_launch_stamped": round(us, 3),
+                      "percentiles_us_p10_p50_p90_max": rows}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,6 +268,14 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip the M=16 and down-shape lines")
     ap.add_argument("--m16-only", action="store_true",
                     help="only time the M=16 verify (K=2560, N=10240) line (rocprofv3 counter runs)")
+    ap.add_argument("--read-sweep", action="store_true",
+                    help="only the streaming-read floor: launch shapes x sizes, fixed cost + bandwidth fit, and "
+                         "the north-star I/O ladder (JSON lines)")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only the per-wave timeline of the north-star GEMV (viper_hip_qlinear_timeline)")
+    ap.add_argument("--only", default="", metavar="LINE",
+                    help="only one line (rocprofv3 runs): config0, down, verify_mM (K=2560 N=10240) or "
+                         "verify_mM_down (K=10240 N=2560), q5_m1 / q6_m8 / w8_m1 ... (config 4)")
     ap.add_argument("--verify-only", type=int, default=0, metavar="M",
                     help="only time the M-row verify (K=2560, N=10240) line (rocprofv3 runs)")
     args = ap.parse_args()
@@ -174,6 +304,30 @@ def main():
 
     N, K, M = 10240, 2560, 1
     qtype, G = int(va.QType.Q4_G64), 64
+    if args.only:
+        one = args.only
+        if one == "config0":
+            res = time_linear(torch, L, gen, qtype, 2560, 2560, 1, steps=args.steps)
+        elif one == "down":
+            res = time_linear(torch, L, gen, qtype, 2560, 10240, 1, steps=args.steps)
+        elif one.startswith("verify_m"):
+            Mv = int(one[len("verify_m"):].split("_")[0])
+            shape = (2560, 10240) if one.endswith("_down") else (10240, 2560)
+            res = time_linear(torch, L, gen, qtype, shape[0], shape[1], Mv, steps=args.steps)
+        elif one[:1] in "qw" and "_m" in one:
+            fmt, mpart = one.split("_m")
+            qt = {"q5": 5, "q6": 6, "w8": 8}[fmt]
+            res = time_linear(torch, L, gen, qt, N, K, int(mpart), steps=args.steps, outliers=True)
+        else:
+            raise SystemExit(f"unknown --only line {one}")
+        print(json.dumps({"line": one, "us": res[0], "gbs": res[1]}), flush=True)
+        return
+    if args.read_sweep:
+        read_sweep(torch, L, gen)
+        return
+    if args.timeline:
+        timeline(torch, L, gen, N, K)
+        return
     if args.m16_only or args.verify_only:
         Mv = 16 if args.m16_only else args.verify_only
         us, gbs = time_linear(torch, L, gen, qtype, N, K, Mv, steps=args.steps)
@@ -195,11 +349,14 @@ def main():
         if rc != 0:
             raise RuntimeError(f"viper_hip_qlinear failed: {rc}")
 
-    for i in range(args.warmup):
+    # at least MIN_STEPS timed dispatches after at least MIN_WARMUP warm-ups,
+    # whatever --steps / --warmup ask (both counts are reported)
+    steps = max(args.steps, MIN_STEPS)
+    warmup = max(args.warmup, MIN_WARMUP)
+    for i in range(warmup):
         launch(i)
-    graph, replays = capture(torch, launch, copies, args.steps)
-    steps = replays * copies
-    job_ms = time_graph(torch, graph, replays)
+    graph = capture_n(torch, launch, steps)
+    job_ms = time_graph(torch, graph, 1)
     ms_per_step = job_ms / steps
     value = alg * steps / (job_ms * 1e-3) / 1e9
     achieved = value
@@ -212,7 +369,7 @@ def main():
         wbytes = N * K // 2
 
         def launch_read(i):
-            rc = L.viper_hip_stream_read(wp[i % copies], wbytes, sink.data_ptr(),
+            rc = L.viper_hip_stream_read(wp[i % copies], wbytes, 320, 5, None, sink.data_ptr(),
                                          torch.cuda.current_stream().cuda_stream)
             if rc != 0:
                 raise RuntimeError(f"viper_hip_stream_read failed: {rc}")
@@ -433,7 +590,9 @@ def main():
         "unit": "GB/s",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
+        "steps_requested": args.steps,
+        "warmup_requested": args.warmup,
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -443,7 +602,8 @@ def main():
         "config": {"workload": "Q4_G64 GEMV M=1 K=2560 N=10240 (north star), fused bf16->int8 quantize",
                    "qtype": "Q4_G64", "M": M, "K": K, "N": N, "weight_copies": copies,
                    "rotation_bytes": copies * copy_bytes, "algorithmic_bytes_per_step": alg,
-                   "timed_region": "HIP graph replays, one launch per weight copy, events on the stream"},
+                   "timed_region": (f"one HIP graph of {steps} launches cycling over the weight copies, replayed once "
+                                    f"after {warmup} eager warm-up launches and one untimed replay; events on the stream")},
         "us_per_gemv": round(ms_per_step * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic},

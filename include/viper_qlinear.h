@@ -46,11 +46,14 @@
  *   viper_hip_sampling_greedy       sampling_greedy_bf16 (kernels/ops/sampling_kernel.cu:66-80).
  *   viper_hip_qlinear_partials      no counterpart: the same kernels, also writing
  *                                   the exact per-group int32 dots for parity tests.
+ *   viper_hip_qlinear_timeline      no counterpart: the M = 1 GEMV with per-wave
+ *                                   timestamps (measurement).
  *   viper_hip_check_quantizer       no counterpart: device self-check of the
  *                                   activation quantizer's rounding.
  *   viper_hip_stream_read           no counterpart: reads a buffer once with the
- *                                   M = 1 GEMV's launch shape (measurement: the
- *                                   floor of one streaming dispatch).
+ *                                   M = 1 GEMV's load pattern and a given launch
+ *                                   shape (measurement: the floor of one
+ *                                   streaming dispatch).
  *
  * Formats (qtype values are viper::quant::QType, include/viper/quant.h:19-26):
  *   Q4_G64 (4)  packed [N][K/2]; k even in the low nibble; nibble = w + 8.
@@ -241,13 +244,32 @@ int viper_hip_qlinear_partials(int qtype, const void* w_packed, const void* w_sc
  * (exp_lo << 7) + i. */
 int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream);
 
-/* Measurement probe, no counterpart in the reference: reads `bytes` (a
- * multiple of 16, 16-byte aligned buffer) once with the launch shape and load
- * pattern of the north-star GEMV (320-thread workgroups, five 16-byte
- * non-temporal loads per lane) and nothing else, so its duration is the
- * floor of one dispatch streaming that many bytes.  sink (4 bytes) is
- * written only if the folded data equals a fixed magic word. */
-int viper_hip_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream);
+/* Measurement entry point, no counterpart in the reference: the M = 1 GEMV
+ * of viper_hip_qlinear (Q4_G64, bf16 x, launch shapes whose lanes tile a row
+ * exactly, e.g. K = 2560) with a per-wave timeline.  Lane 0 of every wave
+ * writes 8 s_memrealtime readings (uint64, 100 MHz) to
+ * stamps[(workgroup * waves + wave) * 8 + i]: wave start, activation and
+ * weight-scale loads issued, weight loads issued, activation quantized into
+ * LDS, workgroup barrier passed, first chunk dotted, last chunk dotted,
+ * output stored.  *workgroups and *waves_per_workgroup (may be NULL) receive
+ * the launch's grid; stamp_bytes must cover it.  y is the GEMV's output; the
+ * readings cost the kernel about 0.2 us. */
+int viper_hip_qlinear_timeline(int qtype, const void* w_packed, const void* w_scales, int scale_enc, int group,
+                               int N, int K, const void* x_bf16, void* y_bf16, uint64_t* stamps, size_t stamp_bytes,
+                               int* workgroups, int* waves_per_workgroup, void* stream);
+
+/* Measurement probe, no counterpart in the reference: the floor of one
+ * dispatch streaming `bytes` with the M = 1 GEMV's load pattern.  Each team
+ * of 16 lanes reads one row of 16 * loads 16-byte chunks (lane l takes chunks
+ * j * 16 + l), with non-temporal loads all issued at once; workgroups of
+ * `threads` threads (64, 128, 256, 320, 512, 640 or 1024) cover threads / 16
+ * rows each, in the GEMV's XCD-aware order; loads is 4, 5, 8, 10 or 16, and
+ * bytes a multiple of threads * loads * 16 (16-byte aligned buffer).  With
+ * y_bf16 (may be NULL) every team also stores one bf16 to y_bf16[row] (the
+ * GEMV's output pattern; bytes / (256 * loads) entries).  Otherwise sink (4
+ * bytes) is written only if the folded data equals a fixed word. */
+int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, void* y_bf16, uint32_t* sink,
+                          void* stream);
 
 #ifdef __cplusplus
 }

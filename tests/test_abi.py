@@ -84,11 +84,15 @@ def test_other_entry_validation():
     assert L.viper_hip_qlinear_partials(4, FAKE, FAKE, 0, 64, 8, 64, FAKE, 1, FAKE, None, None, 0, None, None) == 2
     assert L.viper_hip_check_quantizer(10, 5, FAKE, None) == 2
     assert L.viper_hip_check_quantizer(0, 255, FAKE, None) == 2
-    assert L.viper_hip_stream_read(None, 16, FAKE, None) == 2
-    assert L.viper_hip_stream_read(FAKE, 0, FAKE, None) == 2
-    assert L.viper_hip_stream_read(FAKE, 24, FAKE, None) == 2     # not a multiple of 16
-    assert L.viper_hip_stream_read(FAKE + 8, 16, FAKE, None) == 2  # buffer not 16-byte aligned
-    assert L.viper_hip_stream_read(FAKE, 16, None, None) == 2
+    W = 320 * 5 * 16                                                      # one workgroup's bytes
+    assert L.viper_hip_stream_read(None, W, 320, 5, None, FAKE, None) == 2
+    assert L.viper_hip_stream_read(FAKE, 0, 320, 5, None, FAKE, None) == 2
+    assert L.viper_hip_stream_read(FAKE, W + 16, 320, 5, None, FAKE, None) == 2  # not whole workgroups
+    assert L.viper_hip_stream_read(FAKE + 8, W, 320, 5, None, FAKE, None) == 2   # buffer not 16-byte aligned
+    assert L.viper_hip_stream_read(FAKE, W, 320, 5, None, None, None) == 2
+    assert L.viper_hip_stream_read(FAKE, W, 300, 5, None, FAKE, None) == 2       # no such shape
+    assert L.viper_hip_stream_read(FAKE, W, 320, 6, None, FAKE, None) == 2
+    assert L.viper_hip_stream_read(FAKE, W, 320, 5, FAKE + 1, FAKE, None) == 2   # y not 2-byte aligned
 
 
 def test_registry_mirror():

@@ -637,18 +637,69 @@ def test_quantizer_edge_cases_every_path(torch_dev, qtype, M):
 
 
 def test_stream_read_probe(torch_dev):
-    # the measurement probe reads every byte: a lane whose 16 bytes fold to the
-    # magic word writes it to the sink, zeros leave the sink alone
+    # the measurement probe reads every byte: a lane whose chunks fold to the
+    # magic word writes it to the sink, zeros leave the sink alone; with y,
+    # lane 0 of every 16-lane team stores its fold to y[row] (rows of
+    # 16 * loads 16-byte chunks, any workgroup order)
     torch = torch_dev
     L = va.lib()
-    buf = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    threads, loads = 320, 5
+    rowb = 16 * loads * 16
+    rows = 20 * 40
+    buf = torch.zeros(rows * rowb, dtype=torch.uint8, device="cuda")
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
-    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), sink.data_ptr(), st) == 0
+    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), threads, loads, None, sink.data_ptr(), st) == 0
     torch.cuda.synchronize()
     assert int(sink[0]) == 0
     words = buf.view(torch.int32)
-    words[(1 << 18) - 4] = np.int32(np.uint32(0x9E3779B9).view(np.int32))   # the last 16 bytes
-    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), sink.data_ptr(), st) == 0
+    words[buf.numel() // 4 - 4] = np.int32(np.uint32(0x9E3779B9).view(np.int32))   # the last 16 bytes
+    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), threads, loads, None, sink.data_ptr(), st) == 0
     torch.cuda.synchronize()
     assert np.uint32(int(sink[0]) & 0xFFFFFFFF) == np.uint32(0x9E3779B9)
+    buf.zero_()
+    words[torch.arange(rows, device="cuda") * (rowb // 4)] = torch.arange(rows, dtype=torch.int32, device="cuda")
+    y = torch.full((buf.numel() // (16 * 4 * 16),), -1, dtype=torch.int16, device="cuda")   # rows of the smallest row size
+    for th, ld in ((320, 5), (640, 5), (64, 16), (1024, 4)):
+        rb = 16 * ld * 16
+        n = buf.numel() // (th * ld * 16) * (th * ld * 16)
+        assert n // rb <= y.numel()
+        words.zero_()
+        words[torch.arange(n // rb, device="cuda") * (rb // 4)] = torch.arange(n // rb, dtype=torch.int32, device="cuda")
+        y.fill_(-1)
+        assert L.viper_hip_stream_read(buf.data_ptr(), n, th, ld, y.data_ptr(), sink.data_ptr(), st) == 0
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()[: n // rb].astype(np.int64)
+        np.testing.assert_array_equal(got, np.arange(n // rb))
+
+
+def test_timeline_entry_matches_gemv(torch_dev):
+    # the measurement entry point runs the production GEMV with stamps: y equal
+    # to viper_hip_qlinear's bit for bit, 8 non-decreasing readings per wave,
+    # and shapes without an exact tiling (or another format) rejected
+    import ctypes as C
+    torch = torch_dev
+    L = va.lib()
+    N, K = 4000, 2560
+    packed, scales = O.gen_weights(O.Q4_G64, N, K, 0x71, O.SCALE_FP16)
+    x = O.gen_act(1, K, 0x72)
+    wd, sd, xd = dev(torch, packed), dev(torch, scales), dev(torch, x)
+    y0 = torch.zeros((1, N), dtype=torch.int16, device="cuda")
+    y1 = torch.full((1, N), 7, dtype=torch.int16, device="cuda")
+    stamps = torch.zeros(1 << 18, dtype=torch.int64, device="cuda")
+    grid, waves = C.c_int(0), C.c_int(0)
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.viper_hip_qlinear(4, wd.data_ptr(), sd.data_ptr(), 0, 64, N, K, xd.data_ptr(), 1, y0.data_ptr(),
+                               None, None, 0, st) == 0
+    assert L.viper_hip_qlinear_timeline(4, wd.data_ptr(), sd.data_ptr(), 0, 64, N, K, xd.data_ptr(), y1.data_ptr(),
+                                        stamps.data_ptr(), stamps.numel() * 8, C.byref(grid), C.byref(waves), st) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(y1, np.uint16), host(y0, np.uint16))
+    nw = grid.value * waves.value
+    assert nw > 0
+    t = stamps[: nw * 8].view(nw, 8).cpu().numpy()
+    assert (np.diff(t, axis=1) >= 0).all() and (t[:, 0] > 0).all()
+    assert L.viper_hip_qlinear_timeline(4, wd.data_ptr(), sd.data_ptr(), 0, 64, N, K, xd.data_ptr(), y1.data_ptr(),
+                                        stamps.data_ptr(), 64, None, None, st) == 2          # stamps too small
+    assert L.viper_hip_qlinear_timeline(4, wd.data_ptr(), sd.data_ptr(), 0, 64, N, 2496, xd.data_ptr(),
+                                        y1.data_ptr(), stamps.data_ptr(), stamps.numel() * 8, None, None, st) == 2

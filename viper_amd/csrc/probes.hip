@@ -1,0 +1,77 @@
+// Measurement probe (no counterpart in the reference): the floor of one
+// dispatch that streams a buffer with the M = 1 GEMV's load pattern.
+#include "qlinear_host.h"
+
+namespace vq {
+
+// A team of 16 lanes reads one "row" of 16 * L 16-byte chunks, lane l taking
+// chunks j * 16 + l (j < L) with 16-byte non-temporal loads, all issued at
+// once: the GEMV's pattern (north star: 1280-byte rows, L = 5).  A workgroup
+// of NTT threads covers NTT / 16 consecutive rows, workgroups in the
+// XCD-aware order of the GEMV.  Nothing else happens to the data: the words
+// are folded so the loads stay live.  With y, lane 0 of each team stores one
+// bf16 (the fold) to y[row], the GEMV's output pattern; without it the fold
+// reaches memory only in the (never expected) case that it equals a magic
+// word.
+template <int NTT, int L>
+__global__ void __launch_bounds__(NTT) stream_probe_kernel(const uint8_t* p, uint16_t* y, uint32_t* sink) {
+    constexpr int ROWS = NTT / 16, RB = 16 * L * 16;
+    const int b = xcd_block((int)blockIdx.x, (int)gridDim.x);
+    const int tid = (int)threadIdx.x, l = tid & 15, rr = tid >> 4;
+    const auto r = buf(p + (size_t)b * ROWS * RB, (uint32_t)(ROWS * RB));
+    u32x4 v[L];
+#pragma unroll
+    for (int j = 0; j < L; ++j) v[j] = bload16<AUX_NT>(r, rr * RB + (j * 16 + l) * 16);
+    uint32_t f = 0u;
+#pragma unroll
+    for (int j = 0; j < L; ++j) f ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
+    if (y != nullptr) {
+        if (l == 0) y[(size_t)b * ROWS + rr] = (uint16_t)f;
+    } else if (f == 0x9E3779B9u) {
+        sink[0] = f;
+    }
+}
+
+typedef void (*probe_fn)(const uint8_t*, uint16_t*, uint32_t*);
+
+template <int NTT>
+static probe_fn probe_l(int loads) {
+    switch (loads) {
+        case 4: return stream_probe_kernel<NTT, 4>;
+        case 5: return stream_probe_kernel<NTT, 5>;
+        case 8: return stream_probe_kernel<NTT, 8>;
+        case 10: return stream_probe_kernel<NTT, 10>;
+        case 16: return stream_probe_kernel<NTT, 16>;
+        default: return nullptr;
+    }
+}
+
+static probe_fn probe_kernel(int threads, int loads) {
+    switch (threads) {
+        case 64: return probe_l<64>(loads);
+        case 128: return probe_l<128>(loads);
+        case 256: return probe_l<256>(loads);
+        case 320: return probe_l<320>(loads);
+        case 512: return probe_l<512>(loads);
+        case 640: return probe_l<640>(loads);
+        case 1024: return probe_l<1024>(loads);
+        default: return nullptr;
+    }
+}
+
+}  // namespace vq
+
+extern "C" int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, void* y_bf16,
+                                     uint32_t* sink, void* stream) {
+    const vq::probe_fn fn = vq::probe_kernel(threads, loads);
+    if (fn == nullptr || buf == nullptr || sink == nullptr) return VIPER_INVALID_ARGUMENT;
+    const size_t per_wg = (size_t)threads * (size_t)loads * 16;
+    if (bytes == 0 || bytes % per_wg != 0 || bytes / per_wg > (size_t)INT32_MAX) return VIPER_INVALID_ARGUMENT;
+    if (vq::misaligned(buf, 16) || vq::misaligned(sink, 4) || vq::misaligned(y_bf16, 2)) return VIPER_INVALID_ARGUMENT;
+    const unsigned grid = (unsigned)(bytes / per_wg);
+    const uint8_t* a0 = (const uint8_t*)buf;
+    uint16_t* a1 = (uint16_t*)y_bf16;
+    void* args[] = {&a0, &a1, &sink};
+    vq::launch((const void*)fn, grid, (unsigned)threads, 0, (hipStream_t)stream, args);
+    return vq::status_of(hipGetLastError());
+}

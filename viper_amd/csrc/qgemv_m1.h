@@ -48,25 +48,17 @@ constexpr int M1_DELAY_MR = 8; // the same for MR > 1 rows (MR rows of activatio
 template <int F>
 __host__ __device__ constexpr int m1_exact_k(int ts, int cpl) { return Fmt<F>::CK * ts * cpl; }
 
-// Logical block of workgroup b in a grid of g: the dispatcher deals
-// workgroups to the 8 XCDs in turn (b -> XCD b % 8), so numbering the
-// blocks XCD by XCD gives each XCD one contiguous range of output rows.  Its
-// y stores then fill whole cache lines of one L2 instead of sharing lines
-// with the neighbouring XCDs (north star 4.07 -> 4.03 us).  Any g works: XCD
-// k holds g / 8 blocks, one more when k < g % 8.  The mapping only permutes
-// blocks, so results do not depend on how the hardware deals them.
-__device__ __forceinline__ int xcd_block(int b, int g) {
-    const int k = b & 7;
-    return k * (g >> 3) + min(k, g & 7) + (b >> 3);
-}
-
 // Kernel modes: plain, with the int32 group dots (test entry point), or the
 // gate/up pair with the swiglu epilogue (M1_SWIGLU): the first NTT/2 threads
 // stream P = ROWS/2 rows of the gate matrix (w0), the others the same P rows
 // of the up matrix (w1), and the workgroup writes h = bf16(silu(g) * u) from
 // the two bf16-rounded outputs.  P must be a whole number of waves' teams so
 // every wave reads one matrix.
-enum { M1_PLAIN = 0, M1_PART = 1, M1_SWIGLU = 2 };
+// M1_TL: M1_PLAIN plus a per-wave timeline (measurement entry point
+// viper_hip_qlinear_timeline): the `part` argument then points at
+// [workgroup][wave][M1_TL_STAMPS] uint64 s_memrealtime readings (100 MHz).
+enum { M1_PLAIN = 0, M1_PART = 1, M1_SWIGLU = 2, M1_TL = 3 };
+constexpr int M1_TL_STAMPS = 8;
 __host__ __device__ constexpr bool m1_pair_ok(int ts, int ntt) {
     return (ntt / ts) % 2 == 0 && ((ntt / ts) / 2) % (64 / ts) == 0;
 }
@@ -203,6 +195,15 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     using FT = Fmt<F>;
     constexpr bool PART = MODE == M1_PART;
     constexpr bool SWI = MODE == M1_SWIGLU;
+    constexpr bool TLM = MODE == M1_TL;
+    // timeline stamps (M1_TL only): wave start, activation and scale loads
+    // issued, weight loads issued, activation quantized, barrier passed,
+    // first chunk dotted, last chunk dotted, output stored
+    uint64_t tstamp[M1_TL_STAMPS];
+    auto stamp = [&](int i) {
+        if constexpr (TLM) tstamp[i] = __builtin_amdgcn_s_memrealtime();
+    };
+    stamp(0);
     constexpr bool PRE = PRO == PRO_INT8;
     constexpr bool TWO = PRO == PRO_RMSNORM || PRO == PRO_SWIGLU;  // two bf16 inputs
     // exact tilings: K is the tiling's row length and the argument slot
@@ -359,8 +360,10 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             }
         }
     };
+    stamp(1);
     if constexpr (DELAY > 0) __builtin_amdgcn_s_sleep(DELAY);
     load_seg(0);
+    stamp(2);
 
     // 2. quantize the activation into LDS (trip counts are workgroup-uniform,
     //    so every DPP group reduction sees whole groups).  Q4 stores each
@@ -463,7 +466,9 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
                 if (wave0 + NTT * i < noct) quant_store(tid + NTT * i, load_x(tid + NTT * i));
     }
 
+    stamp(3);
     lds_barrier();
+    stamp(4);
 
     // 3. chunk dots, group sums, fp32 combine (MR > 1: the loop after this one).  Every LDS operand of the
     //    segment is read before the first dot: the reads then overlap the
@@ -512,8 +517,10 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             if constexpr (EXACT) scj = SC[j];
             else scj = (SENC ? bf16f(sv[j]) : f16f(sv[j])) * __uint_as_float(CS[j].y);
             acc = __builtin_fmaf(scj, (float)dot, acc);
+            if (j == 0) stamp(5);
         }
     }
+    stamp(6);
     acc = team_sum<TS>(acc);
     if constexpr (SWI) {
         // gate values through LDS; y0 / y1 (may be null) receive gate and up,
@@ -533,6 +540,14 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         if (l == 0 && row_ok) {
             if (__builtin_expect(res != nullptr, 0)) acc += bf16f(res[row]);
             y[row] = f2bf(acc);
+        }
+    }
+    if constexpr (TLM) {
+        stamp(7);
+        if ((tid & 63) == 0) {
+            uint64_t* o = (uint64_t*)part + ((size_t)blockIdx.x * (NTT / 64) + (tid >> 6)) * M1_TL_STAMPS;
+#pragma unroll
+            for (int i = 0; i < M1_TL_STAMPS; ++i) o[i] = tstamp[i];
         }
     }
 }
@@ -588,6 +603,12 @@ m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, int mode, bool exact, int 
         }
     }
     if (mr != 1) return nullptr;
+    // the timeline: Q4, bf16 prologue, exact tilings
+    if constexpr (PRO == PRO_BF16 && F == 4)
+        if (mode == M1_TL)
+            return !exact ? nullptr
+                          : senc ? m1_kernel_v<F, 1, M1_TL, true, PRO, 1>(ts, ntt, cpl)
+                                 : m1_kernel_v<F, 0, M1_TL, true, PRO, 1>(ts, ntt, cpl);
     if constexpr (PART_OK)
         if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 1>(ts, ntt, cpl, senc, exact);
     if constexpr (PRO == PRO_BF16 || PRO == PRO_RMSNORM)

@@ -181,6 +181,37 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     return status_of(hipGetLastError());
 }
 
+int launch_m1_timeline(int qtype, int senc, int K, const void* x, const void* w, const void* s, void* y, int N,
+                       uint64_t* stamps, size_t stamp_bytes, int* workgroups, int* waves, hipStream_t st) {
+    if (qtype != VIPER_QTYPE_Q4_G64) return VIPER_INVALID_ARGUMENT;
+    const int noct = K / 8;
+    const M1Shape sh = m1_shape(K / 32, N, device_cus(), 0, noct);
+    if (sh.ntt == 0 || K != m1_exact_k<4>(sh.ts, sh.cpl) || (K / 64) % 8 != 0) return VIPER_INVALID_ARGUMENT;
+    const m1_fn fn = m1_kernel(qtype, sh, senc, M1_TL, true, PRO_BF16);
+    if (fn == nullptr) return VIPER_INTERNAL;
+    const int rows = sh.ntt / sh.ts;
+    const int grid = (N + rows - 1) / rows;
+    const size_t need = (size_t)grid * (sh.ntt / 64) * M1_TL_STAMPS * sizeof(uint64_t);
+    if (stamps == nullptr || stamp_bytes < need) return VIPER_INVALID_ARGUMENT;
+    if (workgroups != nullptr) *workgroups = grid;
+    if (waves != nullptr) *waves = sh.ntt / 64;
+    const size_t lds = lds_m1_launch(qtype, K, rows, true);
+    const uint8_t* w0 = (const uint8_t*)w;
+    const uint16_t* s0 = (const uint16_t*)s;
+    uint16_t* y0 = (uint16_t*)y;
+    int kg = grid, n0 = N, e0 = grid, e1 = grid, nz = 0;
+    const uint16_t* r = nullptr;
+    const void* xa = nullptr;
+    float eps = 0.0f;
+    uint16_t* xout = nullptr;
+    int32_t* part = (int32_t*)stamps;
+    const void* nul = nullptr;
+    void* args[] = {&x, &w0, &s0, &y0, &kg, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,
+                    &nul, &nul, &nul, &nz, &nul, &nul, &nul, &nz};
+    launch((const void*)fn, (unsigned)grid, (unsigned)sh.ntt, lds, st, args);
+    return status_of(hipGetLastError());
+}
+
 int launch_m1_swiglu(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
                      const void* wg, const void* sg, const void* wu, const void* su, int N, void* h, void* g_out,
                      void* u_out, hipStream_t st) {

@@ -189,27 +189,6 @@ __global__ void __launch_bounds__(NT) check_quantizer_kernel(int ab0, int32_t* _
     if (threadIdx.x == 0) counts[blockIdx.x] = red[0];
 }
 
-// --------------------------------------------------- streaming-read probe
-
-// Reads a buffer once with the north-star GEMV's launch shape and load
-// pattern (320-thread workgroups, five 16-byte non-temporal loads per lane,
-// all issued at once) and does nothing else: its duration is what one
-// dispatch streaming those bytes costs here, the floor the GEMV is compared
-// with.  The loaded words are folded so the loads stay; the fold reaches
-// memory only in the (never expected) case that it equals the magic word.
-constexpr int SR_NT = 320, SR_LPT = 5;
-__global__ void __launch_bounds__(SR_NT) stream_read_kernel(const uint8_t* p, uint32_t bytes, uint32_t* sink) {
-    const auto r = buf(p, bytes);
-    const int base = (int)blockIdx.x * SR_NT * SR_LPT * 16;
-    u32x4 v[SR_LPT];
-#pragma unroll
-    for (int j = 0; j < SR_LPT; ++j) v[j] = bload16<AUX_NT>(r, base + (j * SR_NT + (int)threadIdx.x) * 16);
-    uint32_t f = 0u;
-#pragma unroll
-    for (int j = 0; j < SR_LPT; ++j) f ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
-    if (f == 0x9E3779B9u) sink[0] = f;
-}
-
 static int launch_quantize(int group, const void* x, int M, int K, void* xq, void* xs, bool mf,
                            hipStream_t st, unsigned* cnt = nullptr, int ncnt = 0) {
     const int oct_total = M * K / 8;
@@ -499,17 +478,17 @@ extern "C" int viper_hip_qlinear_m1_swiglu(int qtype, int scale_enc, int group, 
                                 h_bf16, gate_bf16, up_bf16, (hipStream_t)stream);
 }
 
-extern "C" int viper_hip_stream_read(const void* buf, size_t bytes, uint32_t* sink, void* stream) {
-    if (buf == nullptr || sink == nullptr || bytes == 0 || bytes % 16 != 0 || bytes > (size_t)INT32_MAX)
+extern "C" int viper_hip_qlinear_timeline(int qtype, const void* w_packed, const void* w_scales, int scale_enc,
+                                          int group, int N, int K, const void* x_bf16, void* y_bf16, uint64_t* stamps,
+                                          size_t stamp_bytes, int* workgroups, int* waves_per_workgroup,
+                                          void* stream) {
+    const int rc = vq::validate_weights(qtype, w_packed, w_scales, scale_enc, group, N, K, 1);
+    if (rc != VIPER_OK) return rc;
+    if (x_bf16 == nullptr || y_bf16 == nullptr || vq::misaligned(x_bf16, 16) || vq::misaligned(y_bf16, 2) ||
+        vq::misaligned(stamps, 8))
         return VIPER_INVALID_ARGUMENT;
-    if (vq::misaligned(buf, 16) || vq::misaligned(sink, 4)) return VIPER_INVALID_ARGUMENT;
-    constexpr size_t per_wg = (size_t)vq::SR_NT * vq::SR_LPT * 16;
-    const unsigned grid = (unsigned)((bytes + per_wg - 1) / per_wg);
-    const uint8_t* a0 = (const uint8_t*)buf;
-    uint32_t n = (uint32_t)bytes;
-    void* args[] = {&a0, &n, &sink};
-    vq::launch((const void*)vq::stream_read_kernel, grid, vq::SR_NT, 0, (hipStream_t)stream, args);
-    return vq::status_of(hipGetLastError());
+    return vq::launch_m1_timeline(qtype, scale_enc, K, x_bf16, w_packed, w_scales, y_bf16, N, stamps, stamp_bytes,
+                                  workgroups, waves_per_workgroup, (hipStream_t)stream);
 }
 
 extern "C" int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream) {

@@ -130,6 +130,7 @@ _SYMBOLS = (
     "viper_hip_qlinear_m1",
     "viper_hip_qlinear_m1_swiglu",
     "viper_hip_qlinear_static",
+    "viper_hip_qlinear_timeline",
 )
 
 
@@ -158,9 +159,11 @@ def lib():
     L.viper_hip_qlinear_partials.restype = i32
     L.viper_hip_qlinear_static.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp]
     L.viper_hip_qlinear_static.restype = i32
+    L.viper_hip_qlinear_timeline.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, vp, vp, sz, vp, vp, vp]
+    L.viper_hip_qlinear_timeline.restype = i32
     L.viper_hip_check_quantizer.argtypes = [i32, i32, vp, vp]
     L.viper_hip_check_quantizer.restype = i32
-    L.viper_hip_stream_read.argtypes = [vp, sz, vp, vp]
+    L.viper_hip_stream_read.argtypes = [vp, sz, i32, i32, vp, vp, vp]
     L.viper_hip_stream_read.restype = i32
     L.viper_hip_qlinear_fused2.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     L.viper_hip_qlinear_fused2.restype = i32
