@@ -6,17 +6,18 @@ weight copy.  Weights rotate over >= 512 MB of distinct copies so the 256 MB
 MALL cannot serve them; x, y and the copies are resident in HBM before the
 timed region.
 
-The K timed steps are replayed from a HIP graph (one captured launch per
-weight copy) so the host never throttles the stream; HIP events on that stream
-bracket the timed region.  value = algorithmic bytes * K / elapsed, and the
-roofline's achieved bandwidth uses the same average launch duration
-(elapsed / K), which rocprofv3's per-dispatch kernel durations agree with for
-back-to-back dispatches (profiles/).  Events attached to a single isolated
-dispatch include ~2.5 us of event overhead on this platform and are not used.
-The CPU baseline is the oracle's C restatement of the same GEMV (same
-semantics, seeded inputs), timed on this host with 1 and all threads.
+The K timed steps (at least 200, after at least 20 eager warm-ups) are one
+HIP graph of K launches cycling over the weight copies, replayed once untimed
+and once timed, so the host never throttles the stream and no graph-launch
+boundary falls inside the timed launches; HIP events on that stream bracket
+the timed region.  value = algorithmic bytes * K / elapsed, and the roofline's
+achieved bandwidth uses the same average launch duration (elapsed / K).  Every
+other line is timed the same way (one graph of >= 200 calls).  The CPU
+baseline is the oracle's C restatement of the same GEMV (same semantics,
+seeded inputs), timed on this host with 1 and all threads.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+       python bench.py --read-sweep | --timeline | --only LINE   (measurement modes)
 """
 import argparse
 import ctypes as C
@@ -82,9 +83,8 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False):
             raise RuntimeError(f"qlinear qtype={qtype} N={N} K={K} M={M} failed: {rc}")
     for i in range(20):
         launch(i)
-    g, r = capture(torch, launch, copies, steps)
-    us = time_graph(torch, g, r) * 1e3 / (r * copies)
-    del g, W, S
+    us = time_steps(torch, launch, max(steps, MIN_STEPS))
+    del W, S
     alg = algorithmic_bytes(rb, N, K, M, G)
     return round(us, 3), round(alg / (us * 1e-6) / 1e9, 1)
 
@@ -101,16 +101,13 @@ def capture_n(torch, launch, n):
     return graph
 
 
-def capture(torch, launch, copies, steps):
-    """One HIP graph holding one launch per weight copy; replays to cover steps."""
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(copies):
-            launch(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    return graph, max(1, steps // copies)
+def time_steps(torch, launch, n):
+    """us per call of launch(i) over one HIP graph of n calls (i = 0..n-1, cycling the weight copies),
+    replayed once untimed and once timed."""
+    g = capture_n(torch, launch, n)
+    us = time_graph(torch, g, 1) * 1e3 / n
+    del g
+    return us
 
 
 def time_graph(torch, graph, replays):
@@ -375,11 +372,9 @@ def main():
                 raise RuntimeError(f"viper_hip_stream_read failed: {rc}")
         for i in range(20):
             launch_read(i)
-        gr, rr = capture(torch, launch_read, copies, args.steps)
-        read_us = time_graph(torch, gr, rr) * 1e3 / (rr * copies)
+        read_us = time_steps(torch, launch_read, max(args.steps, MIN_STEPS))
         extras["stream_read_weights_us"] = round(read_us, 3)
         extras["stream_read_weights_gbs"] = round(wbytes / (read_us * 1e-6) / 1e9, 1)
-        del gr
 
         # M=16 speculative verify (K=2560, N=10240): quantize kernel + GEMM
         M16 = 16
@@ -396,12 +391,10 @@ def main():
                 raise RuntimeError(f"M=16 qlinear failed: {rc}")
         for i in range(50):
             launch16(i)
-        g16, r16 = capture(torch, launch16, copies, 400)
-        m16_us = time_graph(torch, g16, r16) * 1e3 / (r16 * copies)
+        m16_us = time_steps(torch, launch16, 400)
         alg16 = algorithmic_bytes(K // 2, N, K, M16)
         extras["m16_verify_us"] = round(m16_us, 3)
         extras["m16_verify_gbs"] = round(alg16 / (m16_us * 1e-6) / 1e9, 1)
-        del g16
 
         # config 2: the other speculative-verify row counts at the north-star shape, and M=16 at the
         # down-projection shape
@@ -438,12 +431,11 @@ def main():
                 raise RuntimeError(f"down qlinear failed: {rc}")
         for i in range(50):
             launchd(i)
-        gd, rd = capture(torch, launchd, copies, 400)
-        d_us = time_graph(torch, gd, rd) * 1e3 / (rd * copies)
+        d_us = time_steps(torch, launchd, 400)
         algd = algorithmic_bytes(Kd // 2, Nd, Kd, 1)
         extras["down_k10240_n2560_us"] = round(d_us, 3)
         extras["down_k10240_n2560_gbs"] = round(algd / (d_us * 1e-6) / 1e9, 1)
-        del gd, Wd, Sd
+        del Wd, Sd
 
         # config 1: gate+up (one fused2 launch, K=2560, N=2x10240) -> swiglu +
         # quantize -> down (K=10240, N=2560) + residual; one step = 3 launches
@@ -476,14 +468,12 @@ def main():
                 raise RuntimeError(f"MLP step failed: {rc}")
         for i in range(20):
             launch_mlp(i)
-        gm1, rm1 = capture(torch, launch_mlp, mcopies, 200)
-        mlp_us = time_graph(torch, gm1, rm1) * 1e3 / (rm1 * mcopies)
+        mlp_us = time_steps(torch, launch_mlp, 200)
         # weights + scales of the three matrices, x and the residual in, gate/up
         # out and back in, int8 activation + scales out and back in, y out
         mlp_bytes = (step_bytes + H * 2 * 2 + 2 * I * 2 * 2 + (I + I // G * 4) * 2 + H * 2)
         extras["mlp_config1_us"] = round(mlp_us, 3)
         extras["mlp_config1_gbs"] = round(mlp_bytes / (mlp_us * 1e-6) / 1e9, 1)
-        del gm1
 
         # the same MLP in 2 launches: gate/up pair with the swiglu epilogue (h bf16), then
         # down + residual quantizing h in its prologue
@@ -499,13 +489,12 @@ def main():
                 raise RuntimeError(f"MLP (2 launches) failed: {rc}")
         for i in range(20):
             launch_mlp2(i)
-        gm2, rm2 = capture(torch, launch_mlp2, mcopies, 200)
-        mlp2_us = time_graph(torch, gm2, rm2) * 1e3 / (rm2 * mcopies)
+        mlp2_us = time_steps(torch, launch_mlp2, 200)
         # weights + scales, x and the residual in, h out and back in, y out
         mlp2_bytes = step_bytes + H * 2 * 2 + I * 2 * 2 + H * 2
         extras["mlp_config1_2launch_us"] = round(mlp2_us, 3)
         extras["mlp_config1_2launch_gbs"] = round(mlp2_bytes / (mlp2_us * 1e-6) / 1e9, 1)
-        del gm2, Wg, Sg, Wu, Su, Wdn, Sdn
+        del Wg, Sg, Wu, Su, Wdn, Sdn
 
         # LM head (config 3's head): bf16 GEMV K=2560, N=166144 (850 MB, larger
         # than the MALL, so one copy streams from HBM every call) + greedy argmax
@@ -529,15 +518,13 @@ def main():
         for i in range(5):
             launch_head(i)
             launch_greedy(i)
-        gh, rh = capture(torch, launch_head, 10, 50)
-        head_us = time_graph(torch, gh, rh) * 1e3 / (rh * 10)
-        gg, rg = capture(torch, launch_greedy, 10, 200)
-        greedy_us = time_graph(torch, gg, rg) * 1e3 / (rg * 10)
+        head_us = time_steps(torch, launch_head, 50)
+        greedy_us = time_steps(torch, launch_greedy, 200)
         head_bytes = Nv * K * 2 + K * 2 + Nv * 2
         extras["lm_head_us"] = round(head_us, 3)
         extras["lm_head_gbs"] = round(head_bytes / (head_us * 1e-6) / 1e9, 1)
         extras["greedy_argmax_us"] = round(greedy_us, 3)
-        del gh, gg, Wh
+        del Wh
 
         # config 3: 22 weight sets x 2 passes (44 slots) of the linear path +
         # final norm + bf16 LM head + greedy token, one step = one graph replay

@@ -48,6 +48,8 @@
  *                                   the exact per-group int32 dots for parity tests.
  *   viper_hip_qlinear_timeline      no counterpart: the M = 1 GEMV with per-wave
  *                                   timestamps (measurement).
+ *   viper_hip_check_bf16_rounding   no counterpart: device self-check of the
+ *                                   bf16 output rounding.
  *   viper_hip_check_quantizer       no counterpart: device self-check of the
  *                                   activation quantizer's rounding.
  *   viper_hip_stream_read           no counterpart: reads a buffer once with the
@@ -235,6 +237,13 @@ int viper_hip_qlinear_partials(int qtype, const void* w_packed, const void* w_sc
                                int scale_enc, int group, int N, int K, const void* x_bf16, int M,
                                void* y_bf16, const void* residual_bf16, void* workspace,
                                size_t workspace_bytes, int32_t* partials, void* stream);
+
+/* Device self-check of the fp32 -> bf16 rounding the kernels use (test
+ * use): every fp32 bit pattern through the hardware conversion and through
+ * the round-to-nearest-even statement (NaN kept quiet with its top payload
+ * bits); adds the number of disagreements to *count (uint64, zeroed by the
+ * caller). */
+int viper_hip_check_bf16_rounding(unsigned long long* count, void* stream);
 
 /* Device self-check of the division-free quantizer step (test use): for
  * every finite bf16 pair (amax, x) with 0 <= x <= amax and amax's exponent

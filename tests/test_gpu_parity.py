@@ -76,6 +76,16 @@ def run_case(torch, qtype, N, K, M, seed, scale_enc=O.SCALE_FP16, residual=False
     return host(yd, np.uint16)
 
 
+def test_device_bf16_rounding_exhaustive(torch_dev):
+    # the kernels' fp32 -> bf16 conversion (hardware) equals round-to-nearest-
+    # even with quiet NaNs (the oracle's f32_to_bf16) on all 2^32 inputs
+    torch = torch_dev
+    cnt = torch.zeros(1, dtype=torch.int64, device="cuda")
+    assert va.lib().viper_hip_check_bf16_rounding(cnt.data_ptr(), torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    assert int(cnt[0]) == 0
+
+
 def test_device_quantizer_exhaustive(torch_dev):
     torch = torch_dev
     counts = torch.full((255 * 128,), -1, dtype=torch.int32, device="cuda")

@@ -49,10 +49,7 @@ __device__ __forceinline__ void unpack8(const u32x4& v, float* f) {
 }
 
 __device__ __forceinline__ u32x4 pack8(const float* f) {
-    return u32x4{(uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16),
-                 (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16),
-                 (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16),
-                 (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16)};
+    return u32x4{f2bf2(f[0], f[1]), f2bf2(f[2], f[3]), f2bf2(f[4], f[5]), f2bf2(f[6], f[7])};
 }
 
 // Quantize the bf16 octet v (octet o of a row of K elements) into xq/xs; all

@@ -413,7 +413,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
                 f0 = silu_mul(f0, g0);
                 f1 = silu_mul(f1, g1);
             }
-            o[j] = (uint32_t)f2bf(f0) | ((uint32_t)f2bf(f1) << 16);
+            o[j] = f2bf2(f0, f1);
         }
         return u32x4{o[0], o[1], o[2], o[3]};
     };

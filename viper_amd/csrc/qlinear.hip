@@ -20,11 +20,12 @@
 // caller, and every weight byte is read once for all M rows.
 //
 // The activation quantizer never divides per element: with s the group scale
-// and r = 1/s (both IEEE divides, once per group), q0 = x*r and
-// q1 = fma(fma(-q0, s, x), r, q0); adding 1.5*2^23 rounds q1 to the nearest
-// even integer and leaves it, two's complement, in the low byte.  For every
-// finite bf16 pair (amax, x) the byte equals RNE(x/s); check_quantizer_kernel
-// and the CPU oracle verify that exhaustively.
+// (an IEEE divide amax/127, once per group) and r = rcp(s) (the hardware
+// reciprocal, within 1 ulp), q0 = x*r and q1 = fma(fma(-q0, s, x), r, q0);
+// adding 1.5*2^23 rounds q1 to the nearest even integer and leaves it, two's
+// complement, in the low byte.  For every finite bf16 pair (amax, x) the byte
+// equals RNE(x/s): check_quantizer_kernel verifies that exhaustively on the
+// device (and the CPU oracle the same steps with an IEEE 1/s).
 
 #include "qlinear_host.h"
 
@@ -160,6 +161,26 @@ quantize_frag64_kernel(const uint16_t* x, int M, int K, int8_t* __restrict__ xq,
     const auto sw = buf(xs, (uint32_t)(K / 64) * 64u);
     bstore16<AUX_SC1>(xw, ok ? (g * 64 + L) * 16 : OOB, o);
     bstore4<AUX_SC1>(sw, (ok && kb == 0) ? (g * 16 + m) * 4 : OOB, __float_as_uint(s));
+}
+
+// ----------------------------------------------- bf16 rounding self-check
+
+// Every fp32 bit pattern through the kernels' conversion (f2bf2, the
+// hardware v_cvt_pk_bf16_f32) and its arithmetic statement f2bf_sw; *count
+// receives the number of disagreements (each thread covers a contiguous
+// range of patterns, two per conversion).
+constexpr int BFC_GRID = 4096, BFC_NT = 256;
+__global__ void __launch_bounds__(BFC_NT) check_bf16_kernel(unsigned long long* __restrict__ count) {
+    constexpr unsigned long long per = (1ull << 32) / ((unsigned long long)BFC_GRID * BFC_NT);
+    const unsigned long long base = ((unsigned long long)blockIdx.x * BFC_NT + threadIdx.x) * per;
+    unsigned bad = 0;
+    for (unsigned long long k = 0; k < per; k += 2) {
+        const float a = __uint_as_float((uint32_t)(base + k)), b = __uint_as_float((uint32_t)(base + k + 1));
+        const uint32_t hw = f2bf2(a, b);
+        bad += (hw & 0xffffu) != f2bf_sw(a);
+        bad += (hw >> 16) != f2bf_sw(b);
+    }
+    if (bad) atomicAdd(count, (unsigned long long)bad);
 }
 
 // --------------------------------------------------- quantizer self-check
@@ -489,6 +510,13 @@ extern "C" int viper_hip_qlinear_timeline(int qtype, const void* w_packed, const
         return VIPER_INVALID_ARGUMENT;
     return vq::launch_m1_timeline(qtype, scale_enc, K, x_bf16, w_packed, w_scales, y_bf16, N, stamps, stamp_bytes,
                                   workgroups, waves_per_workgroup, (hipStream_t)stream);
+}
+
+extern "C" int viper_hip_check_bf16_rounding(unsigned long long* count, void* stream) {
+    if (count == nullptr || vq::misaligned(count, 8)) return VIPER_INVALID_ARGUMENT;
+    void* args[] = {&count};
+    vq::launch((const void*)vq::check_bf16_kernel, vq::BFC_GRID, vq::BFC_NT, 0, (hipStream_t)stream, args);
+    return vq::status_of(hipGetLastError());
 }
 
 extern "C" int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream) {

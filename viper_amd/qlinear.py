@@ -131,6 +131,7 @@ _SYMBOLS = (
     "viper_hip_qlinear_m1_swiglu",
     "viper_hip_qlinear_static",
     "viper_hip_qlinear_timeline",
+    "viper_hip_check_bf16_rounding",
 )
 
 
@@ -161,6 +162,8 @@ def lib():
     L.viper_hip_qlinear_static.restype = i32
     L.viper_hip_qlinear_timeline.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, vp, vp, sz, vp, vp, vp]
     L.viper_hip_qlinear_timeline.restype = i32
+    L.viper_hip_check_bf16_rounding.argtypes = [vp, vp]
+    L.viper_hip_check_bf16_rounding.restype = i32
     L.viper_hip_check_quantizer.argtypes = [i32, i32, vp, vp]
     L.viper_hip_check_quantizer.restype = i32
     L.viper_hip_stream_read.argtypes = [vp, sz, i32, i32, vp, vp, vp]
