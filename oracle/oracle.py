@@ -62,7 +62,7 @@ def lib():
         L.vo_qlinear_prequant.restype = i32
         L.vo_qlinear.argtypes = [i32, vp, vp, i32, i32, i32, vp, i32, vp, vp, vp, vp]
         L.vo_qlinear.restype = i32
-        L.vo_qlinear_omp.argtypes = [i32, vp, vp, i32, i32, i32, vp, i32, vp, vp, i32]
+        L.vo_qlinear_omp.argtypes = [i32, vp, vp, i32, i32, i32, vp, i32, vp, vp, vp, vp, i32]
         L.vo_qlinear_omp.restype = i32
         L.vo_omp_max_threads.argtypes, L.vo_omp_max_threads.restype = [], i32
         L.vo_check_markstein.argtypes = [i32, i32, C.POINTER(C.c_int64)]
@@ -236,13 +236,18 @@ def qlinear_prequant(qtype, packed, scales, scale_enc, N, K, xq, xs, residual=No
     return y, yf, ya
 
 
-def qlinear_omp(qtype, packed, scales, scale_enc, N, K, x_bf16, nthreads=0):
+def qlinear_omp(qtype, packed, scales, scale_enc, N, K, x_bf16, nthreads=0, residual=None, full=False):
+    """qlinear over OpenMP threads: y_bf16, or (y_bf16, y_f32, absterm) with full=True."""
     x_bf16 = np.ascontiguousarray(x_bf16, dtype=np.uint16)
     M = x_bf16.shape[0]
     y = np.zeros((M, N), dtype=np.uint16)
+    yf = np.zeros((M, N), dtype=np.float32) if full else None
+    ya = np.zeros((M, N), dtype=np.float64) if full else None
+    res = None if residual is None else np.ascontiguousarray(residual, dtype=np.uint16)
     _check(lib().vo_qlinear_omp(qtype, _p(np.ascontiguousarray(packed)), _p(np.ascontiguousarray(scales)),
-                                scale_enc, N, K, _p(x_bf16), M, None, _p(y), nthreads), "qlinear_omp")
-    return y
+                                scale_enc, N, K, _p(x_bf16), M, _p(res), _p(y), _p(yf), _p(ya), nthreads),
+           "qlinear_omp")
+    return (y, yf, ya) if full else y
 
 
 def omp_max_threads():

@@ -548,7 +548,7 @@ int vo_omp_max_threads(void) {
 
 int vo_qlinear_omp(int qtype, const uint8_t* packed, const uint16_t* scales, int scale_enc,
                    int N, int K, const uint16_t* x, int M, const uint16_t* residual, uint16_t* y,
-                   int nthreads) {
+                   float* y_f32, double* y_absterm, int nthreads) {
     if (!shape_ok(qtype, N, K) || M <= 0) return -1;
     const int G = vo_group_size(qtype);
     int8_t* xq = (int8_t*)malloc((size_t)M * K);
@@ -565,8 +565,8 @@ int vo_qlinear_omp(int qtype, const uint8_t* packed, const uint16_t* scales, int
 #endif
     for (int n = 0; n < N; ++n)
         for (int m = 0; m < M; ++m)
-            linear_row(qtype, packed, scales, scale_enc, N, K, xq, xs, m, n, residual, y, NULL,
-                       NULL);
+            linear_row(qtype, packed, scales, scale_enc, N, K, xq, xs, m, n, residual, y, y_f32,
+                       y_absterm);
     (void)nthreads;
     free(xq);
     free(xs);

@@ -137,10 +137,11 @@ int vo_qlinear_prequant(int qtype, const uint8_t* packed, const uint16_t* scales
 int vo_qlinear(int qtype, const uint8_t* packed, const uint16_t* scales, int scale_enc,
                int N, int K, const uint16_t* x, int M, const uint16_t* residual,
                uint16_t* y, float* y_f32, double* y_absterm);
-/* Same arithmetic, output rows split over OpenMP threads (CPU baseline). */
+/* Same arithmetic and outputs as vo_qlinear, output rows split over OpenMP
+ * threads (the CPU baseline, and the oracle for production-size checks). */
 int vo_qlinear_omp(int qtype, const uint8_t* packed, const uint16_t* scales, int scale_enc,
                    int N, int K, const uint16_t* x, int M, const uint16_t* residual,
-                   uint16_t* y, int nthreads);
+                   uint16_t* y, float* y_f32, double* y_absterm, int nthreads);
 int vo_omp_max_threads(void);
 
 /* ---- the division-free identity used by the GPU quantizer ----

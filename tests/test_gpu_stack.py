@@ -70,3 +70,82 @@ def test_stack_step_wiring_and_determinism(torch_dev, fused):
     if top[1] - top[0] > 0.1 * scale:
         assert token == int(np.argmax(rf))
     assert token == int(O.argmax_bf16(logits)[0])
+
+
+def _close_bits(hd, hr, what):
+    """Within 1 bf16 ulp (1 in the bit pattern) outside the flush-to-zero range."""
+    tiny = 2.0 ** -100
+    small = np.abs(O.bf16_to_f32(hr)) < tiny
+    assert (np.abs(O.bf16_to_f32(hd))[small] < tiny).all(), what
+    d = np.abs(hd.astype(np.int32) - hr.astype(np.int32))[~small]
+    assert int(d.max(initial=0)) <= 1, f"{what}: {int(d.max())} bf16 steps"
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_stack_production_size_every_launch(torch_dev, fused):
+    """The config-3 step at its real size (hidden 2560, intermediate 10240,
+    20/4 heads of 128, 22 layers looped twice, vocab 166144), every launch of
+    all 44 slots checked against the oracle on the GPU's own inputs (teacher
+    forcing, so each launch is held to the single-kernel bar: GEMV outputs
+    within 1 bf16 ulp or 1e-5 of the sum of |terms|, rmsnorm and swiglu rows
+    within 1 ulp), then the LM head and the greedy token; finally the same
+    step untraced must give the traced run's logits bit for bit."""
+    torch = torch_dev
+    from viper_amd.stack import Stack
+    s = Stack(torch)
+    print(f"stack production size fused={fused}", flush=True)
+    H, I, nQ, nKV = s.H, s.I, s.nQ, s.nKV
+    W = [[(pk.cpu().numpy(), sc.view(torch.int16).cpu().numpy().view(np.uint16), n, k) for (pk, sc, n, k) in lw]
+         for lw in s.w]
+    ln = [u16(t) for t in s.ln]
+    attn = u16(s.attn)
+    Q4, F16 = O.Q4_G64, O.SCALE_FP16
+
+    def gemv(w, x, residual=None):
+        return O.qlinear_omp(Q4, w[0], w[1], F16, w[2], w[3], x, residual=residual, full=True)
+
+    s.trace = True
+    s.x.copy_(s.x0)
+    for slot in range(s.layers * s.passes):
+        l = slot % s.layers
+        wq, wk, wv, wo, wg, wu, wd = W[l]
+        x_in = u16(s.x)
+        s.attention_half(slot, fused)
+        torch.cuda.synchronize()
+        xn = u16(s.xn)
+        _close_bits(xn[0], O.rmsnorm_bf16(x_in, ln[2 * l], s.eps)[0], f"slot {slot} input rmsnorm")
+        for w, out, name in ((wq, s.q, "q"), (wk, s.k, "k"), (wv, s.v, "v")):
+            y, _, a = gemv(w, xn)
+            O.assert_bf16_close(u16(out), y, a, rel=1e-5, what=f"slot {slot} {name}")
+        x_mid = u16(s.x)
+        y, _, a = gemv(wo, attn, residual=x_in)
+        O.assert_bf16_close(x_mid, y, a, rel=1e-5, what=f"slot {slot} o + residual")
+
+        s.mlp_half(slot, fused)
+        torch.cuda.synchronize()
+        xn = u16(s.xn)
+        _close_bits(xn[0], O.rmsnorm_bf16(x_mid, ln[2 * l + 1], s.eps)[0], f"slot {slot} post rmsnorm")
+        g, u, h = u16(s.g), u16(s.ut), u16(s.gt)
+        for w, out, name in ((wg, g, "gate"), (wu, u, "up")):
+            y, _, a = gemv(w, xn)
+            O.assert_bf16_close(out, y, a, rel=1e-5, what=f"slot {slot} {name}")
+        _close_bits(h[0], O.swiglu_bf16(g, u)[0], f"slot {slot} swiglu")
+        y, _, a = gemv(wd, h, residual=x_mid)
+        O.assert_bf16_close(u16(s.x), y, a, rel=1e-5, what=f"slot {slot} down + residual")
+
+    x_fin = u16(s.x)
+    s.head_step()
+    torch.cuda.synchronize()
+    xn = u16(s.xn)
+    _close_bits(xn[0], O.rmsnorm_bf16(x_fin, u16(s.final_ln), s.eps)[0], "final rmsnorm")
+    logits = u16(s.logits)
+    y, _, a = O.linear_bf16(u16(s.head), xn)
+    O.assert_bf16_close(logits, y, a, rel=1e-5, what="lm_head")
+    token = int(s.token.item())
+    assert token == int(O.argmax_bf16(logits)[0])
+
+    s.trace = False
+    (s.step_fused if fused else s.step)()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(s.logits), logits)
+    assert int(s.token.item()) == token

@@ -72,6 +72,11 @@ class Stack:
         self.xs = torch.empty((kmax // 64,), dtype=torch.float32, device="cuda")
         self.logits = torch.empty((1, vocab), dtype=bf, device="cuda")
         self.token = torch.empty((1,), dtype=torch.int32, device="cuda")
+        # trace: every launch also leaves its intermediates readable (the
+        # normalized rows in xn, gate in g, up in ut, h in gt) through the same
+        # kernels' optional outputs, so a test can check each launch in turn
+        self.trace = False
+        self.g = torch.empty((1, I), dtype=bf, device="cuda")
         L = _q.lib()
         self.L = L
 
@@ -83,10 +88,13 @@ class Stack:
         if rc != 0:
             raise RuntimeError(f"{what} failed: {rc}")
 
+    def _norm_out(self, pro):
+        return self.xn.data_ptr() if self.trace and pro == 2 else None
+
     def _m1(self, pro, a, b, outs, eps=0.0, residual=None, st=None):
         n = len(outs)
         vp = C.c_void_p * n
-        rc = self.L.viper_hip_qlinear_m1(Q4, 0, 64, outs[0][0][3], pro, a, b, eps, None, n,
+        rc = self.L.viper_hip_qlinear_m1(Q4, 0, 64, outs[0][0][3], pro, a, b, eps, self._norm_out(pro), n,
                                          vp(*[o[0][0].data_ptr() for o in outs]),
                                          vp(*[o[0][1].data_ptr() for o in outs]),
                                          (C.c_int * n)(*[o[0][2] for o in outs]),
@@ -94,62 +102,79 @@ class Stack:
         self._ok(rc, "qlinear_m1")
 
     def _m1_swiglu(self, pro, a, b, wg, wu, h, eps=0.0, st=None):
-        rc = self.L.viper_hip_qlinear_m1_swiglu(Q4, 0, 64, wg[3], pro, a, b, eps, None, wg[0].data_ptr(),
-                                                wg[1].data_ptr(), wu[0].data_ptr(), wu[1].data_ptr(), wg[2],
-                                                h.data_ptr(), None, None, st)
+        gu = (self.g.data_ptr(), self.ut.data_ptr()) if self.trace else (None, None)
+        rc = self.L.viper_hip_qlinear_m1_swiglu(Q4, 0, 64, wg[3], pro, a, b, eps, self._norm_out(pro),
+                                                wg[0].data_ptr(), wg[1].data_ptr(), wu[0].data_ptr(),
+                                                wu[1].data_ptr(), wg[2], h.data_ptr(), gu[0], gu[1], st)
         self._ok(rc, "qlinear_m1_swiglu")
 
-    def step_fused(self):
-        """One decode step, 4 launches per slot (producers folded, q/k/v together)."""
-        torch, L = self.torch, self.L
-        st = torch.cuda.current_stream().cuda_stream
+    def attention_half(self, l, fused=True):
+        """Slot l's q/k/v projections from rmsnorm(x) and the o projection of
+        the fixed attention output added into x."""
+        L, st = self.L, self.torch.cuda.current_stream().cuda_stream
+        H, nQ, nKV = self.H, self.nQ, self.nKV
+        p = lambda t: t.data_ptr()
+        x = self.x
+        wq, wk, wv, wo = self.w[l % self.layers][:4]
+        ln = self.ln[2 * (l % self.layers)]
+        if fused:
+            self._m1(2, p(x), p(ln), [(wq, self.q), (wk, self.k), (wv, self.v)], eps=self.eps, st=st)
+            self._m1(0, p(self.attn), None, [(wo, x)], residual=p(x), st=st)
+            return
+        self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
+                                              p(self.xs), st), "rmsnorm_quantize")
+        self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wq[0]), p(wq[1]), 0, 64, nQ, H, p(self.xq), p(self.xs), 1,
+                                                  p(self.q), None, st), "q")
+        self._ok(L.viper_hip_qlinear_fused2_prequantized(Q4, p(wk[0]), p(wk[1]), p(wv[0]), p(wv[1]), 0, 64, nKV, H,
+                                                         p(self.xq), p(self.xs), 1, p(self.k), p(self.v), st), "kv")
+        self._ok(L.viper_hip_quantize_act(64, p(self.attn), 1, nQ, p(self.xq), p(self.xs), st), "quantize")
+        self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wo[0]), p(wo[1]), 0, 64, H, nQ, p(self.xq), p(self.xs), 1,
+                                                  p(x), p(x), st), "o")
+
+    def mlp_half(self, l, fused=True):
+        """Slot l's gate/up projections from rmsnorm(x), h = silu(gate) * up
+        (left in self.gt), and the down projection of h added into x."""
+        L, st = self.L, self.torch.cuda.current_stream().cuda_stream
         H, I = self.H, self.I
         p = lambda t: t.data_ptr()
         x = self.x
-        x.copy_(self.x0)
-        for loop in range(self.passes):
-            for l in range(self.layers):
-                wq, wk, wv, wo, wg, wu, wd = self.w[l]
-                self._m1(2, p(x), p(self.ln[2 * l]), [(wq, self.q), (wk, self.k), (wv, self.v)], eps=self.eps, st=st)
-                self._m1(0, p(self.attn), None, [(wo, x)], residual=p(x), st=st)
-                self._m1_swiglu(2, p(x), p(self.ln[2 * l + 1]), wg, wu, self.gt, eps=self.eps, st=st)
-                self._m1(0, p(self.gt), None, [(wd, x)], residual=p(x), st=st)
-        self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(self.final_ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
-                                              p(self.xs), st), "final norm")
-        self._ok(L.viper_hip_linear_bf16(p(self.head), p(self.xn), p(self.logits), 1, self.V, H, st), "lm_head")
+        wg, wu, wd = self.w[l % self.layers][4:]
+        ln = self.ln[2 * (l % self.layers) + 1]
+        if fused:
+            self._m1_swiglu(2, p(x), p(ln), wg, wu, self.gt, eps=self.eps, st=st)
+            self._m1(0, p(self.gt), None, [(wd, x)], residual=p(x), st=st)
+            return
+        self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
+                                              p(self.xs), st), "rmsnorm_quantize")
+        g = self.g if self.trace else self.gt   # the engine writes h over gate
+        self._ok(L.viper_hip_qlinear_fused2_prequantized(Q4, p(wg[0]), p(wg[1]), p(wu[0]), p(wu[1]), 0, 64, I, H,
+                                                         p(self.xq), p(self.xs), 1, p(g), p(self.ut), st),
+                 "gate_up")
+        self._ok(L.viper_hip_swiglu_quantize(p(g), p(self.ut), 1, I, 64, p(self.gt), p(self.xq), p(self.xs), st),
+                 "swiglu_quantize")
+        self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wd[0]), p(wd[1]), 0, 64, H, I, p(self.xq), p(self.xs), 1,
+                                                  p(x), p(x), st), "down")
+
+    def head_step(self):
+        """Final rmsnorm of x (into self.xn), the bf16 LM head and the greedy token."""
+        L, st = self.L, self.torch.cuda.current_stream().cuda_stream
+        p = lambda t: t.data_ptr()
+        self._ok(L.viper_hip_rmsnorm_quantize(p(self.x), p(self.final_ln), self.eps, 1, self.H, 64, p(self.xn),
+                                              p(self.xq), p(self.xs), st), "final norm")
+        self._ok(L.viper_hip_linear_bf16(p(self.head), p(self.xn), p(self.logits), 1, self.V, self.H, st), "lm_head")
         self._ok(L.viper_hip_sampling_greedy(p(self.logits), p(self.token), 1, self.V, st), "greedy")
+
+    def _step(self, fused):
+        self.x.copy_(self.x0)
+        for l in range(self.layers * self.passes):
+            self.attention_half(l, fused)
+            self.mlp_half(l, fused)
+        self.head_step()
+
+    def step_fused(self):
+        """One decode step, 4 launches per slot (producers folded, q/k/v together)."""
+        self._step(True)
 
     def step(self):
         """One decode step of the linear path, reference launch sequence."""
-        torch, L = self.torch, self.L
-        st = torch.cuda.current_stream().cuda_stream
-        H, I, nQ, nKV = self.H, self.I, self.nQ, self.nKV
-        p = lambda t: t.data_ptr()
-        x = self.x
-        x.copy_(self.x0)
-        for loop in range(self.passes):
-            for l in range(self.layers):
-                wq, wk, wv, wo, wg, wu, wd = self.w[l]
-                self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(self.ln[2 * l]), self.eps, 1, H, 64, p(self.xn),
-                                                      p(self.xq), p(self.xs), st), "rmsnorm_quantize")
-                self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wq[0]), p(wq[1]), 0, 64, nQ, H, p(self.xq),
-                                                          p(self.xs), 1, p(self.q), None, st), "q")
-                self._ok(L.viper_hip_qlinear_fused2_prequantized(Q4, p(wk[0]), p(wk[1]), p(wv[0]), p(wv[1]), 0, 64,
-                                                                 nKV, H, p(self.xq), p(self.xs), 1, p(self.k),
-                                                                 p(self.v), st), "kv")
-                self._ok(L.viper_hip_quantize_act(64, p(self.attn), 1, nQ, p(self.xq), p(self.xs), st), "quantize")
-                self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wo[0]), p(wo[1]), 0, 64, H, nQ, p(self.xq),
-                                                          p(self.xs), 1, p(x), p(x), st), "o")
-                self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(self.ln[2 * l + 1]), self.eps, 1, H, 64, p(self.xn),
-                                                      p(self.xq), p(self.xs), st), "rmsnorm_quantize")
-                self._ok(L.viper_hip_qlinear_fused2_prequantized(Q4, p(wg[0]), p(wg[1]), p(wu[0]), p(wu[1]), 0, 64,
-                                                                 I, H, p(self.xq), p(self.xs), 1, p(self.gt),
-                                                                 p(self.ut), st), "gate_up")
-                self._ok(L.viper_hip_swiglu_quantize(p(self.gt), p(self.ut), 1, I, 64, p(self.gt), p(self.xq),
-                                                     p(self.xs), st), "swiglu_quantize")
-                self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wd[0]), p(wd[1]), 0, 64, H, I, p(self.xq),
-                                                          p(self.xs), 1, p(x), p(x), st), "down")
-        self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(self.final_ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
-                                              p(self.xs), st), "final norm")
-        self._ok(L.viper_hip_linear_bf16(p(self.head), p(self.xn), p(self.logits), 1, self.V, H, st), "lm_head")
-        self._ok(L.viper_hip_sampling_greedy(p(self.logits), p(self.token), 1, self.V, st), "greedy")
+        self._step(False)
