@@ -153,10 +153,12 @@ SWEEP_SHAPES = [(64, 16), (128, 10), (256, 5), (256, 10), (320, 5), (320, 10), (
 SWEEP_MB = [13.1072, 28, 56, 112, 557]
 
 
-def _time_probe(torch, L, pool, nbytes, threads, loads, y=None, launches=200):
+def _time_probe(torch, L, pool, nbytes, threads, loads, y=None, launches=200, side_bytes=0):
     """us per dispatch of viper_hip_stream_read over rotating slices of pool (>= 512 MB of distinct
-    data, or >= 2 slices for large sizes)."""
-    stride = (nbytes + 65535) // 65536 * 65536
+    data, or >= 2 slices for large sizes); with side_bytes, every workgroup also reads its own block of
+    that many bytes, placed after the slice's nbytes."""
+    wgs = nbytes // (threads * loads * 16)
+    stride = (nbytes + wgs * side_bytes + 65535) // 65536 * 65536
     copies = max(2, min(40, pool.numel() // stride))
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
     base = pool.data_ptr()
@@ -164,7 +166,9 @@ def _time_probe(torch, L, pool, nbytes, threads, loads, y=None, launches=200):
 
     def launch(i):
         st = torch.cuda.current_stream().cuda_stream   # the capture stream while a graph is captured
-        rc = L.viper_hip_stream_read(base + (i % copies) * stride, nbytes, threads, loads, yp, sink.data_ptr(), st)
+        a = base + (i % copies) * stride
+        rc = L.viper_hip_stream_read(a, nbytes, threads, loads, a + nbytes if side_bytes else None, side_bytes, yp,
+                                     sink.data_ptr(), st)
         if rc != 0:
             raise RuntimeError(f"stream_read {threads}x{loads} {nbytes} failed: {rc}")
     n = max(launches, 2 * copies)
@@ -202,13 +206,15 @@ def read_sweep(torch, L, gen):
             best13 = ((threads, loads), pts[0][1], pts[0][0])
     print(json.dumps({"probe": "best_13MB_shape", "threads": best13[0][0], "loads_per_lane": best13[0][1],
                       "bytes": best13[2], "us": round(best13[1], 3)}), flush=True)
-    # the north-star GEMV's I/O at its own launch shape (320 threads, 5 loads per lane): weights only,
-    # weights + scales (13,952,000 bytes = 545 workgroups), and the same with one bf16 store per row
-    y = torch.empty(545 * 20, dtype=torch.int16, device="cuda")
+    # the north-star GEMV's I/O at its own launch shape (320 threads, 5 loads per lane, 512 workgroups of
+    # 20 rows): the weights; the weights and each workgroup's 1600-byte block of scales (13,926,400 bytes,
+    # as the GEMV reads them); the same with one bf16 store per row
+    y = torch.empty(512 * 20, dtype=torch.int16, device="cuda")
     ladder = {"probe": "north_star_io_ladder"}
     ladder["read_13107200_us"] = round(_time_probe(torch, L, pool, 13107200, 320, 5), 3)
-    ladder["read_13952000_us"] = round(_time_probe(torch, L, pool, 13952000, 320, 5), 3)
-    ladder["read_13952000_store_rows_us"] = round(_time_probe(torch, L, pool, 13952000, 320, 5, y=y), 3)
+    ladder["read_weights_scale_blocks_us"] = round(_time_probe(torch, L, pool, 13107200, 320, 5, side_bytes=1600), 3)
+    ladder["read_weights_scale_blocks_store_rows_us"] = round(
+        _time_probe(torch, L, pool, 13107200, 320, 5, y=y, side_bytes=1600), 3)
     print(json.dumps(ladder), flush=True)
     del pool
 
@@ -254,6 +260,26 @@ def timeline(torch, L, gen, N, K):
                       "percentiles_us_p10_p50_p90_max": rows}), flush=True)
 
 
+def time_config3(torch, stk, fused, replays=10):
+    """us per config-3 decode step (one graph of the whole step, replayed), its weight + head GB/s,
+    and the launches per step."""
+    run = stk.step_fused if fused else stk.step
+    run()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    g.replay()
+    torch.cuda.synchronize()
+    ms = time_graph(torch, g, replays) / replays
+    del g
+    # the step's algorithmic bytes as the benchmark table counts them: weights of the 44 slots and the
+    # head, the slots' activations (4,595,712 B) and the head's x and logits (337,408 B)
+    nbytes = stk.weight_bytes_per_step() + 4_595_712 + 337_408
+    launches = (4 if fused else 9) * stk.layers * stk.passes + 3
+    return round(ms * 1e3, 1), round(nbytes / (ms * 1e-3) / 1e9, 1), launches
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -272,7 +298,8 @@ def main():
                     help="only the per-wave timeline of the north-star GEMV (viper_hip_qlinear_timeline)")
     ap.add_argument("--only", default="", metavar="LINE",
                     help="only one line (rocprofv3 runs): config0, down, verify_mM (K=2560 N=10240) or "
-                         "verify_mM_down (K=10240 N=2560), q5_m1 / q6_m8 / w8_m1 ... (config 4)")
+                         "verify_mM_down (K=10240 N=2560), q5_m1 / q6_m8 / w8_m1 ... (config 4), "
+                         "config3 (fused step) or config3_ref (reference launch sequence)")
     ap.add_argument("--verify-only", type=int, default=0, metavar="M",
                     help="only time the M-row verify (K=2560, N=10240) line (rocprofv3 runs)")
     args = ap.parse_args()
@@ -315,6 +342,10 @@ def main():
             fmt, mpart = one.split("_m")
             qt = {"q5": 5, "q6": 6, "w8": 8}[fmt]
             res = time_linear(torch, L, gen, qt, N, K, int(mpart), steps=args.steps, outliers=True)
+        elif one in ("config3", "config3_ref"):
+            from viper_amd.stack import Stack
+            us, gbs, _ = time_config3(torch, Stack(torch), one == "config3", replays=max(10, args.steps // 100))
+            res = (us, gbs)
         else:
             raise SystemExit(f"unknown --only line {one}")
         print(json.dumps({"line": one, "us": res[0], "gbs": res[1]}), flush=True)
@@ -360,21 +391,28 @@ def main():
 
     extras = {}
     if not args.no_extras:
-        # the floor of one dispatch streaming the same weight bytes: a read-only kernel with the GEMV's
-        # launch shape over the same rotating copies (viper_hip_stream_read)
+        # the floor of one dispatch streaming the same bytes: a read-only kernel with the GEMV's launch
+        # shape over the same rotating copies (viper_hip_stream_read): the weights alone, then the GEMV's
+        # whole I/O (weights, each workgroup's block of scales, one bf16 store per row)
         sink = torch.zeros(4, dtype=torch.int32, device="cuda")
         wbytes = N * K // 2
+        sblock = (N // 512) * (K // G) * 2
 
-        def launch_read(i):
-            rc = L.viper_hip_stream_read(wp[i % copies], wbytes, 320, 5, None, sink.data_ptr(),
+        def launch_read(i, io=False):
+            c = i % copies
+            rc = L.viper_hip_stream_read(wp[c], wbytes, 320, 5, spp[c] if io else None, sblock if io else 0,
+                                         y.data_ptr() if io else None, sink.data_ptr(),
                                          torch.cuda.current_stream().cuda_stream)
             if rc != 0:
                 raise RuntimeError(f"viper_hip_stream_read failed: {rc}")
         for i in range(20):
             launch_read(i)
+            launch_read(i, True)
         read_us = time_steps(torch, launch_read, max(args.steps, MIN_STEPS))
+        io_us = time_steps(torch, lambda i: launch_read(i, True), max(args.steps, MIN_STEPS))
         extras["stream_read_weights_us"] = round(read_us, 3)
         extras["stream_read_weights_gbs"] = round(wbytes / (read_us * 1e-6) / 1e9, 1)
+        extras["stream_read_gemv_io_us"] = round(io_us, 3)
 
         # M=16 speculative verify (K=2560, N=10240): quantize kernel + GEMM
         M16 = 16
@@ -510,52 +548,42 @@ def main():
             if rc != 0:
                 raise RuntimeError(f"LM head failed: {rc}")
 
-        def launch_greedy(i):
-            rc = L.viper_hip_sampling_greedy(yh.data_ptr(), th.data_ptr(), 1, Nv,
-                                             torch.cuda.current_stream().cuda_stream)
+        gws = torch.zeros(16, dtype=torch.uint8, device="cuda")
+
+        def launch_greedy(i, split=False):
+            st = torch.cuda.current_stream().cuda_stream
+            if split:
+                rc = L.viper_hip_sampling_greedy_split(yh.data_ptr(), th.data_ptr(), 1, Nv, gws.data_ptr(), 16, st)
+            else:
+                rc = L.viper_hip_sampling_greedy(yh.data_ptr(), th.data_ptr(), 1, Nv, st)
             if rc != 0:
                 raise RuntimeError(f"greedy failed: {rc}")
         for i in range(5):
             launch_head(i)
             launch_greedy(i)
+            launch_greedy(i, True)
         head_us = time_steps(torch, launch_head, 50)
         greedy_us = time_steps(torch, launch_greedy, 200)
+        greedy_split_us = time_steps(torch, lambda i: launch_greedy(i, True), 200)
         head_bytes = Nv * K * 2 + K * 2 + Nv * 2
         extras["lm_head_us"] = round(head_us, 3)
         extras["lm_head_gbs"] = round(head_bytes / (head_us * 1e-6) / 1e9, 1)
         extras["greedy_argmax_us"] = round(greedy_us, 3)
+        extras["greedy_argmax_split_us"] = round(greedy_split_us, 3)
         del Wh
 
         # config 3: 22 weight sets x 2 passes (44 slots) of the linear path +
-        # final norm + bf16 LM head + greedy token, one step = one graph replay
+        # final norm + bf16 LM head + greedy token, one step = one graph replay;
+        # the reference launch sequence, then the producers folded into the
+        # GEMVs (4 launches per slot)
         from viper_amd.stack import Stack
         stk = Stack(torch)
-        stk.step()
-        torch.cuda.synchronize()
-        g3 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g3):
-            stk.step()
-        g3.replay()
-        torch.cuda.synchronize()
-        s3_ms = time_graph(torch, g3, 10) / 10
-        s3_bytes = stk.weight_bytes_per_step() + 4_595_712 + 337_408
-        extras["config3_step_us"] = round(s3_ms * 1e3, 1)
-        extras["config3_step_gbs"] = round(s3_bytes / (s3_ms * 1e-3) / 1e9, 1)
-        extras["config3_launches_per_step"] = 9 * stk.layers * stk.passes + 3
-        del g3
-        # the same step with the producers folded into the GEMVs (4 launches per slot)
-        stk.step_fused()
-        torch.cuda.synchronize()
-        g4 = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g4):
-            stk.step_fused()
-        g4.replay()
-        torch.cuda.synchronize()
-        s4_ms = time_graph(torch, g4, 10) / 10
-        extras["config3_fused_step_us"] = round(s4_ms * 1e3, 1)
-        extras["config3_fused_step_gbs"] = round(s3_bytes / (s4_ms * 1e-3) / 1e9, 1)
-        extras["config3_fused_launches_per_step"] = 4 * stk.layers * stk.passes + 3
-        del g4, stk
+        for fused, key in ((False, "config3"), (True, "config3_fused")):
+            us, gbs, launches = time_config3(torch, stk, fused)
+            extras[f"{key}_step_us"] = us
+            extras[f"{key}_step_gbs"] = gbs
+            extras[f"{key}_launches_per_step"] = launches
+        del stk
 
     traffic = None
     tpath = os.path.join(ROOT, "profiles", "traffic_q4_m1_k2560_n10240.json")

@@ -44,6 +44,9 @@
  *                                   declared kernels/ops/linear_bf16_kernel.h): the bf16 LM
  *                                   head GEMV (src/viper/model.cpp:300-304).
  *   viper_hip_sampling_greedy       sampling_greedy_bf16 (kernels/ops/sampling_kernel.cu:66-80).
+ *   viper_hip_sampling_greedy_split the same, each row over many workgroups that meet in a
+ *                                   caller workspace (no counterpart; the reference runs one
+ *                                   block per row).
  *   viper_hip_qlinear_partials      no counterpart: the same kernels, also writing
  *                                   the exact per-group int32 dots for parity tests.
  *   viper_hip_qlinear_timeline      no counterpart: the M = 1 GEMV with per-wave
@@ -106,7 +109,7 @@ extern "C" {
 #define VIPER_SCALE_BF16 1
 
 #define VIPER_QLINEAR_MAX_M 16
-#define VIPER_QLINEAR_ABI_VERSION 3
+#define VIPER_QLINEAR_ABI_VERSION 4
 
 int viper_hip_abi_version(void);
 
@@ -216,6 +219,18 @@ int viper_hip_linear_bf16(const void* w_bf16, const void* x_bf16, void* y_bf16, 
  * never wins; a row with nothing above -inf gives 0. */
 int viper_hip_sampling_greedy(const void* logits_bf16, int32_t* out_token, int B, int V, void* stream);
 
+/* viper_hip_sampling_greedy with each row split over workgroups of 4096
+ * logits (41 for a 166144-logit row instead of one), which meet through
+ * workspace: viper_hip_sampling_greedy_workspace_bytes(B) bytes, 8-byte
+ * aligned, zero before the first call; every call leaves it zero again, so
+ * it is reused without clearing (two calls in flight on one workspace race).
+ * Same result as viper_hip_sampling_greedy; rows that are not whole 16-byte
+ * words (V % 8 != 0 or logits not 16-byte aligned) take that kernel and
+ * leave the workspace alone.  No counterpart in the reference. */
+size_t viper_hip_sampling_greedy_workspace_bytes(int B);
+int viper_hip_sampling_greedy_split(const void* logits_bf16, int32_t* out_token, int B, int V, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+
 /* viper_hip_qlinear without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference (whose
@@ -274,11 +289,15 @@ int viper_hip_qlinear_timeline(int qtype, const void* w_packed, const void* w_sc
  * `threads` threads (64, 128, 256, 320, 512, 640 or 1024) cover threads / 16
  * rows each, in the GEMV's XCD-aware order; loads is 4, 5, 8, 10 or 16, and
  * bytes a multiple of threads * loads * 16 (16-byte aligned buffer).  With
- * y_bf16 (may be NULL) every team also stores one bf16 to y_bf16[row] (the
- * GEMV's output pattern; bytes / (256 * loads) entries).  Otherwise sink (4
- * bytes) is written only if the folded data equals a fixed word. */
-int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, void* y_bf16, uint32_t* sink,
-                          void* stream);
+ * side (16-byte aligned; NULL exactly when side_bytes is 0) every workgroup
+ * first reads its own side_bytes (a multiple of 16, at most 16 * threads) at
+ * side + workgroup * side_bytes, one 16-byte load per thread, as the GEMV
+ * reads its block of weight scales.  With y_bf16 (may be NULL) every team
+ * also stores one bf16 to y_bf16[row] (the GEMV's output pattern;
+ * bytes / (256 * loads) entries).  Otherwise sink (4 bytes) is written only
+ * if the folded data equals a fixed word. */
+int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, const void* side, int side_bytes,
+                          void* y_bf16, uint32_t* sink, void* stream);
 
 #ifdef __cplusplus
 }

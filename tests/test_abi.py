@@ -28,7 +28,7 @@ def test_header_symbols_exported():
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(ql._SYMBOLS)
-    assert L.viper_hip_abi_version() == 3
+    assert L.viper_hip_abi_version() == 4
 
 
 def test_group_sizes_and_workspace():
@@ -84,15 +84,27 @@ def test_other_entry_validation():
     assert L.viper_hip_qlinear_partials(4, FAKE, FAKE, 0, 64, 8, 64, FAKE, 1, FAKE, None, None, 0, None, None) == 2
     assert L.viper_hip_check_quantizer(10, 5, FAKE, None) == 2
     assert L.viper_hip_check_quantizer(0, 255, FAKE, None) == 2
+    assert L.viper_hip_sampling_greedy_workspace_bytes(3) == 48
+    assert L.viper_hip_sampling_greedy_workspace_bytes(0) == 0
+    assert L.viper_hip_sampling_greedy_split(FAKE, FAKE, 2, 4096, None, 32, None) == 2        # no workspace
+    assert L.viper_hip_sampling_greedy_split(FAKE, FAKE, 2, 4096, FAKE, 31, None) == 2        # too small
+    assert L.viper_hip_sampling_greedy_split(FAKE, FAKE, 2, 4096, FAKE + 4, 32, None) == 2    # not 8-byte aligned
+    assert L.viper_hip_sampling_greedy_split(FAKE, FAKE, 0, 4096, FAKE, 32, None) == 2
+    assert L.viper_hip_sampling_greedy_split(FAKE + 1, FAKE, 2, 4096, FAKE, 32, None) == 2    # logits not bf16-aligned
     W = 320 * 5 * 16                                                      # one workgroup's bytes
-    assert L.viper_hip_stream_read(None, W, 320, 5, None, FAKE, None) == 2
-    assert L.viper_hip_stream_read(FAKE, 0, 320, 5, None, FAKE, None) == 2
-    assert L.viper_hip_stream_read(FAKE, W + 16, 320, 5, None, FAKE, None) == 2  # not whole workgroups
-    assert L.viper_hip_stream_read(FAKE + 8, W, 320, 5, None, FAKE, None) == 2   # buffer not 16-byte aligned
-    assert L.viper_hip_stream_read(FAKE, W, 320, 5, None, None, None) == 2
-    assert L.viper_hip_stream_read(FAKE, W, 300, 5, None, FAKE, None) == 2       # no such shape
-    assert L.viper_hip_stream_read(FAKE, W, 320, 6, None, FAKE, None) == 2
-    assert L.viper_hip_stream_read(FAKE, W, 320, 5, FAKE + 1, FAKE, None) == 2   # y not 2-byte aligned
+    assert L.viper_hip_stream_read(None, W, 320, 5, None, 0, None, FAKE, None) == 2
+    assert L.viper_hip_stream_read(FAKE, 0, 320, 5, None, 0, None, FAKE, None) == 2
+    assert L.viper_hip_stream_read(FAKE, W + 16, 320, 5, None, 0, None, FAKE, None) == 2  # not whole workgroups
+    assert L.viper_hip_stream_read(FAKE + 8, W, 320, 5, None, 0, None, FAKE, None) == 2   # buffer not 16-byte aligned
+    assert L.viper_hip_stream_read(FAKE, W, 320, 5, None, 0, None, None, None) == 2
+    assert L.viper_hip_stream_read(FAKE, W, 300, 5, None, 0, None, FAKE, None) == 2       # no such shape
+    assert L.viper_hip_stream_read(FAKE, W, 320, 6, None, 0, None, FAKE, None) == 2
+    assert L.viper_hip_stream_read(FAKE, W, 320, 5, None, 0, FAKE + 1, FAKE, None) == 2   # y not 2-byte aligned
+    assert L.viper_hip_stream_read(FAKE, W, 320, 5, FAKE, 1608, None, FAKE, None) == 2    # side not whole words
+    assert L.viper_hip_stream_read(FAKE, W, 320, 5, FAKE, 16 * 321, None, FAKE, None) == 2  # side past one per thread
+    assert L.viper_hip_stream_read(FAKE, W, 320, 5, None, 1600, None, FAKE, None) == 2    # side bytes without side
+    assert L.viper_hip_stream_read(FAKE, W, 320, 5, FAKE, 0, None, FAKE, None) == 2       # side without bytes
+    assert L.viper_hip_stream_read(FAKE + 8, W, 320, 5, FAKE + 8, 16, None, FAKE, None) == 2
 
 
 def test_registry_mirror():

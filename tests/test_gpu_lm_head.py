@@ -83,7 +83,13 @@ def test_lm_head_full_size_greedy(torch_dev):
     assert int(tok.item()) == int(O.argmax_bf16(y_ref)[0])
 
 
-def test_sampling_greedy_known_answers(torch_dev):
+def ws(torch, B, split):
+    """The split entry point's workspace (zeroed once), or None for the one-workgroup kernel."""
+    return torch.zeros(va.greedy_workspace_bytes(B), dtype=torch.uint8, device="cuda") if split else None
+
+
+@pytest.mark.parametrize("split", [False, True])
+def test_sampling_greedy_known_answers(torch_dev, split):
     torch = torch_dev
     rows = np.stack([
         bf16([1.0, 3.0, 3.0, 2.0, -1.0, 0.0, 0.0, 0.0]),
@@ -93,25 +99,27 @@ def test_sampling_greedy_known_answers(torch_dev):
         bf16([-2.0, -1.0, -3.0, -1.0, -7.0, -9.0, -9.0, -9.0]),
     ])
     out = torch.zeros(5, dtype=torch.int32, device="cuda")
-    assert va.sampling_greedy(dev(torch, rows), out).ok()
+    assert va.sampling_greedy(dev(torch, rows), out, workspace=ws(torch, 5, split)).ok()
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), [1, 1, 0, 2, 1])
 
 
-@pytest.mark.parametrize("B,V", [(3, 166144), (2, 1001), (4, 7)])
-def test_sampling_greedy_random(torch_dev, B, V):
+@pytest.mark.parametrize("split", [False, True])
+@pytest.mark.parametrize("B,V", [(3, 166144), (2, 1001), (4, 7), (2, 8200)])
+def test_sampling_greedy_random(torch_dev, B, V, split):
     torch = torch_dev
     rng = np.random.default_rng(V)
     lg = bf16(rng.standard_normal((B, V)))
     lg[0, V // 3] = lg[0, V // 2] = bf16([9.0])[0]   # a tie across lanes: the smaller index
     out = torch.zeros(B, dtype=torch.int32, device="cuda")
-    assert va.sampling_greedy(dev(torch, lg), out).ok()
+    assert va.sampling_greedy(dev(torch, lg), out, workspace=ws(torch, B, split)).ok()
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), O.argmax_bf16(lg))
     assert out.cpu().numpy()[0] == V // 3
 
 
-def test_sampling_greedy_ties_within_a_lane(torch_dev):
+@pytest.mark.parametrize("split", [False, True])
+def test_sampling_greedy_ties_within_a_lane(torch_dev, split):
     # Lane l scans octets l, l + 1024, ... in order: equal maxima in two octets
     # of one lane and twice within one octet (16-byte aligned rows), and in
     # the elements past the last octet (one row, V % 8 != 0), must all resolve
@@ -124,7 +132,7 @@ def test_sampling_greedy_ties_within_a_lane(torch_dev):
     lg[1, 8 * 2000 + 4] = lg[1, 8 * 2000 + 2] = top             # one octet, two equal values
     lg[1, 8 * 2000 + 1] = bf16([np.nan])[0]
     out = torch.zeros(2, dtype=torch.int32, device="cuda")
-    assert va.sampling_greedy(dev(torch, lg), out).ok()
+    assert va.sampling_greedy(dev(torch, lg), out, workspace=ws(torch, 2, split)).ok()
     torch.cuda.synchronize()
     np.testing.assert_array_equal(out.cpu().numpy(), [8 * 6 + 3, 8 * 2000 + 2])
     np.testing.assert_array_equal(out.cpu().numpy(), O.argmax_bf16(lg))
@@ -133,6 +141,41 @@ def test_sampling_greedy_ties_within_a_lane(torch_dev):
     lt[0, Vt - 2] = lt[0, Vt - 1] = top                         # the tail past the last octet
     lt[0, 8 * 17 + 1] = bf16([7.25])[0]
     ot = torch.zeros(1, dtype=torch.int32, device="cuda")
-    assert va.sampling_greedy(dev(torch, lt), ot).ok()
+    assert va.sampling_greedy(dev(torch, lt), ot, workspace=ws(torch, 1, split)).ok()
     torch.cuda.synchronize()
     assert ot.cpu().numpy()[0] == Vt - 2 == O.argmax_bf16(lt)[0]
+
+
+def test_sampling_greedy_split_across_workgroups(torch_dev):
+    # The split kernel's workgroups cover 4096 logits each and meet through
+    # one 64-bit key per row: equal maxima in different workgroups resolve to
+    # the smaller index, -0 and +0 are equal (the first wins), a row with
+    # nothing above -inf (NaN included) gives 0, and the workspace is zero
+    # again after every call, so calls in a row reuse it with other shapes.
+    torch = torch_dev
+    V = 166144
+    neg = bf16([-1.0])[0]
+    lg = np.full((4, V), neg, dtype=np.uint16)
+    lg[0, 4096 * 30 + 5] = lg[0, 4096 * 7 + 4095] = lg[0, V - 1] = bf16([3.0])[0]   # workgroups 7, 30, 40
+    lg[1, :] = bf16([-2.0])[0]
+    lg[1, 4096 * 9 + 1] = bf16([-0.0])[0]
+    lg[1, 4096 * 2 + 3] = bf16([0.0])[0]                                             # +0 first: it wins
+    lg[1, 4096 * 20] = bf16([-0.0])[0]
+    lg[2, :] = bf16([-np.inf])[0]
+    lg[2, 4096 * 12 + 8] = bf16([np.nan])[0]
+    lg[3, :] = bf16([np.nan])[0]
+    lg[3, 4096 * 39 + 77] = bf16([-np.inf])[0]
+    lg[3, 4096 * 40 + 1] = bf16([-65504.0])[0]                                       # the only finite value
+    expect = O.argmax_bf16(lg)
+    np.testing.assert_array_equal(expect, [4096 * 7 + 4095, 4096 * 2 + 3, 0, 4096 * 40 + 1])
+    w = ws(torch, 8, True)
+    out = torch.full((4,), -1, dtype=torch.int32, device="cuda")
+    for rows, V2 in ((4, V), (1, V), (3, 8200), (4, V)):
+        src = lg[:rows, :V2]
+        e = O.argmax_bf16(np.ascontiguousarray(src))
+        out.fill_(-1)
+        assert va.sampling_greedy(dev(torch, src), out[:rows], workspace=w).ok()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out[:rows].cpu().numpy(), e)
+        assert int(w.count_nonzero()) == 0
+

@@ -659,12 +659,27 @@ def test_stream_read_probe(torch_dev):
     buf = torch.zeros(rows * rowb, dtype=torch.uint8, device="cuda")
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
-    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), threads, loads, None, sink.data_ptr(), st) == 0
+    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), threads, loads, None, 0, None, sink.data_ptr(), st) == 0
     torch.cuda.synchronize()
     assert int(sink[0]) == 0
     words = buf.view(torch.int32)
     words[buf.numel() // 4 - 4] = np.int32(np.uint32(0x9E3779B9).view(np.int32))   # the last 16 bytes
-    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), threads, loads, None, sink.data_ptr(), st) == 0
+    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), threads, loads, None, 0, None, sink.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    assert np.uint32(int(sink[0]) & 0xFFFFFFFF) == np.uint32(0x9E3779B9)
+    # the side blocks (one per workgroup, as the GEMV's scale blocks) are read
+    # too: the magic word in the last workgroup's block reaches the sink
+    buf.zero_()
+    sink.zero_()
+    nwg, sb = rows // 20, 1600
+    side = torch.zeros(nwg * sb, dtype=torch.uint8, device="cuda")
+    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), threads, loads, side.data_ptr(), sb, None,
+                                   sink.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    assert int(sink[0]) == 0
+    side.view(torch.int32)[(nwg * sb - 16) // 4] = np.int32(np.uint32(0x9E3779B9).view(np.int32))
+    assert L.viper_hip_stream_read(buf.data_ptr(), buf.numel(), threads, loads, side.data_ptr(), sb, None,
+                                   sink.data_ptr(), st) == 0
     torch.cuda.synchronize()
     assert np.uint32(int(sink[0]) & 0xFFFFFFFF) == np.uint32(0x9E3779B9)
     buf.zero_()
@@ -677,7 +692,7 @@ def test_stream_read_probe(torch_dev):
         words.zero_()
         words[torch.arange(n // rb, device="cuda") * (rb // 4)] = torch.arange(n // rb, dtype=torch.int32, device="cuda")
         y.fill_(-1)
-        assert L.viper_hip_stream_read(buf.data_ptr(), n, th, ld, y.data_ptr(), sink.data_ptr(), st) == 0
+        assert L.viper_hip_stream_read(buf.data_ptr(), n, th, ld, None, 0, y.data_ptr(), sink.data_ptr(), st) == 0
         torch.cuda.synchronize()
         got = y.cpu().numpy()[: n // rb].astype(np.int64)
         np.testing.assert_array_equal(got, np.arange(n // rb))

@@ -134,7 +134,7 @@ def test_stack_production_size_every_launch(torch_dev, fused):
         O.assert_bf16_close(u16(s.x), y, a, rel=1e-5, what=f"slot {slot} down + residual")
 
     x_fin = u16(s.x)
-    s.head_step()
+    s.head_step(fused)
     torch.cuda.synchronize()
     xn = u16(s.xn)
     _close_bits(xn[0], O.rmsnorm_bf16(x_fin, u16(s.final_ln), s.eps)[0], "final rmsnorm")

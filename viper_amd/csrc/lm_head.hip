@@ -197,6 +197,91 @@ argmax_bf16_kernel(const uint16_t* logits, int32_t* __restrict__ out, int V) {
     }
 }
 
+// Split argmax: P workgroups per row, each over GR_OCT consecutive octets
+// (GR_NT threads, GR_OCT / GR_NT octets each, all requested at once), meet
+// through a 64-bit key per row in the caller's workspace:
+//   key = (order(value) << 32) | (0xFFFFFFFF - index),
+// where order maps floats to unsigned integers in the same order (+0 for
+// both zeros, which compare equal), so the largest key is the largest value
+// at its smallest index, the reference's (value, then smaller index) pick.
+// Each workgroup takes the max into the row's key, then (after the max has
+// returned, so it is performed first) counts itself on the row's counter;
+// the workgroup that counts last swaps the key for 0, resets the counter and
+// writes the index.  All four accesses are agent-scope atomics, performed in
+// the order each workgroup issues them, so the last count sees every max.
+// A workgroup with nothing above -inf offers (-inf, 0): a row with nothing
+// above -inf gives 0, as the single-workgroup kernel does.
+constexpr int GR_NT = 256;
+constexpr int GR_OCT = 512;  // octets (4096 logits, 8 KB) per workgroup
+
+__device__ __forceinline__ uint64_t greedy_key(float v, int i) {
+    const uint32_t u = v == 0.0f ? 0u : __float_as_uint(v);
+    const uint32_t o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)o << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)i);
+}
+
+__global__ void __launch_bounds__(GR_NT)
+argmax_split_kernel(const uint16_t* logits, int32_t* __restrict__ out, int V, int P, uint64_t* keys,
+                    unsigned* cnt) {
+    __shared__ float sv[GR_NT / 64];
+    __shared__ int si[GR_NT / 64];
+    constexpr int PT = GR_OCT / GR_NT;
+    const int b = (int)blockIdx.x / P, p = (int)blockIdx.x % P;
+    const int tid = (int)threadIdx.x;
+    const int noct = V / 8;  // whole octets (the host takes this kernel for V % 8 == 0 only)
+    const int o0 = p * GR_OCT;
+    const int n = min(GR_OCT, noct - o0);
+    const auto rr = buf(logits + (size_t)b * V + (size_t)o0 * 8, (uint32_t)n * 16);
+    u32x4 q[PT];
+#pragma unroll
+    for (int i = 0; i < PT; ++i) q[i] = bload16(rr, (tid + i * GR_NT) * 16);
+    float best = -__builtin_inff();
+    int boct = -1;
+#pragma unroll
+    for (int i = 0; i < PT; ++i) {
+        const int o = tid + i * GR_NT;
+        const float m = octet_max(q[i]);
+        if (o < n && m > best) {
+            best = m;
+            boct = o;
+        }
+    }
+    int idx = 0;
+    if (boct >= 0) {
+        const u32x4 v = bload16(rr, boct * 16);
+        const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
+        idx = (o0 + boct) * 8 + 7;
+#pragma unroll
+        for (int j = 7; j >= 0; --j)
+            if (bf16f((wd[j >> 1] >> (16 * (j & 1))) & 0xffffu) == best) idx = (o0 + boct) * 8 + j;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        better(best, idx, ov, oi);
+    }
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = best;
+        si[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int i = 1; i < GR_NT / 64; ++i) better(best, idx, sv[i], si[i]);
+        const uint64_t prev =
+            __hip_atomic_fetch_max(keys + b, greedy_key(best, idx), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // the count depends on the returned max (no key is all ones), so it
+        // is issued only after the max is performed
+        const unsigned inc = 1u + (unsigned)(prev == ~0ull);
+        const unsigned t = __hip_atomic_fetch_add(cnt + b, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (t == (unsigned)(P - 1)) {
+            const uint64_t k = __hip_atomic_exchange(keys + b, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(cnt + b, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            out[b] = (int32_t)(0xFFFFFFFFu - (uint32_t)k);
+        }
+    }
+}
+
 // ---- host
 
 typedef void (*lh_fn)(const uint16_t*, const uint16_t*, uint16_t*, int, int, int);
@@ -253,6 +338,31 @@ extern "C" int viper_hip_sampling_greedy(const void* logits_bf16, int32_t* out_t
     const uint16_t* a0 = (const uint16_t*)logits_bf16;
     void* args[] = {&a0, &out_token, &V};
     (void)hipLaunchKernel((const void*)vq::argmax_bf16_kernel, dim3((unsigned)B), dim3(vq::AM_NT), args, 0,
+                          (hipStream_t)stream);
+    return vq::status_of(hipGetLastError());
+}
+
+extern "C" size_t viper_hip_sampling_greedy_workspace_bytes(int B) {
+    return B > 0 ? (size_t)B * 16 : 0;
+}
+
+extern "C" int viper_hip_sampling_greedy_split(const void* logits_bf16, int32_t* out_token, int B, int V,
+                                               void* workspace, size_t workspace_bytes, void* stream) {
+    if (logits_bf16 == nullptr || out_token == nullptr || workspace == nullptr || B <= 0 || V <= 0)
+        return VIPER_INVALID_ARGUMENT;
+    if (vq::misaligned(logits_bf16, 2) || vq::misaligned(out_token, 4) || vq::misaligned(workspace, 8) ||
+        workspace_bytes < viper_hip_sampling_greedy_workspace_bytes(B))
+        return VIPER_INVALID_ARGUMENT;
+    // rows that are not whole 16-byte octets take the one-workgroup kernel
+    if (vq::misaligned(logits_bf16, 16) || V % 8 != 0)
+        return viper_hip_sampling_greedy(logits_bf16, out_token, B, V, stream);
+    int P = (V / 8 + vq::GR_OCT - 1) / vq::GR_OCT;
+    if ((long)P * B > (long)INT32_MAX) return VIPER_INVALID_ARGUMENT;
+    const uint16_t* a0 = (const uint16_t*)logits_bf16;
+    uint64_t* keys = (uint64_t*)workspace;
+    unsigned* cnt = (unsigned*)(keys + B);
+    void* args[] = {&a0, &out_token, &V, &P, &keys, &cnt};
+    (void)hipLaunchKernel((const void*)vq::argmax_split_kernel, dim3((unsigned)(P * B)), dim3(vq::GR_NT), args, 0,
                           (hipStream_t)stream);
     return vq::status_of(hipGetLastError());
 }

@@ -12,17 +12,22 @@ namespace vq {
 // are folded so the loads stay live.  With y, lane 0 of each team stores one
 // bf16 (the fold) to y[row], the GEMV's output pattern; without it the fold
 // reaches memory only in the (never expected) case that it equals a magic
-// word.
+// word.  With side (side_bytes per workgroup, a multiple of 16, at most
+// 16 * NTT), threads t < side_bytes / 16 first load 16 bytes each of the
+// workgroup's side block, as the GEMV loads its block of weight scales.
 template <int NTT, int L>
-__global__ void __launch_bounds__(NTT) stream_probe_kernel(const uint8_t* p, uint16_t* y, uint32_t* sink) {
+__global__ void __launch_bounds__(NTT) stream_probe_kernel(const uint8_t* p, uint16_t* y, uint32_t* sink,
+                                                           const uint8_t* side, int side_bytes) {
     constexpr int ROWS = NTT / 16, RB = 16 * L * 16;
     const int b = xcd_block((int)blockIdx.x, (int)gridDim.x);
     const int tid = (int)threadIdx.x, l = tid & 15, rr = tid >> 4;
+    const auto sr = buf(side + (size_t)b * side_bytes, (uint32_t)side_bytes);
+    const u32x4 sv = bload16(sr, tid * 16 < side_bytes ? tid * 16 : OOB);
     const auto r = buf(p + (size_t)b * ROWS * RB, (uint32_t)(ROWS * RB));
     u32x4 v[L];
 #pragma unroll
     for (int j = 0; j < L; ++j) v[j] = bload16<AUX_NT>(r, rr * RB + (j * 16 + l) * 16);
-    uint32_t f = 0u;
+    uint32_t f = sv.x ^ sv.y ^ sv.z ^ sv.w;
 #pragma unroll
     for (int j = 0; j < L; ++j) f ^= v[j].x ^ v[j].y ^ v[j].z ^ v[j].w;
     if (y != nullptr) {
@@ -32,7 +37,7 @@ __global__ void __launch_bounds__(NTT) stream_probe_kernel(const uint8_t* p, uin
     }
 }
 
-typedef void (*probe_fn)(const uint8_t*, uint16_t*, uint32_t*);
+typedef void (*probe_fn)(const uint8_t*, uint16_t*, uint32_t*, const uint8_t*, int);
 
 template <int NTT>
 static probe_fn probe_l(int loads) {
@@ -61,17 +66,21 @@ static probe_fn probe_kernel(int threads, int loads) {
 
 }  // namespace vq
 
-extern "C" int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, void* y_bf16,
-                                     uint32_t* sink, void* stream) {
+extern "C" int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, const void* side,
+                                     int side_bytes, void* y_bf16, uint32_t* sink, void* stream) {
     const vq::probe_fn fn = vq::probe_kernel(threads, loads);
     if (fn == nullptr || buf == nullptr || sink == nullptr) return VIPER_INVALID_ARGUMENT;
     const size_t per_wg = (size_t)threads * (size_t)loads * 16;
     if (bytes == 0 || bytes % per_wg != 0 || bytes / per_wg > (size_t)INT32_MAX) return VIPER_INVALID_ARGUMENT;
-    if (vq::misaligned(buf, 16) || vq::misaligned(sink, 4) || vq::misaligned(y_bf16, 2)) return VIPER_INVALID_ARGUMENT;
+    if (vq::misaligned(buf, 16) || vq::misaligned(sink, 4) || vq::misaligned(y_bf16, 2) || vq::misaligned(side, 16))
+        return VIPER_INVALID_ARGUMENT;
+    if (side_bytes < 0 || side_bytes % 16 != 0 || side_bytes > 16 * threads || (side_bytes > 0) != (side != nullptr))
+        return VIPER_INVALID_ARGUMENT;
     const unsigned grid = (unsigned)(bytes / per_wg);
     const uint8_t* a0 = (const uint8_t*)buf;
     uint16_t* a1 = (uint16_t*)y_bf16;
-    void* args[] = {&a0, &a1, &sink};
+    const uint8_t* a3 = (const uint8_t*)side;
+    void* args[] = {&a0, &a1, &sink, &a3, &side_bytes};
     vq::launch((const void*)fn, grid, (unsigned)threads, 0, (hipStream_t)stream, args);
     return vq::status_of(hipGetLastError());
 }

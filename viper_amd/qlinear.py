@@ -127,6 +127,8 @@ _SYMBOLS = (
     "viper_hip_swiglu_quantize",
     "viper_hip_linear_bf16",
     "viper_hip_sampling_greedy",
+    "viper_hip_sampling_greedy_workspace_bytes",
+    "viper_hip_sampling_greedy_split",
     "viper_hip_qlinear_m1",
     "viper_hip_qlinear_m1_swiglu",
     "viper_hip_qlinear_static",
@@ -166,7 +168,7 @@ def lib():
     L.viper_hip_check_bf16_rounding.restype = i32
     L.viper_hip_check_quantizer.argtypes = [i32, i32, vp, vp]
     L.viper_hip_check_quantizer.restype = i32
-    L.viper_hip_stream_read.argtypes = [vp, sz, i32, i32, vp, vp, vp]
+    L.viper_hip_stream_read.argtypes = [vp, sz, i32, i32, vp, i32, vp, vp, vp]
     L.viper_hip_stream_read.restype = i32
     L.viper_hip_qlinear_fused2.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     L.viper_hip_qlinear_fused2.restype = i32
@@ -181,6 +183,10 @@ def lib():
     L.viper_hip_linear_bf16.restype = i32
     L.viper_hip_sampling_greedy.argtypes = [vp, vp, i32, i32, vp]
     L.viper_hip_sampling_greedy.restype = i32
+    L.viper_hip_sampling_greedy_workspace_bytes.argtypes = [i32]
+    L.viper_hip_sampling_greedy_workspace_bytes.restype = sz
+    L.viper_hip_sampling_greedy_split.argtypes = [vp, vp, i32, i32, vp, sz, vp]
+    L.viper_hip_sampling_greedy_split.restype = i32
     L.viper_hip_qlinear_m1.argtypes = [i32, i32, i32, i32, i32, vp, vp, C.c_float, vp, i32, vp, vp, vp, vp, vp, vp]
     L.viper_hip_qlinear_m1.restype = i32
     L.viper_hip_qlinear_m1_swiglu.argtypes = [i32, i32, i32, i32, i32, vp, vp, C.c_float, vp, vp, vp, vp, vp, i32,
@@ -376,12 +382,23 @@ def linear_bf16(w, x, y, stream=None) -> Status:
     return _status(rc, "viper_hip_linear_bf16")
 
 
-def sampling_greedy(logits, out_token, stream=None) -> Status:
-    """out_token[b] = argmax of logits[b, :] (bf16), smallest index on ties."""
+def sampling_greedy(logits, out_token, stream=None, workspace=None) -> Status:
+    """out_token[b] = argmax of logits[b, :] (bf16), smallest index on ties.  With a workspace
+    (greedy_workspace_bytes(B) bytes, zero before its first use) each row is split over many
+    workgroups (viper_hip_sampling_greedy_split)."""
     V = logits.shape[-1]
     B = int(logits.numel() // V)
+    if workspace is not None:
+        nbytes = workspace.numel() * workspace.element_size()
+        rc = lib().viper_hip_sampling_greedy_split(ptr(logits), ptr(out_token), B, V, ptr(workspace), nbytes,
+                                                   _stream(stream))
+        return _status(rc, "viper_hip_sampling_greedy_split")
     rc = lib().viper_hip_sampling_greedy(ptr(logits), ptr(out_token), B, V, _stream(stream))
     return _status(rc, "viper_hip_sampling_greedy")
+
+
+def greedy_workspace_bytes(B: int) -> int:
+    return int(lib().viper_hip_sampling_greedy_workspace_bytes(B))
 
 
 def check_quantizer(exp_lo, exp_hi, counts, stream=None) -> Status:

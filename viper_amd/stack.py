@@ -72,6 +72,8 @@ class Stack:
         self.xs = torch.empty((kmax // 64,), dtype=torch.float32, device="cuda")
         self.logits = torch.empty((1, vocab), dtype=bf, device="cuda")
         self.token = torch.empty((1,), dtype=torch.int32, device="cuda")
+        # the split greedy pick's workspace: zero once, every call leaves it zero
+        self.greedy_ws = torch.zeros((16,), dtype=torch.uint8, device="cuda")
         # trace: every launch also leaves its intermediates readable (the
         # normalized rows in xn, gate in g, up in ut, h in gt) through the same
         # kernels' optional outputs, so a test can check each launch in turn
@@ -155,21 +157,26 @@ class Stack:
         self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wd[0]), p(wd[1]), 0, 64, H, I, p(self.xq), p(self.xs), 1,
                                                   p(x), p(x), st), "down")
 
-    def head_step(self):
-        """Final rmsnorm of x (into self.xn), the bf16 LM head and the greedy token."""
+    def head_step(self, fused=True):
+        """Final rmsnorm of x (into self.xn), the bf16 LM head and the greedy token (fused: each
+        logits row split over many workgroups, viper_hip_sampling_greedy_split)."""
         L, st = self.L, self.torch.cuda.current_stream().cuda_stream
         p = lambda t: t.data_ptr()
         self._ok(L.viper_hip_rmsnorm_quantize(p(self.x), p(self.final_ln), self.eps, 1, self.H, 64, p(self.xn),
                                               p(self.xq), p(self.xs), st), "final norm")
         self._ok(L.viper_hip_linear_bf16(p(self.head), p(self.xn), p(self.logits), 1, self.V, self.H, st), "lm_head")
-        self._ok(L.viper_hip_sampling_greedy(p(self.logits), p(self.token), 1, self.V, st), "greedy")
+        if fused:
+            self._ok(L.viper_hip_sampling_greedy_split(p(self.logits), p(self.token), 1, self.V, p(self.greedy_ws),
+                                                       self.greedy_ws.numel(), st), "greedy")
+        else:
+            self._ok(L.viper_hip_sampling_greedy(p(self.logits), p(self.token), 1, self.V, st), "greedy")
 
     def _step(self, fused):
         self.x.copy_(self.x0)
         for l in range(self.layers * self.passes):
             self.attention_half(l, fused)
             self.mlp_half(l, fused)
-        self.head_step()
+        self.head_step(fused)
 
     def step_fused(self):
         """One decode step, 4 launches per slot (producers folded, q/k/v together)."""
