@@ -40,6 +40,7 @@ constexpr int M1_XS = 4;    // activation octets per thread loaded before the we
 constexpr int M1_XS_MR = 8; // the same for MR > 1 rows (all of them: no later rounds)
 constexpr int M1_DELAY = 6; // weight-issue delay, s_sleep units (one activation row)
 constexpr int M1_DELAY_MR = 8; // the same for MR > 1 rows (MR rows of activation ahead of the weights)
+constexpr int M1_DELAY_PAIR = 16; // the same for the gate/up pair (twice the weight stream per workgroup)
 
 // Row length of an exact tiling (TS lanes x CPL chunks of CK weights): an
 // exact launch's K is this constant, so its load rounds and offsets are
@@ -212,14 +213,21 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     constexpr int KX = EXACT ? m1_exact_k<F>(TS, CPL) : 0;
     const int grid = K;
     if constexpr (EXACT) K = KX;
-    // SPARE: in a 256- or 320-thread workgroup of an exact tiling with the
-    // bf16 prologue, the first wave stages no activation and issues its
-    // weights at once, without the delay; the other ANT threads stage the
-    // row (in one more round where needed).  The weight stream then starts a
-    // wave earlier: north star 3.91 -> 3.75 us, K = N = 2560 2.52 -> 2.43 us
-    // (the 640-thread down shape and the gate/up pair do not gain).  The
-    // staged LDS row is the same either way.
-    constexpr bool SPARE = EXACT && MR == 1 && PRO == PRO_BF16 && MODE != M1_SWIGLU && (NTT == 256 || NTT == 320);
+    // SPARE: the first wave stages no activation and issues its weights at
+    // once, without the delay; the other ANT threads stage the row (in one
+    // more round where needed).  The weight stream then starts a wave
+    // earlier.  Taken where it was measured to pay: exact tilings of 256 or
+    // 320 threads with the bf16 prologue (north star 3.91 -> 3.75 us,
+    // K = N = 2560 2.52 -> 2.43 us) and the gate/up pair, whose other waves
+    // also wait longer (M1_DELAY_PAIR: 6.33 -> 5.80 us at K = 2560,
+    // N = 10240).  The staged LDS row is the same either way; for the rmsnorm
+    // prologue the pair keeps one octet per staging thread (K / 8 <= ANT), so
+    // each wave's sum of squares covers the same octets as without the spare
+    // wave and the row's sum (wave sums in wave order, the spare wave's 0
+    // first) is unchanged bit for bit.
+    constexpr bool SPARE = EXACT && MR == 1 &&
+                           ((PRO == PRO_BF16 && MODE != M1_SWIGLU && (NTT == 256 || NTT == 320)) ||
+                            (MODE == M1_SWIGLU && (PRO == PRO_BF16 || (PRO == PRO_RMSNORM && KX / 8 <= NTT - 64))));
     constexpr int A0 = SPARE ? 64 : 0;  // first staging thread
     constexpr int ANT = NTT - A0;       // staging threads
     constexpr int XS = EXACT ? (MR * (KX / 8) + ANT - 1) / ANT : MR > 1 ? M1_XS_MR : M1_XS;
@@ -331,8 +339,8 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < XS; ++i) {
-            if (i == 0 || NTT * i < noct) {
-                const int o = tid + NTT * i;
+            if ((i == 0 || ANT * i < noct) && stager) {
+                const int o = at + ANT * i;
                 if constexpr (PRE) xv[i].z = bload4(xsr, (o % OPC == 0) ? (o / OPG) * 4 : OOB);
                 else av[i] = bload16(xsr, o * 16);
             }
@@ -393,7 +401,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         float ss = 0.0f;
 #pragma unroll
         for (int i = 0; i < XS; ++i) {
-            if (tid + NTT * i < noct) {
+            if (stager && at + ANT * i < noct) {
                 const u32x4 v = xv[i];
                 const uint32_t wd[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
@@ -463,7 +471,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     for (int i = 0; i < XS; ++i) {
         if (i < xiters && wave0 + ANT * i < noct && stager) {
             if constexpr (TWO) {
-                const int o = tid + NTT * i;
+                const int o = at + ANT * i;
                 const u32x4 v = produce(xv[i], av[i]);
                 if (PRO == PRO_RMSNORM && xout != nullptr && blockIdx.x == 0 && o < noct)
                     *(u32x4*)(xout + (size_t)o * 8) = v;
@@ -580,7 +588,8 @@ m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
 #define VQ_M1(TS_, NTT_, CPL_)                                                                      \
     if constexpr ((MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_)) && (MR == 1 || m1_mr_shape_ok(TS_, NTT_, CPL_))) \
         if (ts == TS_ && ntt == NTT_ && cpl == CPL_)                                                \
-            return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, MR, MR == 1 ? M1_DELAY : M1_DELAY_MR>;
+            return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, MR,                          \
+                                   MODE == M1_SWIGLU ? M1_DELAY_PAIR : MR == 1 ? M1_DELAY : M1_DELAY_MR>;
     VQ_M1(8, 128, 10) VQ_M1(8, 192, 10) VQ_M1(8, 320, 10) VQ_M1(16, 256, 10) VQ_M1(16, 640, 10)
     VQ_M1(32, 320, 10) VQ_M1(32, 640, 10) VQ_M1(64, 640, 10) VQ_M1(16, 256, 5) VQ_M1(16, 320, 5)
     VQ_M1(16, 640, 5) VQ_M1(32, 640, 5) VQ_M1(64, 640, 5)
