@@ -286,12 +286,12 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     const size_t need = workspace_need(qtype, N, K, M);
     if (wsp == nullptr || wsp_bytes < need || misaligned(wsp, 16)) return VIPER_INVALID_ARGUMENT;
     // Few rows: every workgroup quantizes the rows itself, one launch (the
-    // workspace stays required for M > 1 whichever kernel runs).  Two rows of
-    // one matrix on the M = 1 kernel's dot path; 3..8 rows on the matrix cores
-    // with the quantize into LDS (north-star shape: M = 3 6.15 us, 5 6.63 us,
-    // 8 7.49 us against 6.28 / 8.21 / 8.25 us for the next-best path; at
-    // M >= 10 the rows' quantize in every workgroup costs more than the
-    // quantize launch).
+    // workspace stays required for M > 1 whichever kernel runs).  Two to four
+    // rows of one matrix on the M = 1 kernel's dot path; 5..8 rows (and fused
+    // pairs of 3..8) on the matrix cores with the quantize into LDS
+    // (north-star shape: M = 5 6.63 us, 8 7.49 us against 8.21 / 8.25 us for
+    // the next-best path; at M >= 10 the rows' quantize in every workgroup
+    // costs more than the quantize launch).
     const bool mf = mfma_ok(qtype, K, M, s) && (b.w == nullptr || mfma_ok(qtype, K, M, b.s));
     if (b.w == nullptr && M == 2 && m1_rows_ok(qtype, K, M)) {
         const M1Out outs[1] = {{w, s, y, N}};
@@ -305,15 +305,18 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     // two launches (W8 3 rows 8.37 against 9.23 us), and Q5/Q6 8 rows in two
     // launches (8.65 / 8.89 against 9.01 / 9.10 us); 6 rows of every format
     // and 8 of W8 stay here.
+    // 3 or 4 rows of one matrix take the multi-row dot kernel below in every
+    // format (Q4 at K = 2560, N = 10240: 4 rows 6.03 against 6.29 us here).
     const bool hi = qtype == VIPER_QTYPE_Q5_G64 || qtype == VIPER_QTYPE_Q6_G64;
+    const bool rows_ok = b.w == nullptr && m1_rows_ok(qtype, K, M) && (long)M * K <= 32768;
     const bool bf_ok = mf && M >= 3 && M <= (hi ? 7 : 8) && !split_ok && rc_bf16_ok(qtype, N, K, M, b.w != nullptr);
-    if (bf_ok && (qtype == VIPER_QTYPE_Q4_G64 || M > 4))
+    if (bf_ok && (M > 4 || !rows_ok))
         return launch_rc(qtype, w, s, senc, N, K, x, nullptr, RC_BF16, M, y, res, part, b.w, b.s, b.y, st);
-    // (3 or 4 rows here where the LDS copy does not fit: while every
+    // (3 or 4 rows here also where the LDS copy does not fit: while every
     // workgroup's share of the rows' quantize stays small; down shape
     // K = 10240: 3 rows 8.8 us against about 9.5 us for two launches with the K
     // split)
-    if (b.w == nullptr && m1_rows_ok(qtype, K, M) && (long)M * K <= 32768) {
+    if (rows_ok) {
         const M1Out outs[1] = {{w, s, y, N}};
         return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, M);
     }
