@@ -42,6 +42,7 @@ constexpr int M1_DELAY = 6; // weight-issue delay, s_sleep units (one activation
 constexpr int M1_DELAY_MR = 8; // the same for MR > 1 rows (MR rows of activation ahead of the weights)
 constexpr int M1_DELAY_PAIR = 16; // the same for the gate/up pair (twice the weight stream per workgroup)
 constexpr int M1_DELAY_RMS = 3;   // the same for the rmsnorm prologue (q/k/v: 3.31 -> 3.23 us against 6)
+constexpr int M1_DELAY_WIDE = 10; // the same for a wide launch with the bf16 prologue (W8, K = 2560: 5.80 -> 5.71 us)
 
 // Row length of an exact tiling (TS lanes x CPL chunks of CK weights): an
 // exact launch's K is this constant, so its load rounds and offsets are
@@ -61,9 +62,22 @@ __host__ __device__ constexpr int m1_exact_k(int ts, int cpl) { return Fmt<F>::C
 // [workgroup][wave][M1_TL_STAMPS] uint64 s_memrealtime readings (100 MHz).
 enum { M1_PLAIN = 0, M1_PART = 1, M1_SWIGLU = 2, M1_TL = 3 };
 
+// A wide launch: an exact tiling whose activation rows fill at most half of
+// its threads' octet slots (W8 at K = 2560 on 640 threads, the gate/up pair),
+// so half of its waves stage nothing.
+template <int F>
+__host__ __device__ constexpr bool m1_wide(bool exact, int ts, int ntt, int cpl, int mr) {
+    return exact && mr * (m1_exact_k<F>(ts, cpl) / 8) <= ntt / 2;
+}
+
 // Weight-issue delay of a launch kind (s_sleep units).
-__host__ __device__ constexpr int m1_delay(int mode, int mr, int pro) {
-    return mode == M1_SWIGLU ? M1_DELAY_PAIR : mr > 1 ? M1_DELAY_MR : pro == PRO_RMSNORM ? M1_DELAY_RMS : M1_DELAY;
+template <int F>
+__host__ __device__ constexpr int m1_delay(bool exact, int ts, int ntt, int cpl, int mode, int mr, int pro) {
+    return mode == M1_SWIGLU                                   ? M1_DELAY_PAIR
+           : mr > 1                                            ? M1_DELAY_MR
+           : pro == PRO_RMSNORM                                ? M1_DELAY_RMS
+           : pro == PRO_BF16 && m1_wide<F>(exact, ts, ntt, cpl, mr) ? M1_DELAY_WIDE
+                                                               : M1_DELAY;
 }
 constexpr int M1_TL_STAMPS = 8;
 __host__ __device__ constexpr bool m1_pair_ok(int ts, int ntt) {
@@ -223,8 +237,9 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // once, without the delay; the other ANT threads stage the row (in one
     // more round where needed).  The weight stream then starts a wave
     // earlier.  Taken where it was measured to pay: exact tilings of 256 or
-    // 320 threads with the bf16 prologue (north star 3.91 -> 3.75 us,
-    // K = N = 2560 2.52 -> 2.43 us) and the gate/up pair, whose other waves
+    // 320 threads and wide ones with the bf16 prologue (north star 3.91 ->
+    // 3.75 us, K = N = 2560 2.52 -> 2.43 us, W8 at K = 2560 6.00 -> 5.80 us)
+    // and the gate/up pair, whose other waves
     // also wait longer (M1_DELAY_PAIR: 6.33 -> 5.80 us at K = 2560,
     // N = 10240).  The staged LDS row is the same either way; for the rmsnorm
     // prologue the pair keeps one octet per staging thread (K / 8 <= ANT), so
@@ -232,7 +247,8 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // wave and the row's sum (wave sums in wave order, the spare wave's 0
     // first) is unchanged bit for bit.
     constexpr bool SPARE = EXACT && MR == 1 &&
-                           ((PRO == PRO_BF16 && MODE != M1_SWIGLU && (NTT == 256 || NTT == 320)) ||
+                           ((PRO == PRO_BF16 && MODE != M1_SWIGLU &&
+                             (NTT == 256 || NTT == 320 || m1_wide<F>(EXACT, TS, NTT, CPL, MR))) ||
                             (MODE == M1_SWIGLU && (PRO == PRO_BF16 || (PRO == PRO_RMSNORM && KX / 8 <= NTT - 64))));
     constexpr int A0 = SPARE ? 64 : 0;  // first staging thread
     constexpr int ANT = NTT - A0;       // staging threads
@@ -595,7 +611,7 @@ m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
     if constexpr ((MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_)) && (MR == 1 || m1_mr_shape_ok(TS_, NTT_, CPL_))) \
         if (ts == TS_ && ntt == NTT_ && cpl == CPL_)                                                \
             return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, MR,                          \
-                                   m1_delay(MODE, MR, PRO)>;
+                                   m1_delay<F>(EXACT, TS_, NTT_, CPL_, MODE, MR, PRO)>;
     VQ_M1(8, 128, 10) VQ_M1(8, 192, 10) VQ_M1(8, 320, 10) VQ_M1(16, 256, 10) VQ_M1(16, 640, 10)
     VQ_M1(32, 320, 10) VQ_M1(32, 640, 10) VQ_M1(64, 640, 10) VQ_M1(16, 256, 5) VQ_M1(16, 320, 5)
     VQ_M1(16, 640, 5) VQ_M1(32, 640, 5) VQ_M1(64, 640, 5)
