@@ -39,7 +39,9 @@ gemv_bf16_kernel(const uint16_t* __restrict__ w, const uint16_t* x, uint16_t* __
     const int tid = (int)threadIdx.x;
     const int l = tid % TS;
     const int rr = tid / TS;
-    const int row0 = (int)blockIdx.x * ROWS;
+    // row blocks in XCD order (each XCD streams one contiguous range of rows):
+    // 121.5 -> 117.3 us for the 166144 x 2560 head
+    const int row0 = xcd_block((int)blockIdx.x, (int)gridDim.x) * ROWS;
     const int row = row0 + rr;
     const int nrows = min(ROWS, N - row0);
     const bool row_ok = rr < nrows;
