@@ -149,3 +149,32 @@ def test_stack_production_size_every_launch(torch_dev, fused):
     torch.cuda.synchronize()
     np.testing.assert_array_equal(u16(s.logits), logits)
     assert int(s.token.item()) == token
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_stack_step_graph_replays_equal_eager(torch_dev, fused):
+    """The decode step captured in one HIP graph (as the bench times it): three replays, with eager
+    steps between them, each give the eager step's logits and token bit for bit (the split greedy
+    pick's workspace is left zero by every call, so replays need no clearing)."""
+    torch = torch_dev
+    from viper_amd.stack import Stack
+    s = Stack(torch, hidden=512, inter=1024, n_heads=4, n_kv_heads=1, head_dim=128, layers=3, passes=2,
+              vocab=20000, seed=11)
+    run = s.step_fused if fused else s.step
+    run()
+    torch.cuda.synchronize()
+    logits, token = u16(s.logits), int(s.token.item())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        run()
+    for i in range(3):
+        s.logits.zero_()
+        s.token.fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(u16(s.logits), logits, err_msg=f"replay {i}")
+        assert int(s.token.item()) == token
+        run()   # eager work between the replays
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(u16(s.logits), logits)
+    assert int(s.greedy_ws.count_nonzero()) == 0
