@@ -239,13 +239,13 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // earlier.  Taken where it was measured to pay: exact tilings of 256 or
     // 320 threads and wide ones with the bf16 prologue (north star 3.91 ->
     // 3.75 us, K = N = 2560 2.52 -> 2.43 us, W8 at K = 2560 6.00 -> 5.80 us)
-    // and the gate/up pair, whose other waves
-    // also wait longer (M1_DELAY_PAIR: 6.33 -> 5.80 us at K = 2560,
-    // N = 10240).  The staged LDS row is the same either way; for the rmsnorm
-    // prologue the pair keeps one octet per staging thread (K / 8 <= ANT), so
-    // each wave's sum of squares covers the same octets as without the spare
-    // wave and the row's sum (wave sums in wave order, the spare wave's 0
-    // first) is unchanged bit for bit.
+    // and the gate/up pair, whose other waves also wait longer
+    // (M1_DELAY_PAIR: 6.33 -> 5.80 us at K = 2560, N = 10240).  The staged
+    // LDS row is the same either way; for the rmsnorm prologue the pair keeps
+    // one octet per staging thread (K / 8 <= ANT), so each wave's sum of
+    // squares covers the same octets as without the spare wave and the row's
+    // sum (wave sums in wave order, the spare wave's 0 first) is unchanged
+    // bit for bit.
     constexpr bool SPARE = EXACT && MR == 1 &&
                            ((PRO == PRO_BF16 && MODE != M1_SWIGLU &&
                              (NTT == 256 || NTT == 320 || m1_wide<F>(EXACT, TS, NTT, CPL, MR))) ||
