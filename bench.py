@@ -1,20 +1,21 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized linear hot path on one MI355X.
 
-A step is one Q4_G64 M=1 GEMV (K=2560, N=10240: the north-star shape) over one
-weight copy.  Weights rotate over >= 512 MB of distinct copies so the 256 MB
-MALL cannot serve them; x, y and the copies are resident in HBM before the
-timed region.
+A step is one pass of the hot path over one batch of synthetic input: the
+Q4_G64 M=1 GEMV (K=2560, N=10240: the north-star shape) over each of the
+weight copies in turn (40 copies, 557 MB: more than the 256 MB MALL, so every
+weight byte comes from HBM); x, y and the copies are resident in HBM before
+the timed region.
 
-The K timed steps (at least 200, after at least 20 eager warm-ups) are one
-HIP graph of K launches cycling over the weight copies, replayed once untimed
-and once timed, so the host never throttles the stream and no graph-launch
-boundary falls inside the timed launches; HIP events on that stream bracket
-the timed region.  value = algorithmic bytes * K / elapsed, and the roofline's
-achieved bandwidth uses the same average launch duration (elapsed / K).  Every
-other line is timed the same way (one graph of >= 200 calls).  The CPU
-baseline is the oracle's C restatement of the same GEMV (same semantics,
-seeded inputs), timed on this host with 1 and all threads.
+Exactly K steps are timed (K * 40 dispatches, so K >= 5 gives the >= 200
+dispatches a measurement needs), after W warm-up steps run eagerly: HIP graphs
+of up to 25 steps (1000 launches) each, every graph replayed once untimed and
+then back to back in the timed region, bracketed by HIP events on the replay
+stream, so the host never throttles the stream.  value = algorithmic bytes *
+dispatches / elapsed; the roofline's achieved bandwidth uses the same average
+dispatch duration (us_per_gemv).  Every other line is timed over one graph of
+>= 200 calls.  The CPU baseline is the oracle's C restatement of the same GEMV
+(same semantics, seeded inputs), timed on this host with 1 and all threads.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
        python bench.py --read-sweep | --timeline | --only LINE   (measurement modes)
@@ -33,7 +34,8 @@ sys.path.insert(0, ROOT)
 METRIC = "Q4_G64 GEMV µs + achieved HBM GB/s (% of peak) at M=1; M=16 verify µs"
 PEAK_GBS = 8000.0
 ROTATE_BYTES = 512 * 1024 * 1024
-MIN_STEPS, MIN_WARMUP = 200, 20
+MIN_STEPS = 200  # calls per line for the lines other than the headline
+GRAPH_STEPS = 25  # headline steps per captured graph
 
 
 def algorithmic_bytes(qtype_bytes_per_row, N, K, M, G=64):
@@ -286,8 +288,8 @@ def time_config3(torch, stk, fused, replays=10):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=4000)
-    ap.add_argument("--warmup", type=int, default=400)
+    ap.add_argument("--steps", type=int, default=100, help="timed steps (one GEMV over each weight copy)")
+    ap.add_argument("--warmup", type=int, default=10, help="eager warm-up steps")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (FETCH_SIZE/WRITE_SIZE calibration under rocprofv3)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -380,16 +382,31 @@ def main():
         if rc != 0:
             raise RuntimeError(f"viper_hip_qlinear failed: {rc}")
 
-    # at least MIN_STEPS timed dispatches after at least MIN_WARMUP warm-ups,
-    # whatever --steps / --warmup ask (both counts are reported)
-    steps = max(args.steps, MIN_STEPS)
-    warmup = max(args.warmup, MIN_WARMUP)
-    for i in range(warmup):
+    # exactly --steps steps of `copies` dispatches each, after --warmup eager steps
+    steps, warmup = max(1, args.steps), max(0, args.warmup)
+    for i in range(warmup * copies):
         launch(i)
-    graph = capture_n(torch, launch, steps)
-    job_ms = time_graph(torch, graph, 1)
+    full, rest = divmod(steps, GRAPH_STEPS)
+    graphs = []
+    if full:
+        graphs.append((capture_n(torch, launch, GRAPH_STEPS * copies), full))
+    if rest:
+        graphs.append((capture_n(torch, launch, rest * copies), 1))
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for g, reps in graphs:
+        for _ in range(reps):
+            g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    job_ms = e0.elapsed_time(e1)
+    dispatches = steps * copies
+    del graphs
     ms_per_step = job_ms / steps
-    value = alg * steps / (job_ms * 1e-3) / 1e9
+    us_per_gemv = job_ms * 1e3 / dispatches
+    value = alg * dispatches / (job_ms * 1e-3) / 1e9
     achieved = value
 
     extras = {}
@@ -411,8 +428,8 @@ def main():
         for i in range(20):
             launch_read(i)
             launch_read(i, True)
-        read_us = time_steps(torch, launch_read, max(args.steps, MIN_STEPS))
-        io_us = time_steps(torch, lambda i: launch_read(i, True), max(args.steps, MIN_STEPS))
+        read_us = time_steps(torch, launch_read, max(10 * copies, MIN_STEPS))
+        io_us = time_steps(torch, lambda i: launch_read(i, True), max(10 * copies, MIN_STEPS))
         extras["stream_read_weights_us"] = round(read_us, 3)
         extras["stream_read_weights_gbs"] = round(wbytes / (read_us * 1e-6) / 1e9, 1)
         extras["stream_read_gemv_io_us"] = round(io_us, 3)
@@ -609,8 +626,6 @@ def main():
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
-        "steps_requested": args.steps,
-        "warmup_requested": args.warmup,
         "ms_per_step": round(ms_per_step, 6),
         "higher_is_better": True,
         "scaling": "weak",
@@ -619,10 +634,13 @@ def main():
         "data": "synthetic (seeded: uniform int4 weights, fp16 log-uniform scales, bf16 N(0,1) x)",
         "config": {"workload": "Q4_G64 GEMV M=1 K=2560 N=10240 (north star), fused bf16->int8 quantize",
                    "qtype": "Q4_G64", "M": M, "K": K, "N": N, "weight_copies": copies,
-                   "rotation_bytes": copies * copy_bytes, "algorithmic_bytes_per_step": alg,
-                   "timed_region": (f"one HIP graph of {steps} launches cycling over the weight copies, replayed once "
-                                    f"after {warmup} eager warm-up launches and one untimed replay; events on the stream")},
-        "us_per_gemv": round(ms_per_step * 1e3, 3),
+                   "rotation_bytes": copies * copy_bytes, "algorithmic_bytes_per_gemv": alg,
+                   "algorithmic_bytes_per_step": alg * copies,
+                   "step": f"one GEMV over each of the {copies} weight copies ({copies} dispatches)",
+                   "timed_region": (f"{steps} steps = {dispatches} dispatches: HIP graphs of up to {GRAPH_STEPS} steps, "
+                                    f"each replayed once untimed, then back to back between events on the stream, "
+                                    f"after {warmup} eager warm-up steps")},
+        "us_per_gemv": round(us_per_gemv, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic},
         "cpu_baseline": cpu,
