@@ -74,7 +74,7 @@
  *   y[m][n] = bf16_RNE( sum_g ws[n][g] * xs[m][g] * D[m][n][g] [+ residual] ),
  *   D = exact int32 group dot.
  *
- * Alignment: w_packed and x 16 bytes, xq 8 bytes, xs 4 bytes, scales, y and
+ * Alignment: w_packed, scales and x 16 bytes, xq 8 bytes, xs 4 bytes, y and
  * residual 2 bytes, partials 4 bytes.  Shapes: N, K, M > 0, K % G == 0,
  * M <= 16.
  */

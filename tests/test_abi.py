@@ -65,6 +65,8 @@ FAKE = 0x10000  # never dereferenced: every call below fails validation first
     (dict(group=32), 2),            # group does not match the format
     (dict(senc=2), 2),
     (dict(w=FAKE + 8), 2),          # weights not 16-byte aligned
+    (dict(s=FAKE + 2), 2),          # scales not 16-byte aligned (read in 16-byte blocks)
+    (dict(s=FAKE + 8), 2),
     (dict(x=FAKE + 4), 2),
     (dict(M=2), 2),                 # M > 1 needs a workspace
 ])

@@ -84,6 +84,13 @@ __host__ __device__ constexpr size_t rc_lds_bytes(int hstr, int RB, int W) {
 // RC_BF16: the LDS copy of the fragments (64 lanes x QB bytes per group) and
 // of the [group][16] activation scales, after the regions above.
 __host__ __device__ constexpr size_t rc_act_lds_bytes(int qb, int ng) { return (size_t)ng * 64 * qb + (size_t)ng * 64; }
+// Single-segment launches with fragment input stage their scales in LDS
+// after the regions above: the weight scales of the workgroup's rows for its
+// quads ([row][quad], 8 bytes each, rows of whole 16-row tiles), then the
+// activation scales of its quads ([group][16] fp32).
+__host__ __device__ constexpr size_t rc_stage_bytes(int RB, int nq) {
+    return (size_t)16 * ((RB + 1) / 2) * nq * 8 + (size_t)nq * 256;
+}
 
 template <int F, int RB, int QW>
 struct RcSeg {
@@ -132,7 +139,8 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     static_assert(SK == 1 || AM == RC_FRAG, "the K split reads fragments");
     constexpr int G = F == 8 ? 32 : 64;
     extern __shared__ __align__(16) uint8_t smem[];
-    const int tid = (int)threadIdx.x, L = tid & 63, wave = tid >> 6;
+    // the wave index as a scalar: per-quad conditions are then uniform branches
+    const int tid = (int)threadIdx.x, L = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n16 = L & 15, kb = L >> 4, qi = ((kb & 1) << 1) | (kb >> 1);
     const int NG = K / G, NQ = NG / 4 / SK;  // quads of this workgroup's part of K
     const int nseg = ONE ? 1 : (NQ + W * QW - 1) / (W * QW);
@@ -160,12 +168,17 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     const int hrb = NG * (FM::HQ / 4);       // high plane: HQ / 4 bytes per group
     // (with a K split the resources start at the part's first quad: the
     // offsets below stay those of an unsplit launch with NQ quads)
-    const auto wr = buf(w + (size_t)row0 * rbytes + q0 * 128, (uint32_t)(nrows * rbytes - q0 * 128));
-    const auto hr = buf(w + (size_t)N * rbytes + (size_t)row0 * hrb + q0 * FM::HQ, (uint32_t)(nrows * hrb - q0 * FM::HQ));
-    const auto sr = buf(ws + (size_t)row0 * NG + 4 * q0, (uint32_t)(nrows * NG - 4 * q0) * 2);
-    const auto xr = buf(xq + (size_t)q0 * 4 * 64 * FM::QB,
-                        XNAT ? (uint32_t)(M * K) : XBF ? (uint32_t)(M * K) * 2 : (uint32_t)(NG - 4 * q0) * 64 * FM::QB);
-    const auto xsr = buf(xs + (size_t)q0 * 4 * 16, XNAT ? (uint32_t)(M * NG * 4) : XBF ? 0u : (uint32_t)(NG - 4 * q0) * 64);
+    const uint8_t* wp = w + (size_t)row0 * rbytes + q0 * 128;
+    const uint8_t* hp = w + (size_t)N * rbytes + (size_t)row0 * hrb + q0 * FM::HQ;
+    const uint16_t* sp0 = ws + (size_t)row0 * NG + 4 * q0;
+    const int8_t* xp = xq + (size_t)q0 * 4 * 64 * FM::QB;
+    const float* xsp = xs + (size_t)q0 * 4 * 16;
+    const uint32_t wn = (uint32_t)(nrows * rbytes - q0 * 128), hn = (uint32_t)(nrows * hrb - q0 * FM::HQ);
+    const uint32_t sn = (uint32_t)(nrows * NG - 4 * q0) * 2;
+    const uint32_t xn = XNAT ? (uint32_t)(M * K) : XBF ? (uint32_t)(M * K) * 2 : (uint32_t)(NG - 4 * q0) * 64 * FM::QB;
+    const uint32_t xsn = XNAT ? (uint32_t)(M * NG * 4) : XBF ? 0u : (uint32_t)(NG - 4 * q0) * 64;
+    const auto xr = buf(xp, xn);
+    const auto xsr = buf(xsp, xsn);
     const bool m_ok = n16 < M;  // A row of this lane
     // RC_BF16: the LDS fragments and scales (after the transpose buffers and
     // the cross-wave sums)
@@ -183,50 +196,83 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         }
         issue_fence();
     }
+    // Staged scales (single segment, fragment input): the block's weight
+    // scales for this part's NQ quads in 8-byte pieces (piece c = row c % 8RB
+    // of quad c / 8RB) and the part's activation scales in 16-byte pieces,
+    // one or two loads per thread instead of a load per lane, tile and quad
+    // (those small loads, queued ahead of every wave's weights: down shape
+    // M = 4 9.4 -> 9.1 us, M = 16 10.0 -> 9.7 us).  Rows past the block read
+    // as zero.  Not for RC_BF16: its staging stores would wait for the weight
+    // scales from HBM before the rows' quantize (M = 8 7.5 -> 8.0 us); not
+    // for Q5/Q6, whose high-plane loads follow (8 rows: 8.5 / 8.7 -> 9.1 /
+    // 9.3 us).  (Forming the products ws * xs here, before the weights
+    // arrive, took 32-48 more VGPRs: the K split lost its second workgroup
+    // per CU.)
+    constexpr bool STG = ONE && AM == RC_FRAG && FM::HQ == 0;
+    constexpr int R8 = 8 * RB;
+    constexpr int SI = (R8 * QW + 63) / 64;  // pieces per thread: 8RB * NQ <= 8RB * W * QW
+    uint8_t* wsl = smem + rc_lds_bytes(FM::HSTR, RB, W);
+    uint8_t* xsl = wsl + (size_t)16 * T * NQ * 8;
+    u32x2 stw[STG ? SI : 1];
+    u32x4 stx = {0u, 0u, 0u, 0u};
+    if constexpr (STG) {
+        const auto wst = buf(ws + (size_t)row0 * NG, (uint32_t)(nrows * NG) * 2);
+#pragma unroll
+        for (int i = 0; i < SI; ++i) {
+            const int c = tid + NTT * i, q = c / R8, r = c - q * R8;
+            stw[i] = bload8(wst, q < NQ ? (r * NG + 4 * (q0 + q)) * 2 : OOB);
+        }
+        stx = bload16(xsr, tid < NQ * 16 ? tid * 16 : OOB);
+    }
 
     auto load = [&](Seg& S, int seg) {
 #pragma unroll
         for (int j = 0; j < QW; ++j) {
+            // a wave past the part's last quad loads nothing: its resources
+            // are empty (sizes chosen by a uniform condition), which needs no
+            // per-lane select or branch around the loads
             const int Q = wave + W * (seg * QW + j);
             const bool ok = Q < NQ;
+            const auto xrj = buf(xp, ok ? xn : 0u), xsrj = buf(xsp, ok ? xsn : 0u), srj = buf(sp0, ok ? sn : 0u);
 #pragma unroll
             for (int h = 0; h < 4 && !XBF; ++h) {
                 const int g = 4 * Q + h;
                 int ao;
-                if constexpr (XNAT) ao = (ok && m_ok) ? n16 * K + g * G + FM::QB * qi : OOB;
-                else ao = (ok && m_ok) ? (g * 64 + L) * FM::QB : OOB;
+                if constexpr (XNAT) ao = m_ok ? n16 * K + g * G + FM::QB * qi : OOB;
+                else ao = m_ok ? (g * 64 + L) * FM::QB : OOB;
                 if constexpr (FM::QB == 16) {
-                    S.A[j][h] = bload16(xr, ao);
+                    S.A[j][h] = bload16(xrj, ao);
                 } else {
-                    const u32x2 v = bload8(xr, ao);
+                    const u32x2 v = bload8(xrj, ao);
                     S.A[j][h] = u32x4{v.x, v.y, 0u, 0u};
                 }
                 if constexpr (XNAT) {
                     uint32_t v[4];
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        v[r] = bload4(xsr, (ok && 4 * kb + r < M) ? ((4 * kb + r) * NG + g) * 4 : OOB);
+                    for (int r = 0; r < 4; ++r) v[r] = bload4(xsrj, 4 * kb + r < M ? ((4 * kb + r) * NG + g) * 4 : OOB);
                     S.XS[j][h] = u32x4{v[0], v[1], v[2], v[3]};
-                } else {
-                    S.XS[j][h] = bload16(xsr, ok ? (g * 16 + 4 * kb) * 4 : OOB);
+                } else if constexpr (!STG) {
+                    S.XS[j][h] = bload16(xsrj, (g * 16 + 4 * kb) * 4);
                 }
             }
+            if constexpr (!STG)
 #pragma unroll
-            for (int t = 0; t < T; ++t) S.S[j][t] = bload8(sr, ok ? ((16 * t + n16) * NG + 4 * Q) * 2 : OOB);
+                for (int t = 0; t < T; ++t) S.S[j][t] = bload8(srj, ((16 * t + n16) * NG + 4 * Q) * 2);
         }
         issue_fence();
 #pragma unroll
         for (int j = 0; j < QW; ++j) {
             const int Q = wave + W * (seg * QW + j);
             const bool ok = Q < NQ;
+            const auto wrj = buf(wp, ok ? wn : 0u), hrj = buf(hp, ok ? hn : 0u);
 #pragma unroll
             for (int b = 0; b < RB; ++b) {
                 const int rw = 8 * b + (L >> 3);
-                S.WV[j][b] = bload16<AUX_NT>(wr, ok ? rw * rbytes + (8 * Q + (L & 7)) * 16 : OOB);
+                S.WV[j][b] = bload16<AUX_NT>(wrj, rw * rbytes + (8 * Q + (L & 7)) * 16);
                 if constexpr (FM::HQ == 32) {
-                    S.HV[j][b][0] = bload4<AUX_NT>(hr, ok ? rw * hrb + Q * 32 + (L & 7) * 4 : OOB);
+                    S.HV[j][b][0] = bload4<AUX_NT>(hrj, rw * hrb + Q * 32 + (L & 7) * 4);
                 } else if constexpr (FM::HQ == 64) {
-                    const u32x2 hh = bload8<AUX_NT>(hr, ok ? rw * hrb + Q * 64 + (L & 7) * 8 : OOB);
+                    const u32x2 hh = bload8<AUX_NT>(hrj, rw * hrb + Q * 64 + (L & 7) * 8);
                     S.HV[j][b][0] = hh.x;
                     S.HV[j][b][1] = hh.y;
                 }
@@ -397,7 +443,29 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     if constexpr (ONE) {
         Seg S;
         load(S, 0);
+        if constexpr (STG) {
+            issue_fence();  // the weight requests stay ahead of the staging stores
+#pragma unroll
+            for (int i = 0; i < SI; ++i) {
+                const int c = tid + NTT * i, q = c / R8, r = c - q * R8;
+                if (q < NQ) *(u32x2*)(wsl + (r * NQ + q) * 8) = stw[i];
+            }
+            if (tid < NQ * 16) *(u32x4*)(xsl + tid * 16) = stx;
+            lds_barrier();
+        }
         if constexpr (XBF) quantize();
+        if constexpr (STG) {
+#pragma unroll
+            for (int j = 0; j < QW; ++j) {
+                const int Q = wave + W * j;
+                if (Q < NQ) {
+#pragma unroll
+                    for (int t = 0; t < T; ++t) S.S[j][t] = *(const u32x2*)(wsl + ((16 * t + n16) * NQ + Q) * 8);
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) S.XS[j][h] = *(const u32x4*)(xsl + ((4 * Q + h) * 16 + 4 * kb) * 4);
+                }
+            }
+        }
         compute(S, 0);
     } else {
         Seg S0, S1;

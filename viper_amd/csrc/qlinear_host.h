@@ -48,7 +48,8 @@ inline int validate_weights(int qtype, const void* w, const void* s, int senc, i
     if (N <= 0 || K <= 0 || M <= 0 || M > VIPER_QLINEAR_MAX_M) return VIPER_INVALID_ARGUMENT;
     if (K % G != 0) return VIPER_INVALID_ARGUMENT;
     if ((int64_t)M * K > INT32_MAX / 2) return VIPER_INVALID_ARGUMENT;
-    if (misaligned(w, 16) || misaligned(s, 2)) return VIPER_INVALID_ARGUMENT;
+    // the kernels read scales in 8- and 16-byte loads (a workgroup's scale block at once)
+    if (misaligned(w, 16) || misaligned(s, 16)) return VIPER_INVALID_ARGUMENT;
     return VIPER_OK;
 }
 
