@@ -605,10 +605,15 @@ constexpr int M1_SHAPES[][3] = {{8, 128, 10}, {8, 192, 10}, {8, 320, 10}, {16, 2
                                 {32, 320, 10}, {32, 640, 10}, {64, 640, 10}, {16, 256, 5}, {16, 320, 5},
                                 {16, 640, 5}, {32, 640, 5}, {64, 640, 5}};
 
+// A shape of 5 chunk slots per lane is only ever an exact tiling (m1_shape
+// picks those by TS * CPL == chunks per row, and every such K tiles exactly;
+// rows that do not tile take 10 slots), so its non-exact variants are not
+// built.
 template <int F, int SENC, int MODE, bool EXACT, int PRO, int MR>
 m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
 #define VQ_M1(TS_, NTT_, CPL_)                                                                      \
-    if constexpr ((MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_)) && (MR == 1 || m1_mr_shape_ok(TS_, NTT_, CPL_))) \
+    if constexpr ((EXACT || CPL_ == 10) && (MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_)) &&          \
+                  (MR == 1 || m1_mr_shape_ok(TS_, NTT_, CPL_)))                                     \
         if (ts == TS_ && ntt == NTT_ && cpl == CPL_)                                                \
             return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, MR,                          \
                                    m1_delay<F>(EXACT, TS_, NTT_, CPL_, MODE, MR, PRO)>;
