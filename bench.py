@@ -285,6 +285,75 @@ def time_config3(torch, stk, fused, replays=10):
     return round(ms * 1e3, 1), round(nbytes / (ms * 1e-3) / 1e9, 1), launches
 
 
+def time_mlp(torch, L, gen, qtype=4, G=64, forms=("ref", "2launch")):
+    """Config 1 (M = 1 MLP: gate+up K=2560 -> 2x10240, SwiGLU, down K=10240 -> 2560, all Q4_G64, weights
+    rotating over >= 512 MB): the reference's launch sequence (fused2 gate/up, swiglu + quantize,
+    prequantized down + residual) and the 2-launch form (gate/up pair with the swiglu epilogue, down
+    quantizing h in its prologue + residual).  Returns {line: value} for the forms asked for."""
+    N, K = 10240, 2560
+    extras = {}
+    H, I = 2560, 10240
+    step_bytes = 3 * (N * K // 2 + N * (K // G) * 2)
+    mcopies = max(2, -(-ROTATE_BYTES // step_bytes) + 1)
+    Wg, Sg = make_weights(torch, mcopies, I, H, gen)
+    Wu, Su = make_weights(torch, mcopies, I, H, gen)
+    Wdn, Sdn = make_weights(torch, mcopies, H, I, gen)
+    xm = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
+    rm = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
+    gm = torch.empty((1, I), dtype=torch.bfloat16, device="cuda")
+    um = torch.empty((1, I), dtype=torch.bfloat16, device="cuda")
+    ym = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
+    xqm = torch.empty((1, I), dtype=torch.int8, device="cuda")
+    xsm = torch.empty((1, I // G), dtype=torch.float32, device="cuda")
+
+    def launch_mlp(i):
+        c = i % mcopies
+        st = torch.cuda.current_stream().cuda_stream
+        rc = L.viper_hip_qlinear_fused2(qtype, Wg[c].data_ptr(), Sg[c].data_ptr(), Wu[c].data_ptr(),
+                                        Su[c].data_ptr(), 0, G, I, H, xm.data_ptr(), 1, gm.data_ptr(),
+                                        um.data_ptr(), None, 0, st)
+        rc = rc or L.viper_hip_swiglu_quantize(gm.data_ptr(), um.data_ptr(), 1, I, G, gm.data_ptr(),
+                                               xqm.data_ptr(), xsm.data_ptr(), st)
+        rc = rc or L.viper_hip_qlinear_prequantized(qtype, Wdn[c].data_ptr(), Sdn[c].data_ptr(), 0, G, H, I,
+                                                    xqm.data_ptr(), xsm.data_ptr(), 1, ym.data_ptr(),
+                                                    rm.data_ptr(), st)
+        if rc != 0:
+            raise RuntimeError(f"MLP step failed: {rc}")
+    if "ref" in forms:
+        for i in range(20):
+            launch_mlp(i)
+        mlp_us = time_steps(torch, launch_mlp, 200)
+    # weights + scales of the three matrices, x and the residual in, gate/up
+    # out and back in, int8 activation + scales out and back in, y out
+    mlp_bytes = (step_bytes + H * 2 * 2 + 2 * I * 2 * 2 + (I + I // G * 4) * 2 + H * 2)
+    if "ref" in forms:
+        extras["mlp_config1_us"] = round(mlp_us, 3)
+        extras["mlp_config1_gbs"] = round(mlp_bytes / (mlp_us * 1e-6) / 1e9, 1)
+
+    # the same MLP in 2 launches: gate/up pair with the swiglu epilogue (h bf16), then
+    # down + residual quantizing h in its prologue
+    def launch_mlp2(i):
+        c = i % mcopies
+        st = torch.cuda.current_stream().cuda_stream
+        rc = L.viper_hip_qlinear_m1_swiglu(qtype, 0, G, H, 0, xm.data_ptr(), None, 0.0, None,
+                                           Wg[c].data_ptr(), Sg[c].data_ptr(), Wu[c].data_ptr(),
+                                           Su[c].data_ptr(), I, gm.data_ptr(), None, None, st)
+        rc = rc or L.viper_hip_qlinear(qtype, Wdn[c].data_ptr(), Sdn[c].data_ptr(), 0, G, H, I, gm.data_ptr(),
+                                       1, ym.data_ptr(), rm.data_ptr(), None, 0, st)
+        if rc != 0:
+            raise RuntimeError(f"MLP (2 launches) failed: {rc}")
+    if "2launch" in forms:
+        for i in range(20):
+            launch_mlp2(i)
+        mlp2_us = time_steps(torch, launch_mlp2, 200)
+        # weights + scales, x and the residual in, h out and back in, y out
+        mlp2_bytes = step_bytes + H * 2 * 2 + I * 2 * 2 + H * 2
+        extras["mlp_config1_2launch_us"] = round(mlp2_us, 3)
+        extras["mlp_config1_2launch_gbs"] = round(mlp2_bytes / (mlp2_us * 1e-6) / 1e9, 1)
+    del Wg, Sg, Wu, Su, Wdn, Sdn
+    return extras
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -303,8 +372,8 @@ def main():
                     help="only the per-wave timeline of the north-star GEMV (viper_hip_qlinear_timeline)")
     ap.add_argument("--only", default="", metavar="LINE",
                     help="only one line (rocprofv3 runs): config0, down, verify_mM (K=2560 N=10240) or "
-                         "verify_mM_down (K=10240 N=2560), q5_m1 / q6_m8 / w8_m1 ... (config 4), "
-                         "config3 (fused step) or config3_ref (reference launch sequence)")
+                         "verify_mM_down (K=10240 N=2560), q5_m1 / q6_m8 / w8_m1 ... (config 4), config1 / "
+                         "config1_2launch (MLP), config3 (fused step) or config3_ref (reference launch sequence)")
     ap.add_argument("--verify-only", type=int, default=0, metavar="M",
                     help="only time the M-row verify (K=2560, N=10240) line (rocprofv3 runs)")
     args = ap.parse_args()
@@ -347,6 +416,10 @@ def main():
             fmt, mpart = one.split("_m")
             qt = {"q5": 5, "q6": 6, "w8": 8}[fmt]
             res = time_linear(torch, L, gen, qt, N, K, int(mpart), steps=args.steps, outliers=True)
+        elif one in ("config1", "config1_2launch"):
+            r = time_mlp(torch, L, gen, qtype, G, ("ref",) if one == "config1" else ("2launch",))
+            key = "mlp_config1_us" if one == "config1" else "mlp_config1_2launch_us"
+            res = (r[key], r[key.replace("_us", "_gbs")])
         elif one in ("config3", "config3_ref"):
             from viper_amd.stack import Stack
             us, gbs, _ = time_config3(torch, Stack(torch), one == "config3", replays=max(10, args.steps // 100))
@@ -497,62 +570,7 @@ def main():
 
         # config 1: gate+up (one fused2 launch, K=2560, N=2x10240) -> swiglu +
         # quantize -> down (K=10240, N=2560) + residual; one step = 3 launches
-        H, I = 2560, 10240
-        step_bytes = 3 * (N * K // 2 + N * (K // G) * 2)
-        mcopies = max(2, -(-ROTATE_BYTES // step_bytes) + 1)
-        Wg, Sg = make_weights(torch, mcopies, I, H, gen)
-        Wu, Su = make_weights(torch, mcopies, I, H, gen)
-        Wdn, Sdn = make_weights(torch, mcopies, H, I, gen)
-        xm = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
-        rm = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
-        gm = torch.empty((1, I), dtype=torch.bfloat16, device="cuda")
-        um = torch.empty((1, I), dtype=torch.bfloat16, device="cuda")
-        ym = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
-        xqm = torch.empty((1, I), dtype=torch.int8, device="cuda")
-        xsm = torch.empty((1, I // G), dtype=torch.float32, device="cuda")
-
-        def launch_mlp(i):
-            c = i % mcopies
-            st = torch.cuda.current_stream().cuda_stream
-            rc = L.viper_hip_qlinear_fused2(qtype, Wg[c].data_ptr(), Sg[c].data_ptr(), Wu[c].data_ptr(),
-                                            Su[c].data_ptr(), 0, G, I, H, xm.data_ptr(), 1, gm.data_ptr(),
-                                            um.data_ptr(), None, 0, st)
-            rc = rc or L.viper_hip_swiglu_quantize(gm.data_ptr(), um.data_ptr(), 1, I, G, gm.data_ptr(),
-                                                   xqm.data_ptr(), xsm.data_ptr(), st)
-            rc = rc or L.viper_hip_qlinear_prequantized(qtype, Wdn[c].data_ptr(), Sdn[c].data_ptr(), 0, G, H, I,
-                                                        xqm.data_ptr(), xsm.data_ptr(), 1, ym.data_ptr(),
-                                                        rm.data_ptr(), st)
-            if rc != 0:
-                raise RuntimeError(f"MLP step failed: {rc}")
-        for i in range(20):
-            launch_mlp(i)
-        mlp_us = time_steps(torch, launch_mlp, 200)
-        # weights + scales of the three matrices, x and the residual in, gate/up
-        # out and back in, int8 activation + scales out and back in, y out
-        mlp_bytes = (step_bytes + H * 2 * 2 + 2 * I * 2 * 2 + (I + I // G * 4) * 2 + H * 2)
-        extras["mlp_config1_us"] = round(mlp_us, 3)
-        extras["mlp_config1_gbs"] = round(mlp_bytes / (mlp_us * 1e-6) / 1e9, 1)
-
-        # the same MLP in 2 launches: gate/up pair with the swiglu epilogue (h bf16), then
-        # down + residual quantizing h in its prologue
-        def launch_mlp2(i):
-            c = i % mcopies
-            st = torch.cuda.current_stream().cuda_stream
-            rc = L.viper_hip_qlinear_m1_swiglu(qtype, 0, G, H, 0, xm.data_ptr(), None, 0.0, None,
-                                               Wg[c].data_ptr(), Sg[c].data_ptr(), Wu[c].data_ptr(),
-                                               Su[c].data_ptr(), I, gm.data_ptr(), None, None, st)
-            rc = rc or L.viper_hip_qlinear(qtype, Wdn[c].data_ptr(), Sdn[c].data_ptr(), 0, G, H, I, gm.data_ptr(),
-                                           1, ym.data_ptr(), rm.data_ptr(), None, 0, st)
-            if rc != 0:
-                raise RuntimeError(f"MLP (2 launches) failed: {rc}")
-        for i in range(20):
-            launch_mlp2(i)
-        mlp2_us = time_steps(torch, launch_mlp2, 200)
-        # weights + scales, x and the residual in, h out and back in, y out
-        mlp2_bytes = step_bytes + H * 2 * 2 + I * 2 * 2 + H * 2
-        extras["mlp_config1_2launch_us"] = round(mlp2_us, 3)
-        extras["mlp_config1_2launch_gbs"] = round(mlp2_bytes / (mlp2_us * 1e-6) / 1e9, 1)
-        del Wg, Sg, Wu, Su, Wdn, Sdn
+        extras.update(time_mlp(torch, L, gen, qtype, G))
 
         # LM head (config 3's head): bf16 GEMV K=2560, N=166144 (850 MB, larger
         # than the MALL, so one copy streams from HBM every call) + greedy argmax
