@@ -374,6 +374,18 @@ def test_q4_rowcontig_shapes(torch_dev, N, K, M):
     run_case(torch_dev, O.Q4_G64, N, K, M, seed=5000 + K + M, residual=(M % 2 == 0))
 
 
+# Staged scales with two loads per thread (W8 with two quads per wave and 40
+# or 48 rows per workgroup: the only shapes whose weight-scale block has more
+# 8-byte pieces than the workgroup has threads): the unsplit M = 16 launch at
+# the north-star shape and the K split with 48-row blocks, with and without
+# the partials output (separate kernel variants).
+@pytest.mark.parametrize("N,K,M", [(10240, 2560, 16), (6000, 10240, 9)])
+@pytest.mark.parametrize("partials", [True, False])
+def test_w8_staged_scales_two_loads_per_thread(torch_dev, N, K, M, partials):
+    run_case(torch_dev, O.W8_G32, N, K, M, seed=7100 + M, scale_enc=O.SCALE_BF16, residual=True,
+             check_partials=partials)
+
+
 def test_verify_m16_full_size(torch_dev):
     # config 2: M=16 speculative verify at the north-star shape
     run_case(torch_dev, O.Q4_G64, 10240, 2560, 16, seed=0x5EED0002)
