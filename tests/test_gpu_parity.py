@@ -560,6 +560,31 @@ def test_fused2_matches_two_calls(torch_dev):
         np.testing.assert_array_equal(a.cpu().numpy(), b.cpu().numpy())
 
 
+@pytest.mark.parametrize("N,K,M", [(10240, 2560, 1), (1000, 2560, 16), (2560, 10240, 4), (640, 2560, 5)])
+def test_output_and_residual_two_byte_aligned(torch_dev, N, K, M):
+    # y and the residual need only 2-byte alignment: one element off a 16-byte
+    # boundary gives the same bits as aligned buffers (M = 1, the matrix-core
+    # kernel from fragments, the K split, the one-launch bf16-row path)
+    torch = torch_dev
+    packed, scales = O.gen_weights(O.Q4_G64, N, K, 91 + M, O.SCALE_FP16)
+    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K, scale_enc=va.ScaleEnc.FP16)
+    x = dev(torch, O.gen_act(M, K, 92))
+    res = O.gen_act(M, N, 93)
+    ws = torch.zeros(max(16, va.workspace_bytes(4, N, K, M)), dtype=torch.uint8, device="cuda") if M > 1 else None
+    ya = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    ra = dev(torch, res)
+    yb_buf = torch.zeros(M * N + 1, dtype=torch.int16, device="cuda")
+    rb_buf = torch.zeros(M * N + 1, dtype=torch.int16, device="cuda")
+    rb_buf[1:] = ra.view(-1)
+    yb, rb = yb_buf[1:].view(M, N), rb_buf[1:].view(M, N)
+    assert yb.data_ptr() % 16 == 2 and rb.data_ptr() % 16 == 2
+    assert va.linear(w, x, ya, residual=ra, workspace=ws).ok()
+    assert va.linear(w, x, yb, residual=rb, workspace=ws).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(ya.cpu().numpy(), yb.cpu().numpy())
+    assert int(yb_buf[0].item()) == 0  # nothing written before the output
+
+
 @pytest.mark.parametrize("M", [1, 3])
 def test_residual_in_place(torch_dev, M):
     # y aliasing the residual, as the reference engine calls its residual GEMV
