@@ -243,6 +243,35 @@ def test_k_split_alternating_inputs(torch_dev):
         O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
 
 
+def test_k_split_two_streams_concurrent(torch_dev):
+    # two K-split calls in flight at once on two streams (default priority),
+    # each with its own workspace: every result equals its single-stream one
+    # bit for bit (no exchange crosses workspaces, no spin runs out)
+    torch = torch_dev
+    qtype, N, K = O.Q4_G64, 2560, 10240
+    cases = []
+    for M, seed in ((4, 5700), (16, 5710)):
+        packed, scales = O.gen_weights(qtype, N, K, seed, O.SCALE_FP16)
+        w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, 64,
+                               va.ScaleEnc(O.SCALE_FP16))
+        x = dev(torch, O.gen_act(M, K, seed + 1))
+        ws = torch.full((va.workspace_bytes(qtype, N, K, M),), 255, dtype=torch.uint8, device="cuda")
+        y0 = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+        assert va.linear(w, x, y0, workspace=ws).ok()
+        cases.append((w, x, ws, y0))
+    outs = [[torch.zeros_like(c[3]) for _ in range(10)] for c in cases]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for i in range(10):
+        for (w, x, ws, _), s, o in zip(cases, streams, outs):
+            assert va.linear(w, x, o[i], workspace=ws, stream=s).ok()
+    torch.cuda.synchronize()
+    for (_, _, _, y0), o in zip(cases, outs):
+        ref = y0.cpu().numpy()
+        for t in o:
+            np.testing.assert_array_equal(t.cpu().numpy(), ref)
+
+
 # BASELINE config 2 as stated: M in {2, 4, 8, 16} at both shapes, full size,
 # int32 group dots bit-exact and bf16 within the bar.
 @pytest.mark.parametrize("M", [2, 4, 8, 16])
