@@ -179,3 +179,26 @@ def test_sampling_greedy_split_across_workgroups(torch_dev):
         np.testing.assert_array_equal(out[:rows].cpu().numpy(), e)
         assert int(w.count_nonzero()) == 0
 
+
+def test_sampling_greedy_split_two_streams_concurrent(torch_dev):
+    # two split greedy picks in flight at once on two streams (default
+    # priority), each with its own workspace, called repeatedly: every token
+    # equals the oracle's argmax and each workspace is zero afterwards
+    torch = torch_dev
+    V, B = 166144, 3
+    rng = np.random.default_rng(7)
+    lgs = [bf16(rng.standard_normal((B, V)).astype(np.float32)) for _ in range(2)]
+    expect = [O.argmax_bf16(lg) for lg in lgs]
+    lds = [dev(torch, lg) for lg in lgs]
+    wss = [ws(torch, B, True) for _ in range(2)]
+    outs = [[torch.full((B,), -1, dtype=torch.int32, device="cuda") for _ in range(8)] for _ in range(2)]
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    torch.cuda.synchronize()
+    for i in range(8):
+        for k in range(2):
+            assert va.sampling_greedy(lds[k], outs[k][i], stream=streams[k], workspace=wss[k]).ok()
+    torch.cuda.synchronize()
+    for k in range(2):
+        for o in outs[k]:
+            np.testing.assert_array_equal(o.cpu().numpy(), expect[k])
+        assert int(wss[k].sum().item()) == 0
