@@ -109,7 +109,8 @@ extern "C" {
 #define VIPER_SCALE_BF16 1
 
 #define VIPER_QLINEAR_MAX_M 16
-#define VIPER_QLINEAR_ABI_VERSION 4
+/* 5: weight scales must be 16-byte aligned (4 accepted 2-byte aligned scales) */
+#define VIPER_QLINEAR_ABI_VERSION 5
 
 int viper_hip_abi_version(void);
 

@@ -28,7 +28,7 @@ def test_header_symbols_exported():
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(ql._SYMBOLS)
-    assert L.viper_hip_abi_version() == 4
+    assert L.viper_hip_abi_version() == 5
 
 
 def test_group_sizes_and_workspace():
