@@ -114,3 +114,11 @@ def test_registry_mirror():
         "BF16", "FP32", "Q4_G64", "Q5_G64", "Q6_G64", "W8_G32", "UNKNOWN"]
     assert va.is_lossless(0) and va.is_lossless(1) and not va.is_lossless(4)
     assert va.packed_bytes(va.QType.Q5_G64, 2, 64) == 2 * 32 + 2 * 8
+
+
+def test_wrapper_rejects_host_tensors():
+    # a CPU tensor's address would reach the kernels as a device address
+    torch = pytest.importorskip("torch")
+    with pytest.raises(ValueError):
+        ql.ptr(torch.zeros(4))
+    assert ql.ptr(None) is None

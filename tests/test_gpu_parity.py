@@ -632,6 +632,19 @@ def test_residual_in_place(torch_dev, M):
     O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
 
 
+def test_wrapper_rejects_non_contiguous(torch_dev):
+    # a strided view would be read as a dense array: the wrapper refuses it
+    torch = torch_dev
+    N, K = 64, 128
+    packed, scales = O.gen_weights(O.Q4_G64, N, K, 61, O.SCALE_FP16)
+    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K, scale_enc=va.ScaleEnc.FP16)
+    xt = torch.zeros((K, 2), dtype=torch.int16, device="cuda").t()
+    assert not xt.is_contiguous()
+    with pytest.raises(ValueError):
+        va.linear(w, xt, torch.zeros((2, N), dtype=torch.int16, device="cuda"),
+                  workspace=torch.zeros(va.workspace_bytes(4, N, K, 2), dtype=torch.uint8, device="cuda"))
+
+
 def test_zero_weight_kat(torch_dev):
     # all-0x88 Q4 bytes are all-zero weights: y is exactly the residual
     torch = torch_dev

@@ -197,9 +197,15 @@ def lib():
 
 
 def ptr(t) -> Optional[int]:
-    """Device address of a torch tensor (None stays None)."""
+    """Device address of a torch tensor (None stays None).  The kernels read and write every tensor as a
+    dense array in device memory, so a CPU tensor (a host address on the GPU) or a non-contiguous view
+    (read as if dense) raises ValueError instead of reaching the C ABI."""
     if t is None:
         return None
+    if not t.is_cuda:
+        raise ValueError("viper_amd: tensor arguments must be GPU tensors")
+    if not t.is_contiguous():
+        raise ValueError("viper_amd: tensor arguments must be contiguous")
     return t.data_ptr()
 
 
