@@ -196,16 +196,20 @@ def lib():
     return L
 
 
-def ptr(t) -> Optional[int]:
+def ptr(t, itemsize: Optional[int] = None) -> Optional[int]:
     """Device address of a torch tensor (None stays None).  The kernels read and write every tensor as a
-    dense array in device memory, so a CPU tensor (a host address on the GPU) or a non-contiguous view
-    (read as if dense) raises ValueError instead of reaching the C ABI."""
+    dense array of fixed-size elements in device memory, so a CPU tensor (a host address on the GPU), a
+    non-contiguous view (read as if dense) or elements of another size than the argument's (itemsize:
+    1 for packed weights and int8 activations, 2 for bf16 data and 16-bit scales, 4 for fp32 scales and
+    int32 outputs) raise ValueError instead of reaching the C ABI."""
     if t is None:
         return None
     if not t.is_cuda:
         raise ValueError("viper_amd: tensor arguments must be GPU tensors")
     if not t.is_contiguous():
         raise ValueError("viper_amd: tensor arguments must be contiguous")
+    if itemsize is not None and t.element_size() != itemsize:
+        raise ValueError(f"viper_amd: expected {itemsize}-byte elements, got {t.dtype}")
     return t.data_ptr()
 
 
@@ -260,8 +264,8 @@ def linear(w: QuantizedWeight, x, y, residual=None, workspace=None, stream=None)
     if residual is not None and residual.numel() != M * N:
         return Status(StatusCode.SHAPE_MISMATCH, "linear: residual shape")
     ws_ptr, ws_n = (None, 0) if workspace is None else (ptr(workspace), workspace.numel() * workspace.element_size())
-    rc = lib().viper_hip_qlinear(int(w.qtype), ptr(w.data), ptr(w.scales), int(w.scale_enc), w.group_size,
-                                 N, K, ptr(x), M, ptr(y), ptr(residual), ws_ptr, ws_n, _stream(stream))
+    rc = lib().viper_hip_qlinear(int(w.qtype), ptr(w.data, 1), ptr(w.scales, 2), int(w.scale_enc), w.group_size,
+                                 N, K, ptr(x, 2), M, ptr(y, 2), ptr(residual, 2), ws_ptr, ws_n, _stream(stream))
     return _status(rc, "viper_hip_qlinear")
 
 
@@ -269,24 +273,24 @@ def linear_partials(w: QuantizedWeight, x, y, partials, residual=None, workspace
     K, N = w.cols, w.rows
     M = _shape_mk(x, K)
     ws_ptr, ws_n = (None, 0) if workspace is None else (ptr(workspace), workspace.numel() * workspace.element_size())
-    rc = lib().viper_hip_qlinear_partials(int(w.qtype), ptr(w.data), ptr(w.scales), int(w.scale_enc),
-                                          w.group_size, N, K, ptr(x), M, ptr(y), ptr(residual), ws_ptr, ws_n,
-                                          ptr(partials), _stream(stream))
+    rc = lib().viper_hip_qlinear_partials(int(w.qtype), ptr(w.data, 1), ptr(w.scales, 2), int(w.scale_enc),
+                                          w.group_size, N, K, ptr(x, 2), M, ptr(y, 2), ptr(residual, 2), ws_ptr, ws_n,
+                                          ptr(partials, 4), _stream(stream))
     return _status(rc, "viper_hip_qlinear_partials")
 
 
 def quantize_act(x, group, xq, xs, stream=None) -> Status:
     K = xq.shape[-1]
     M = int(xq.numel() // K)
-    rc = lib().viper_hip_quantize_act(group, ptr(x), M, K, ptr(xq), ptr(xs), _stream(stream))
+    rc = lib().viper_hip_quantize_act(group, ptr(x, 2), M, K, ptr(xq, 1), ptr(xs, 4), _stream(stream))
     return _status(rc, "viper_hip_quantize_act")
 
 
 def linear_prequantized(w: QuantizedWeight, xq, xs, y, residual=None, stream=None) -> Status:
     K, N = w.cols, w.rows
     M = int(xq.numel() // K)
-    rc = lib().viper_hip_qlinear_prequantized(int(w.qtype), ptr(w.data), ptr(w.scales), int(w.scale_enc),
-                                              w.group_size, N, K, ptr(xq), ptr(xs), M, ptr(y), ptr(residual),
+    rc = lib().viper_hip_qlinear_prequantized(int(w.qtype), ptr(w.data, 1), ptr(w.scales, 2), int(w.scale_enc),
+                                              w.group_size, N, K, ptr(xq, 1), ptr(xs, 4), M, ptr(y, 2), ptr(residual, 2),
                                               _stream(stream))
     return _status(rc, "viper_hip_qlinear_prequantized")
 
@@ -303,8 +307,8 @@ def linear_fused2(w0: QuantizedWeight, w1: QuantizedWeight, x, y0, y1, workspace
     K, N = w0.cols, w0.rows
     M = _shape_mk(x, K)
     ws_ptr, ws_n = (None, 0) if workspace is None else (ptr(workspace), workspace.numel() * workspace.element_size())
-    rc = lib().viper_hip_qlinear_fused2(int(w0.qtype), ptr(w0.data), ptr(w0.scales), ptr(w1.data), ptr(w1.scales),
-                                        int(w0.scale_enc), w0.group_size, N, K, ptr(x), M, ptr(y0), ptr(y1),
+    rc = lib().viper_hip_qlinear_fused2(int(w0.qtype), ptr(w0.data, 1), ptr(w0.scales, 2), ptr(w1.data, 1), ptr(w1.scales, 2),
+                                        int(w0.scale_enc), w0.group_size, N, K, ptr(x, 2), M, ptr(y0, 2), ptr(y1, 2),
                                         ws_ptr, ws_n, _stream(stream))
     return _status(rc, "viper_hip_qlinear_fused2")
 
@@ -314,9 +318,9 @@ def linear_fused2_prequantized(w0: QuantizedWeight, w1: QuantizedWeight, xq, xs,
         return Status(StatusCode.SHAPE_MISMATCH, "linear_fused2: the two weights differ in kind or shape")
     K, N = w0.cols, w0.rows
     M = int(xq.numel() // K)
-    rc = lib().viper_hip_qlinear_fused2_prequantized(int(w0.qtype), ptr(w0.data), ptr(w0.scales), ptr(w1.data),
-                                                     ptr(w1.scales), int(w0.scale_enc), w0.group_size, N, K,
-                                                     ptr(xq), ptr(xs), M, ptr(y0), ptr(y1), _stream(stream))
+    rc = lib().viper_hip_qlinear_fused2_prequantized(int(w0.qtype), ptr(w0.data, 1), ptr(w0.scales, 2), ptr(w1.data, 1),
+                                                     ptr(w1.scales, 2), int(w0.scale_enc), w0.group_size, N, K,
+                                                     ptr(xq, 1), ptr(xs, 4), M, ptr(y0, 2), ptr(y1, 2), _stream(stream))
     return _status(rc, "viper_hip_qlinear_fused2_prequantized")
 
 
@@ -324,8 +328,8 @@ def rmsnorm_quantize(x, gamma, eps, group, xq, xs, out=None, stream=None) -> Sta
     """xq/xs (and out, bf16) from rmsnorm(x) * gamma, per row of x [M, H]."""
     H = gamma.numel()
     M = int(x.numel() // H)
-    rc = lib().viper_hip_rmsnorm_quantize(ptr(x), ptr(gamma), float(eps), M, H, group, ptr(out), ptr(xq),
-                                          ptr(xs), _stream(stream))
+    rc = lib().viper_hip_rmsnorm_quantize(ptr(x, 2), ptr(gamma, 2), float(eps), M, H, group, ptr(out, 2), ptr(xq, 1),
+                                          ptr(xs, 4), _stream(stream))
     return _status(rc, "viper_hip_rmsnorm_quantize")
 
 
@@ -333,7 +337,7 @@ def swiglu_quantize(gate, up, group, xq, xs, out=None, stream=None) -> Status:
     """xq/xs (and out, bf16; may be gate itself) from silu(gate) * up, rows of [M, I]."""
     I = gate.shape[-1]
     M = int(gate.numel() // I)
-    rc = lib().viper_hip_swiglu_quantize(ptr(gate), ptr(up), M, I, group, ptr(out), ptr(xq), ptr(xs),
+    rc = lib().viper_hip_swiglu_quantize(ptr(gate, 2), ptr(up, 2), M, I, group, ptr(out, 2), ptr(xq, 1), ptr(xs, 4),
                                          _stream(stream))
     return _status(rc, "viper_hip_swiglu_quantize")
 
@@ -358,10 +362,10 @@ def linear_m1(ws, prologue, a, b, ys, eps=0.0, norm_out=None, residual=None, str
         return Status(StatusCode.SHAPE_MISMATCH, "linear_m1: weights differ in kind or K")
     arr = lambda vals: (C.c_void_p * n)(*vals)
     rc = lib().viper_hip_qlinear_m1(int(w0.qtype), int(w0.scale_enc), w0.group_size, w0.cols, int(prologue),
-                                    ptr(a), ptr(b), float(eps), ptr(norm_out), n,
-                                    arr([ptr(w.data) for w in ws]), arr([ptr(w.scales) for w in ws]),
-                                    (C.c_int * n)(*[w.rows for w in ws]), arr([ptr(y) for y in ys]),
-                                    ptr(residual), _stream(stream))
+                                    ptr(a, 1 if int(prologue) == int(Prologue.INT8) else 2), ptr(b, 4 if int(prologue) == int(Prologue.INT8) else 2), float(eps), ptr(norm_out, 2), n,
+                                    arr([ptr(w.data, 1) for w in ws]), arr([ptr(w.scales, 2) for w in ws]),
+                                    (C.c_int * n)(*[w.rows for w in ws]), arr([ptr(y, 2) for y in ys]),
+                                    ptr(residual, 2), _stream(stream))
     return _status(rc, "viper_hip_qlinear_m1")
 
 
@@ -374,9 +378,9 @@ def linear_m1_swiglu(w_gate, w_up, prologue, a, b, h, eps=0.0, norm_out=None, ga
             (w_up.qtype, w_up.rows, w_up.cols, w_up.group_size, w_up.scale_enc):
         return Status(StatusCode.SHAPE_MISMATCH, "linear_m1_swiglu: gate and up differ in kind or shape")
     rc = lib().viper_hip_qlinear_m1_swiglu(int(w_gate.qtype), int(w_gate.scale_enc), w_gate.group_size, w_gate.cols,
-                                           int(prologue), ptr(a), ptr(b), float(eps), ptr(norm_out),
-                                           ptr(w_gate.data), ptr(w_gate.scales), ptr(w_up.data), ptr(w_up.scales),
-                                           w_gate.rows, ptr(h), ptr(gate_out), ptr(up_out), _stream(stream))
+                                           int(prologue), ptr(a, 1 if int(prologue) == int(Prologue.INT8) else 2), ptr(b, 4 if int(prologue) == int(Prologue.INT8) else 2), float(eps), ptr(norm_out, 2),
+                                           ptr(w_gate.data, 1), ptr(w_gate.scales, 2), ptr(w_up.data, 1), ptr(w_up.scales, 2),
+                                           w_gate.rows, ptr(h, 2), ptr(gate_out, 2), ptr(up_out, 2), _stream(stream))
     return _status(rc, "viper_hip_qlinear_m1_swiglu")
 
 
@@ -384,7 +388,7 @@ def linear_bf16(w, x, y, stream=None) -> Status:
     """y[M, N] = x[M, K] w[N, K]^T, all bf16 (the LM head)."""
     N, K = w.shape
     M = int(x.numel() // K)
-    rc = lib().viper_hip_linear_bf16(ptr(w), ptr(x), ptr(y), M, N, K, _stream(stream))
+    rc = lib().viper_hip_linear_bf16(ptr(w, 2), ptr(x, 2), ptr(y, 2), M, N, K, _stream(stream))
     return _status(rc, "viper_hip_linear_bf16")
 
 
@@ -396,10 +400,10 @@ def sampling_greedy(logits, out_token, stream=None, workspace=None) -> Status:
     B = int(logits.numel() // V)
     if workspace is not None:
         nbytes = workspace.numel() * workspace.element_size()
-        rc = lib().viper_hip_sampling_greedy_split(ptr(logits), ptr(out_token), B, V, ptr(workspace), nbytes,
+        rc = lib().viper_hip_sampling_greedy_split(ptr(logits, 2), ptr(out_token, 4), B, V, ptr(workspace), nbytes,
                                                    _stream(stream))
         return _status(rc, "viper_hip_sampling_greedy_split")
-    rc = lib().viper_hip_sampling_greedy(ptr(logits), ptr(out_token), B, V, _stream(stream))
+    rc = lib().viper_hip_sampling_greedy(ptr(logits, 2), ptr(out_token, 4), B, V, _stream(stream))
     return _status(rc, "viper_hip_sampling_greedy")
 
 
