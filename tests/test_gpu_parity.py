@@ -643,6 +643,10 @@ def test_wrapper_rejects_non_contiguous(torch_dev):
     with pytest.raises(ValueError):
         va.linear(w, xt, torch.zeros((2, N), dtype=torch.int16, device="cuda"),
                   workspace=torch.zeros(va.workspace_bytes(4, N, K, 2), dtype=torch.uint8, device="cuda"))
+    # and an fp32 x, which would be read as pairs of bf16
+    with pytest.raises(ValueError):
+        va.linear(w, torch.zeros((1, K), dtype=torch.float32, device="cuda"),
+                  torch.zeros((1, N), dtype=torch.int16, device="cuda"))
 
 
 def test_zero_weight_kat(torch_dev):
