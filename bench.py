@@ -378,8 +378,9 @@ def main():
                     help="only time the M-row verify (K=2560, N=10240) line (rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the GEMV shards by output rows; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the GEMV would shard by "
+              "output rows, each GPU running the same kernel on its share of N). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
