@@ -54,7 +54,8 @@ def make_weights(torch, copies, N, K, gen, row_bytes=None, G=64):
     return w, s
 
 
-# bytes per weight row and group size of each format (the layouts of DESIGN.md section 3)
+# bytes per weight row and group size of each format: Q4 K/2 nibbles; Q5/Q6 the nibble plane plus a
+# 1- or 2-bit high plane; W8 one byte per weight (the layouts viper_qlinear.h documents)
 ROW_BYTES = {4: lambda K: K // 2, 5: lambda K: K * 5 // 8, 6: lambda K: K * 6 // 8, 8: lambda K: K}
 GROUP = {4: 64, 5: 64, 6: 64, 8: 32}
 
