@@ -18,7 +18,7 @@ dispatch duration (us_per_gemv).  Every other line is timed over one graph of
 (same semantics, seeded inputs), timed on this host with 1 and all threads.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-       python bench.py --read-sweep | --timeline | --only LINE   (measurement modes)
+       python bench.py --read-sweep | --timeline [q4|q5|q6|w8] | --only LINE   (measurement modes)
 """
 import argparse
 import ctypes as C
@@ -222,13 +222,14 @@ def read_sweep(torch, L, gen):
     del pool
 
 
-def timeline(torch, L, gen, N, K):
-    """Per-wave timeline of the north-star GEMV: percentiles of each stamp over all waves of one
-    dispatch (the last of a back-to-back sequence over rotating weights), in us from the first wave's
-    start."""
-    copy_bytes = N * K // 2 + N * (K // 64) * 2
+def timeline(torch, L, gen, N, K, qt=4):
+    """Per-wave timeline of the M=1 GEMV of format qt at the north-star shape: percentiles of each
+    stamp over all waves of one dispatch (the last of a back-to-back sequence over rotating weights),
+    in us from the first wave's start."""
+    G = GROUP[qt]
+    copy_bytes = N * ROW_BYTES[qt](K) + N * (K // G) * 2
     copies = max(2, -(-ROTATE_BYTES // copy_bytes) + 1)
-    W, S = make_weights(torch, copies, N, K, gen)
+    W, S = make_weights(torch, copies, N, K, gen, row_bytes=ROW_BYTES[qt](K), G=G)
     x = torch.randn((1, K), device="cuda", generator=gen).to(torch.bfloat16)
     y = torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
     stamps = torch.zeros(1 << 20, dtype=torch.int64, device="cuda")
@@ -237,7 +238,7 @@ def timeline(torch, L, gen, N, K):
     def launch(i):
         c = i % copies
         st = torch.cuda.current_stream().cuda_stream   # the capture stream while a graph is captured
-        rc = L.viper_hip_qlinear_timeline(4, W[c].data_ptr(), S[c].data_ptr(), 0, 64, N, K, x.data_ptr(),
+        rc = L.viper_hip_qlinear_timeline(qt, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K, x.data_ptr(),
                                           y.data_ptr(), stamps.data_ptr(), stamps.numel() * 8, C.byref(grid),
                                           C.byref(waves), st)
         if rc != 0:
@@ -258,7 +259,8 @@ def timeline(torch, L, gen, N, K):
     for i, nm in enumerate(names):
         v = np.sort(t[:, i])
         rows[nm] = [round(float(np.percentile(v, p)), 3) for p in (10, 50, 90)] + [round(float(v[-1]), 3)]
-    print(json.dumps({"timeline": "qgemv_m1 Q4_G64 K=2560 N=10240", "workgroups": grid.value,
+    name = {4: "Q4_G64", 5: "Q5_G64", 6: "Q6_G64", 8: "W8_G32"}[qt]
+    print(json.dumps({"timeline": f"qgemv_m1 {name} K={K} N={N}", "workgroups": grid.value,
                       "waves_per_workgroup": waves.value, "us_per_launch_stamped": round(us, 3),
                       "percentiles_us_p10_p50_p90_max": rows}), flush=True)
 
@@ -369,8 +371,9 @@ def main():
     ap.add_argument("--read-sweep", action="store_true",
                     help="only the streaming-read floor: launch shapes x sizes, fixed cost + bandwidth fit, and "
                          "the north-star I/O ladder (JSON lines)")
-    ap.add_argument("--timeline", action="store_true",
-                    help="only the per-wave timeline of the north-star GEMV (viper_hip_qlinear_timeline)")
+    ap.add_argument("--timeline", nargs="?", const="q4", default=None, choices=("q4", "q5", "q6", "w8"),
+                    help="only the per-wave timeline of the M=1 GEMV at the north-star shape, Q4_G64 unless a "
+                         "format is named (viper_hip_qlinear_timeline)")
     ap.add_argument("--only", default="", metavar="LINE",
                     help="only one line (rocprofv3 runs): config0, down, verify_mM (K=2560 N=10240) or "
                          "verify_mM_down (K=10240 N=2560), q5_m1 / q6_m8 / w8_m1 ... (config 4), config1 / "
@@ -434,7 +437,7 @@ def main():
         read_sweep(torch, L, gen)
         return
     if args.timeline:
-        timeline(torch, L, gen, N, K)
+        timeline(torch, L, gen, N, K, {"q4": 4, "q5": 5, "q6": 6, "w8": 8}[args.timeline])
         return
     if args.m16_only or args.verify_only:
         Mv = 16 if args.m16_only else args.verify_only

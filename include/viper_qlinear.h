@@ -270,8 +270,8 @@ int viper_hip_check_bf16_rounding(unsigned long long* count, void* stream);
 int viper_hip_check_quantizer(int exp_lo, int exp_hi, int32_t* counts, void* stream);
 
 /* Measurement entry point, no counterpart in the reference: the M = 1 GEMV
- * of viper_hip_qlinear (Q4_G64, bf16 x, launch shapes whose lanes tile a row
- * exactly, e.g. K = 2560) with a per-wave timeline.  Lane 0 of every wave
+ * of viper_hip_qlinear (any quantized format, bf16 x, launch shapes whose
+ * lanes tile a row exactly, e.g. K = 2560) with a per-wave timeline.  Lane 0 of every wave
  * writes 8 s_memrealtime readings (uint64, 100 MHz) to
  * stamps[(workgroup * waves + wave) * 8 + i]: wave start, activation and
  * weight-scale loads issued, weight loads issued, activation quantized into

@@ -784,15 +784,17 @@ def test_stream_read_probe(torch_dev):
         np.testing.assert_array_equal(got, np.arange(n // rb))
 
 
-def test_timeline_entry_matches_gemv(torch_dev):
+@pytest.mark.parametrize("qt", [O.Q4_G64, O.Q5_G64, O.Q6_G64, O.W8_G32])
+def test_timeline_entry_matches_gemv(torch_dev, qt):
     # the measurement entry point runs the production GEMV with stamps: y equal
     # to viper_hip_qlinear's bit for bit, 8 non-decreasing readings per wave,
-    # and shapes without an exact tiling (or another format) rejected
+    # and shapes without an exact tiling rejected
     import ctypes as C
     torch = torch_dev
     L = va.lib()
     N, K = 4000, 2560
-    packed, scales = O.gen_weights(O.Q4_G64, N, K, 0x71, O.SCALE_FP16)
+    G = 32 if qt == O.W8_G32 else 64
+    packed, scales = O.gen_weights(qt, N, K, 0x71, O.SCALE_FP16)
     x = O.gen_act(1, K, 0x72)
     wd, sd, xd = dev(torch, packed), dev(torch, scales), dev(torch, x)
     y0 = torch.zeros((1, N), dtype=torch.int16, device="cuda")
@@ -800,9 +802,9 @@ def test_timeline_entry_matches_gemv(torch_dev):
     stamps = torch.zeros(1 << 18, dtype=torch.int64, device="cuda")
     grid, waves = C.c_int(0), C.c_int(0)
     st = torch.cuda.current_stream().cuda_stream
-    assert L.viper_hip_qlinear(4, wd.data_ptr(), sd.data_ptr(), 0, 64, N, K, xd.data_ptr(), 1, y0.data_ptr(),
+    assert L.viper_hip_qlinear(qt, wd.data_ptr(), sd.data_ptr(), 0, G, N, K, xd.data_ptr(), 1, y0.data_ptr(),
                                None, None, 0, st) == 0
-    assert L.viper_hip_qlinear_timeline(4, wd.data_ptr(), sd.data_ptr(), 0, 64, N, K, xd.data_ptr(), y1.data_ptr(),
+    assert L.viper_hip_qlinear_timeline(qt, wd.data_ptr(), sd.data_ptr(), 0, G, N, K, xd.data_ptr(), y1.data_ptr(),
                                         stamps.data_ptr(), stamps.numel() * 8, C.byref(grid), C.byref(waves), st) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(y1, np.uint16), host(y0, np.uint16))
@@ -810,7 +812,7 @@ def test_timeline_entry_matches_gemv(torch_dev):
     assert nw > 0
     t = stamps[: nw * 8].view(nw, 8).cpu().numpy()
     assert (np.diff(t, axis=1) >= 0).all() and (t[:, 0] > 0).all()
-    assert L.viper_hip_qlinear_timeline(4, wd.data_ptr(), sd.data_ptr(), 0, 64, N, K, xd.data_ptr(), y1.data_ptr(),
+    assert L.viper_hip_qlinear_timeline(qt, wd.data_ptr(), sd.data_ptr(), 0, G, N, K, xd.data_ptr(), y1.data_ptr(),
                                         stamps.data_ptr(), 64, None, None, st) == 2          # stamps too small
-    assert L.viper_hip_qlinear_timeline(4, wd.data_ptr(), sd.data_ptr(), 0, 64, N, 2496, xd.data_ptr(),
+    assert L.viper_hip_qlinear_timeline(qt, wd.data_ptr(), sd.data_ptr(), 0, G, N, 2496, xd.data_ptr(),
                                         y1.data_ptr(), stamps.data_ptr(), stamps.numel() * 8, None, None, st) == 2

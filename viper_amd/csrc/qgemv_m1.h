@@ -652,8 +652,8 @@ m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, int mode, bool exact, int 
         }
     }
     if (mr != 1) return nullptr;
-    // the timeline: Q4, bf16 prologue, exact tilings
-    if constexpr (PRO == PRO_BF16 && F == 4)
+    // the timeline: bf16 prologue, exact tilings
+    if constexpr (PRO == PRO_BF16)
         if (mode == M1_TL)
             return !exact ? nullptr
                           : senc ? m1_kernel_v<F, 1, M1_TL, true, PRO, 1>(ts, ntt, cpl)

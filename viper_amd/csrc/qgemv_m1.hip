@@ -183,10 +183,10 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
 
 int launch_m1_timeline(int qtype, int senc, int K, const void* x, const void* w, const void* s, void* y, int N,
                        uint64_t* stamps, size_t stamp_bytes, int* workgroups, int* waves, hipStream_t st) {
-    if (qtype != VIPER_QTYPE_Q4_G64) return VIPER_INVALID_ARGUMENT;
+    const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32, group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
     const int noct = K / 8;
-    const M1Shape sh = m1_shape(K / 32, N, device_cus(), 0, noct);
-    if (sh.ntt == 0 || K != m1_exact_k<4>(sh.ts, sh.cpl) || (K / 64) % 8 != 0) return VIPER_INVALID_ARGUMENT;
+    const M1Shape sh = m1_shape(K / ck, N, device_cus(), 0, noct);
+    if (sh.ntt == 0 || K != ck * sh.ts * sh.cpl || (K / group) % 8 != 0) return VIPER_INVALID_ARGUMENT;
     const m1_fn fn = m1_kernel(qtype, sh, senc, M1_TL, true, PRO_BF16);
     if (fn == nullptr) return VIPER_INTERNAL;
     const int rows = sh.ntt / sh.ts;
