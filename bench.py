@@ -60,9 +60,11 @@ ROW_BYTES = {4: lambda K: K // 2, 5: lambda K: K * 5 // 8, 6: lambda K: K * 6 //
 GROUP = {4: 64, 5: 64, 6: 64, 8: 32}
 
 
-def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False):
+def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False, prequantized=False):
     """us per call of viper_hip_qlinear (bf16 x, fused or separate quantize) over rotating weights;
-    outliers: 5% of the activation channels (a fixed seeded set) scaled x20, as config 4 states."""
+    outliers: 5% of the activation channels (a fixed seeded set) scaled x20, as config 4 states;
+    prequantized: x quantized once (viper_hip_quantize_act) outside the timed calls, each call
+    viper_hip_qlinear_prequantized (int8 rows and their fp32 group scales in, bf16 y out)."""
     G = GROUP[qtype]
     rb = ROW_BYTES[qtype](K)
     copy_bytes = N * rb + N * (K // G) * 2
@@ -76,12 +78,22 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False):
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     nws = L.viper_hip_qlinear_workspace_bytes(qtype, N, K, M)
     ws = torch.empty(max(nws, 16), dtype=torch.uint8, device="cuda")
+    if prequantized:
+        xq = torch.empty(M * K, dtype=torch.int8, device="cuda")
+        xs = torch.empty(M * (K // G), dtype=torch.float32, device="cuda")
+        if L.viper_hip_quantize_act(G, x.data_ptr(), M, K, xq.data_ptr(), xs.data_ptr(),
+                                    torch.cuda.current_stream().cuda_stream) != 0:
+            raise RuntimeError("quantize_act failed")
 
     def launch(i):
         c = i % copies
-        rc = L.viper_hip_qlinear(qtype, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K, x.data_ptr(), M,
-                                 y.data_ptr(), None, ws.data_ptr() if nws else None, nws,
-                                 torch.cuda.current_stream().cuda_stream)
+        st = torch.cuda.current_stream().cuda_stream
+        if prequantized:
+            rc = L.viper_hip_qlinear_prequantized(qtype, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K,
+                                                  xq.data_ptr(), xs.data_ptr(), M, y.data_ptr(), None, st)
+        else:
+            rc = L.viper_hip_qlinear(qtype, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K, x.data_ptr(), M,
+                                     y.data_ptr(), None, ws.data_ptr() if nws else None, nws, st)
         if rc != 0:
             raise RuntimeError(f"qlinear qtype={qtype} N={N} K={K} M={M} failed: {rc}")
     for i in range(20):
@@ -89,6 +101,8 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False):
     us = time_steps(torch, launch, max(steps, MIN_STEPS))
     del W, S
     alg = algorithmic_bytes(rb, N, K, M, G)
+    if prequantized:  # int8 rows + fp32 group scales in place of the bf16 rows
+        alg += M * K + M * (K // G) * 4 - 2 * M * K
     return round(us, 3), round(alg / (us * 1e-6) / 1e9, 1)
 
 
@@ -376,7 +390,9 @@ def main():
                          "format is named (viper_hip_qlinear_timeline)")
     ap.add_argument("--only", default="", metavar="LINE",
                     help="only one line (rocprofv3 runs): config0, down, verify_mM (K=2560 N=10240) or "
-                         "verify_mM_down (K=10240 N=2560), q5_m1 / q6_m8 / w8_m1 ... (config 4), config1 / "
+                         "verify_mM_down (K=10240 N=2560), pre_mM[_down] (the same through the prequantized "
+                         "entry, x quantized once outside the timed calls), q5_m1 / q6_m8 / w8_m1 ... "
+                         "(config 4), config1 / "
                          "config1_2launch (MLP), config3 (fused step) or config3_ref (reference launch sequence)")
     ap.add_argument("--verify-only", type=int, default=0, metavar="M",
                     help="only time the M-row verify (K=2560, N=10240) line (rocprofv3 runs)")
@@ -413,10 +429,11 @@ def main():
             res = time_linear(torch, L, gen, qtype, 2560, 2560, 1, steps=args.steps)
         elif one == "down":
             res = time_linear(torch, L, gen, qtype, 2560, 10240, 1, steps=args.steps)
-        elif one.startswith("verify_m"):
-            Mv = int(one[len("verify_m"):].split("_")[0])
+        elif one.startswith("verify_m") or one.startswith("pre_m"):
+            Mv = int(one.split("_m")[1].split("_")[0])
             shape = (2560, 10240) if one.endswith("_down") else (10240, 2560)
-            res = time_linear(torch, L, gen, qtype, shape[0], shape[1], Mv, steps=args.steps)
+            res = time_linear(torch, L, gen, qtype, shape[0], shape[1], Mv, steps=args.steps,
+                              prequantized=one.startswith("pre_m"))
         elif one[:1] in "qw" and "_m" in one:
             fmt, mpart = one.split("_m")
             qt = {"q5": 5, "q6": 6, "w8": 8}[fmt]

@@ -39,7 +39,8 @@ namespace vq {
 constexpr int M1_XS = 4;    // activation octets per thread loaded before the weights
 constexpr int M1_XS_MR = 8; // the same for MR > 1 rows (all of them: no later rounds)
 constexpr int M1_DELAY = 6; // weight-issue delay, s_sleep units (one activation row)
-constexpr int M1_DELAY_MR = 8; // the same for MR > 1 rows (MR rows of activation ahead of the weights)
+constexpr int M1_DELAY_MR = 8; // the same for MR > 1 bf16 rows (MR rows of activation ahead of the weights)
+constexpr int M1_DELAY_ROUND = 4; // the same for MR > 1 int8 rows, per staging round of the rows
 constexpr int M1_DELAY_PAIR = 16; // the same for the gate/up pair (twice the weight stream per workgroup)
 constexpr int M1_DELAY_RMS = 3;   // the same for the rmsnorm prologue (q/k/v: 3.31 -> 3.23 us against 6)
 constexpr int M1_DELAY_WIDE = 10; // the same for a wide launch with the bf16 prologue (W8, K = 2560: 5.80 -> 5.71 us)
@@ -70,10 +71,18 @@ __host__ __device__ constexpr bool m1_wide(bool exact, int ts, int ntt, int cpl,
     return exact && mr * (m1_exact_k<F>(ts, cpl) / 8) <= ntt / 2;
 }
 
-// Weight-issue delay of a launch kind (s_sleep units).
+// Weight-issue delay of a launch kind (s_sleep units).  Int8 rows (MR > 1)
+// wait in proportion to their staging rounds (one 8-byte load per thread and
+// round, all issued before the weights): K = 10240, N = 2560 with 2 / 4 rows
+// (4 / 8 rounds) 5.9 / 8.2 us at 8 units against 5.1 / 7.6 us at 16 / 32;
+// K = 2560, N = 10240 with 2 / 4 rows on 320 threads (2 / 4 rounds) best at
+// 8 / 16.  The bf16 rows, which quantize what they load, are best at 8 in all
+// four cases.
 template <int F>
 __host__ __device__ constexpr int m1_delay(bool exact, int ts, int ntt, int cpl, int mode, int mr, int pro) {
     return mode == M1_SWIGLU                                   ? M1_DELAY_PAIR
+           : mr > 1 && pro == PRO_INT8
+               ? M1_DELAY_ROUND * (exact ? (mr * (m1_exact_k<F>(ts, cpl) / 8) + ntt - 1) / ntt : M1_XS_MR)
            : mr > 1                                            ? M1_DELAY_MR
            : pro == PRO_RMSNORM                                ? M1_DELAY_RMS
            : pro == PRO_BF16 && m1_wide<F>(exact, ts, ntt, cpl, mr) ? M1_DELAY_WIDE
@@ -342,12 +351,18 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // preceding every load of the wave.
     const int at = tid - A0;  // staging thread index (negative on the spare wave)
     const bool stager = !SPARE || __builtin_amdgcn_readfirstlane(tid) >= A0;  // wave-uniform
+    // int8 rows (MR > 1): every round is issued, the rounds past the rows
+    // reading zeros through the buffers' ranges (M * K bytes, M * K / G
+    // scales).  A branch per round (the row count is a run-time value) made
+    // the compiler wait for each load at the branch join and spill it to
+    // scratch: 20 us instead of 8.2 us at K = 10240 with 4 rows.
+    constexpr bool ALL_ROUNDS = PRE && MR > 1;
     u32x4 xv[XS], av[XS];
 #pragma unroll
     for (int i = 0; i < XS; ++i) {
         xv[i] = u32x4{0u, 0u, 0u, 0u};
         av[i] = xv[i];
-        if ((i == 0 || ANT * i < noct) && stager) {
+        if (ALL_ROUNDS || ((i == 0 || ANT * i < noct) && stager)) {
             if constexpr (PRE) {
                 const u32x2 q = bload8(xr, (at + ANT * i) * 8);
                 xv[i] = u32x4{q.x, q.y, 0u, 0u};
@@ -361,7 +376,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < XS; ++i) {
-            if ((i == 0 || ANT * i < noct) && stager) {
+            if (ALL_ROUNDS || ((i == 0 || ANT * i < noct) && stager)) {
                 const int o = at + ANT * i;
                 if constexpr (PRE) xv[i].z = bload4(xsr, (o % OPC == 0) ? (o / OPG) * 4 : OOB);
                 else av[i] = bload16(xsr, o * 16);
