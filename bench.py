@@ -389,7 +389,7 @@ def main():
                     help="only the per-wave timeline of the M=1 GEMV at the north-star shape, Q4_G64 unless a "
                          "format is named (viper_hip_qlinear_timeline)")
     ap.add_argument("--only", default="", metavar="LINE",
-                    help="only one line (rocprofv3 runs): config0, down, verify_mM (K=2560 N=10240) or "
+                    help="only one line (rocprofv3 runs): config0[_pre], down, verify_mM (K=2560 N=10240) or "
                          "verify_mM_down (K=10240 N=2560), pre_mM[_down] (the same through the prequantized "
                          "entry, x quantized once outside the timed calls), q5_m1 / q6_m8 / w8_m1 ... "
                          "(config 4), config1 / "
@@ -425,8 +425,9 @@ def main():
     qtype, G = int(va.QType.Q4_G64), 64
     if args.only:
         one = args.only
-        if one == "config0":
-            res = time_linear(torch, L, gen, qtype, 2560, 2560, 1, steps=args.steps)
+        if one in ("config0", "config0_pre"):
+            res = time_linear(torch, L, gen, qtype, 2560, 2560, 1, steps=args.steps,
+                              prequantized=one == "config0_pre")
         elif one == "down":
             res = time_linear(torch, L, gen, qtype, 2560, 10240, 1, steps=args.steps)
         elif one.startswith("verify_m") or one.startswith("pre_m"):

@@ -41,6 +41,11 @@ constexpr int M1_XS_MR = 8; // the same for MR > 1 rows (all of them: no later r
 constexpr int M1_DELAY = 6; // weight-issue delay, s_sleep units (one activation row)
 constexpr int M1_DELAY_MR = 8; // the same for MR > 1 bf16 rows (MR rows of activation ahead of the weights)
 constexpr int M1_DELAY_ROUND = 4; // the same for MR > 1 int8 rows, per staging round of the rows
+// the same for one int8 row on an exact tiling, by workgroup size: 256 threads
+// (K = N = 2560: 2.60 -> 2.50 us against 6) and 640 threads (K = 10240,
+// N = 2560: 4.41 -> 4.18 us); 320 threads (K = 2560, N = 10240) is best at 6
+constexpr int M1_DELAY_INT8_256 = 2;
+constexpr int M1_DELAY_INT8_640 = 8;
 constexpr int M1_DELAY_PAIR = 16; // the same for the gate/up pair (twice the weight stream per workgroup)
 constexpr int M1_DELAY_RMS = 3;   // the same for the rmsnorm prologue (q/k/v: 3.31 -> 3.23 us against 6)
 constexpr int M1_DELAY_WIDE = 10; // the same for a wide launch with the bf16 prologue (W8, K = 2560: 5.80 -> 5.71 us)
@@ -84,6 +89,8 @@ __host__ __device__ constexpr int m1_delay(bool exact, int ts, int ntt, int cpl,
            : mr > 1 && pro == PRO_INT8
                ? M1_DELAY_ROUND * (exact ? (mr * (m1_exact_k<F>(ts, cpl) / 8) + ntt - 1) / ntt : M1_XS_MR)
            : mr > 1                                            ? M1_DELAY_MR
+           : pro == PRO_INT8 && exact && ntt == 256            ? M1_DELAY_INT8_256
+           : pro == PRO_INT8 && exact && ntt == 640            ? M1_DELAY_INT8_640
            : pro == PRO_RMSNORM                                ? M1_DELAY_RMS
            : pro == PRO_BF16 && m1_wide<F>(exact, ts, ntt, cpl, mr) ? M1_DELAY_WIDE
                                                                : M1_DELAY;
