@@ -506,7 +506,7 @@ def test_bf16_rows_match_prequantized(torch_dev, qtype, N, K, M):
 
 
 @pytest.mark.parametrize("N,K,M", [(200, 2560, 3), (70, 10240, 16), (40, 192, 2), (6001, 4096, 16), (45, 10240, 4),
-                                   (300, 10240, 3), (130, 7680, 2)])
+                                   (300, 10240, 3), (130, 7680, 2), (90, 7680, 3), (90, 7680, 4)])
 def test_prequantized_entry(torch_dev, N, K, M):
     # activations in viper_hip_quantize_act's layout ([M][K] int8, [M][K/G] fp32)
     torch = torch_dev
