@@ -563,6 +563,14 @@ def main():
         us_v, gbs_v = time_linear(torch, L, gen, qtype, 2560, 2560, 1)
         extras["config0_us"], extras["config0_gbs"] = us_v, gbs_v
 
+        # the prequantized entry (the reference engine's dp4a_smem_gemv call sites: int8 rows quantized
+        # by the producer kernel): M=1 at the three shapes, 2-4 rows at the down shape
+        for nm, (Nq, Kq), Mv in (("pre_config0", (2560, 2560), 1), ("pre_m1", (N, K), 1),
+                                 ("pre_m1_down", (2560, 10240), 1), ("pre_m2_down", (2560, 10240), 2),
+                                 ("pre_m3_down", (2560, 10240), 3), ("pre_m4_down", (2560, 10240), 4)):
+            us_v, gbs_v = time_linear(torch, L, gen, qtype, Nq, Kq, Mv, prequantized=True)
+            extras[f"{nm}_us"], extras[f"{nm}_gbs"] = us_v, gbs_v
+
         # config 4: Q5_G64, Q6_G64 and W8_G32 at M=1 and M=8, K=2560, N=10240
         for qt, nm in ((5, "q5"), (6, "q6"), (8, "w8")):
             for Mv in (1, 8):
