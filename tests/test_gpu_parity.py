@@ -526,9 +526,11 @@ def test_prequantized_entry(torch_dev, N, K, M):
 
 
 @pytest.mark.parametrize("qtype", FORMATS)
-@pytest.mark.parametrize("N,K", [(2560, 2560), (61, 10240)])
+@pytest.mark.parametrize("N,K", [(2560, 2560), (61, 10240), (10240, 2560), (10010, 2560)])
 def test_prequantized_m1(torch_dev, qtype, N, K):
     # M = 1 from int8 activations: the M = 1 kernel's prequantized prologue
+    # (one octet per thread on 256 threads; Q4's two octets per thread on 320
+    # and 640, a ragged last workgroup at N = 10010)
     torch = torch_dev
     G = O.group_size(qtype)
     packed, scales = O.gen_weights(qtype, N, K, 50 + qtype, O.SCALE_FP16)
@@ -546,7 +548,7 @@ def test_prequantized_m1(torch_dev, qtype, N, K):
 # fused2 for k/v and gate/up): M = 1 (fused quantize), M > 1 (matrix cores),
 # K with an odd group count (two v_dot4 launches).
 @pytest.mark.parametrize("qtype", FORMATS)
-@pytest.mark.parametrize("N,K,M", [(300, 2560, 1), (70, 2560, 16), (90, 2560, 6), (33, 192, 3)])
+@pytest.mark.parametrize("N,K,M", [(300, 2560, 1), (5120, 2560, 1), (70, 2560, 16), (90, 2560, 6), (33, 192, 3)])
 @pytest.mark.parametrize("prequantized", [False, True])
 def test_fused2(torch_dev, qtype, N, K, M, prequantized):
     torch = torch_dev

@@ -43,9 +43,11 @@ constexpr int M1_DELAY_MR = 8; // the same for MR > 1 bf16 rows (MR rows of acti
 constexpr int M1_DELAY_ROUND = 4; // the same for MR > 1 int8 rows, per staging round of the rows
 // the same for one int8 row on an exact tiling, by workgroup size: 256 threads
 // (K = N = 2560: 2.60 -> 2.50 us against 6) and 640 threads (K = 10240,
-// N = 2560: 4.41 -> 4.18 us); 320 threads (K = 2560, N = 10240) is best at 6
+// N = 2560: 4.41 -> 4.18 us; Q4's two-octet staging 4.09 us at 4); 320
+// threads (K = 2560, N = 10240) is best at 6 either way
 constexpr int M1_DELAY_INT8_256 = 2;
 constexpr int M1_DELAY_INT8_640 = 8;
+constexpr int M1_DELAY_PAIR8_640 = 4;
 constexpr int M1_DELAY_PAIR = 16; // the same for the gate/up pair (twice the weight stream per workgroup)
 constexpr int M1_DELAY_RMS = 3;   // the same for the rmsnorm prologue (q/k/v: 3.31 -> 3.23 us against 6)
 constexpr int M1_DELAY_WIDE = 10; // the same for a wide launch with the bf16 prologue (W8, K = 2560: 5.80 -> 5.71 us)
@@ -90,7 +92,7 @@ __host__ __device__ constexpr int m1_delay(bool exact, int ts, int ntt, int cpl,
                ? M1_DELAY_ROUND * (exact ? (mr * (m1_exact_k<F>(ts, cpl) / 8) + ntt - 1) / ntt : M1_XS_MR)
            : mr > 1                                            ? M1_DELAY_MR
            : pro == PRO_INT8 && exact && ntt == 256            ? M1_DELAY_INT8_256
-           : pro == PRO_INT8 && exact && ntt == 640            ? M1_DELAY_INT8_640
+           : pro == PRO_INT8 && exact && ntt == 640            ? (F == 4 ? M1_DELAY_PAIR8_640 : M1_DELAY_INT8_640)
            : pro == PRO_RMSNORM                                ? M1_DELAY_RMS
            : pro == PRO_BF16 && m1_wide<F>(exact, ts, ntt, cpl, mr) ? M1_DELAY_WIDE
                                                                : M1_DELAY;
@@ -268,7 +270,16 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
                             (MODE == M1_SWIGLU && (PRO == PRO_BF16 || (PRO == PRO_RMSNORM && KX / 8 <= NTT - 64))));
     constexpr int A0 = SPARE ? 64 : 0;  // first staging thread
     constexpr int ANT = NTT - A0;       // staging threads
-    constexpr int XS = EXACT ? (MR * (KX / 8) + ANT - 1) / ANT : MR > 1 ? M1_XS_MR : M1_XS;
+    // Q4 from one int8 row on 320 or 640 threads (PAIR8): each staging thread
+    // takes two octets with one 16-byte load and stores them with one 16-byte
+    // LDS write, a chunk's two lanes summing its correction; the waves past the
+    // row's K/16 pairs stage nothing and issue their weights at once.  Bit for
+    // bit the same LDS row as one octet per thread; K = 2560, N = 10240 4.06 ->
+    // 3.84 us, K = 10240, N = 2560 4.19 -> 4.09 us; on 256 threads (K = N =
+    // 2560) one octet per thread stays faster (2.54 against 2.64 us).
+    constexpr bool PAIR8 = PRE && MR == 1 && EXACT && F == 4 && !SPARE && (NTT == 320 || NTT == 640);
+    constexpr int XS = PAIR8 ? (KX / 16 + ANT - 1) / ANT
+                       : EXACT ? (MR * (KX / 8) + ANT - 1) / ANT : MR > 1 ? M1_XS_MR : M1_XS;
     constexpr int ROWS = NTT / TS;
     const int M = MR == 1 ? 1 : e1;  // activation rows
     constexpr int HB = FT::HIW * 4;  // high-plane bytes per chunk: Q5 4, Q6 8
@@ -357,7 +368,8 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // wait for its argument load then follows these requests instead of
     // preceding every load of the wave.
     const int at = tid - A0;  // staging thread index (negative on the spare wave)
-    const bool stager = !SPARE || __builtin_amdgcn_readfirstlane(tid) >= A0;  // wave-uniform
+    const bool stager = PAIR8 ? (__builtin_amdgcn_readfirstlane(tid) & ~63) < KX / 16
+                              : (!SPARE || __builtin_amdgcn_readfirstlane(tid) >= A0);  // wave-uniform
     // int8 rows (MR > 1): every round is issued, the rounds past the rows
     // reading zeros through the buffers' ranges (M * K bytes, M * K / G
     // scales).  A branch per round (the row count is a run-time value) made
@@ -370,7 +382,9 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         xv[i] = u32x4{0u, 0u, 0u, 0u};
         av[i] = xv[i];
         if (ALL_ROUNDS || ((i == 0 || ANT * i < noct) && stager)) {
-            if constexpr (PRE) {
+            if constexpr (PAIR8) {
+                xv[i] = bload16(xr, (at + ANT * i) * 16);  // octets 2p, 2p + 1
+            } else if constexpr (PRE) {
                 const u32x2 q = bload8(xr, (at + ANT * i) * 8);
                 xv[i] = u32x4{q.x, q.y, 0u, 0u};
             } else {
@@ -385,7 +399,8 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         for (int i = 0; i < XS; ++i) {
             if (ALL_ROUNDS || ((i == 0 || ANT * i < noct) && stager)) {
                 const int o = at + ANT * i;
-                if constexpr (PRE) xv[i].z = bload4(xsr, (o % OPC == 0) ? (o / OPG) * 4 : OOB);
+                if constexpr (PAIR8) av[i].x = bload4(xsr, ((2 * o) % OPC == 0) ? ((2 * o) / OPG) * 4 : OOB);
+                else if constexpr (PRE) xv[i].z = bload4(xsr, (o % OPC == 0) ? (o / OPG) * 4 : OOB);
                 else av[i] = bload16(xsr, o * 16);
             }
         }
@@ -513,7 +528,22 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     const int wave0 = (tid & ~63) - A0;  // waves with no octet skip the quantize
 #pragma unroll
     for (int i = 0; i < XS; ++i) {
-        if (i < xiters && wave0 + ANT * i < noct && stager) {
+        if constexpr (PAIR8) {
+            // pair p = octets 2p, 2p + 1 as (ql, qh) nibble words; the chunk
+            // (4 octets) is lanes 2c, 2c + 1, its scale loaded by the even one
+            const int p = at + ANT * i;
+            if (wave0 + ANT * i < KX / 16 && stager) {
+                const u32x4 v = xv[i];
+                const uint32_t ql0 = nibbles8(v.x, v.y), qh0 = nibbles8(v.x >> 4, v.y >> 4);
+                const uint32_t ql1 = nibbles8(v.z, v.w), qh1 = nibbles8(v.z >> 4, v.w >> 4);
+                int cs = (int)udot8(ql0, 0x11111111u, 0u) + (int)udot8(ql1, 0x11111111u, 0u);
+                cs += dpp_i<DPP_SWAP1>(cs);
+                if (p < KX / 16) {
+                    *(u32x4*)(lxq + (size_t)p * 16) = u32x4{ql0, qh0, ql1, qh1};
+                    if ((p & 1) == 0) lcs[p >> 1] = u32x2{(uint32_t)(-8 * cs), av[i].x};
+                }
+            }
+        } else if (i < xiters && wave0 + ANT * i < noct && stager) {
             if constexpr (TWO) {
                 const int o = at + ANT * i;
                 const u32x4 v = produce(xv[i], av[i]);
@@ -525,7 +555,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             }
         }
     }
-    if constexpr (!TWO && MR == 1) {
+    if constexpr (!TWO && MR == 1 && !PAIR8) {
         if (__builtin_expect(xiters > XS, 0))
             for (int i = XS; i < xiters; ++i)
                 if (stager && wave0 + ANT * i < noct) quant_store(at + ANT * i, load_x(at + ANT * i));
