@@ -58,6 +58,11 @@ constexpr int M1_DELAY_WIDE = 10; // the same for a wide launch with the bf16 pr
 // the north-star launch, placed before the weight loads).
 template <int F>
 __host__ __device__ constexpr int m1_exact_k(int ts, int cpl) { return Fmt<F>::CK * ts * cpl; }
+__host__ __device__ constexpr int m1_max(int a, int b) { return a > b ? a : b; }
+// Activation bytes (int8) a staging thread loads per round for int8 rows: 16
+// for Q4 on 320 or 640 threads (two octets), else 8.
+template <int F>
+__host__ __device__ constexpr int m1_row_bytes(int ntt) { return F == 4 && (ntt == 320 || ntt == 640) ? 16 : 8; }
 
 // Kernel modes: plain, with the int32 group dots (test entry point), or the
 // gate/up pair with the swiglu epilogue (M1_SWIGLU): the first NTT/2 threads
@@ -80,16 +85,18 @@ __host__ __device__ constexpr bool m1_wide(bool exact, int ts, int ntt, int cpl,
 
 // Weight-issue delay of a launch kind (s_sleep units).  Int8 rows (MR > 1)
 // wait in proportion to their staging rounds (one 8-byte load per thread and
-// round, all issued before the weights): K = 10240, N = 2560 with 2 / 4 rows
-// (4 / 8 rounds) 5.9 / 8.2 us at 8 units against 5.1 / 7.6 us at 16 / 32;
-// K = 2560, N = 10240 with 2 / 4 rows on 320 threads (2 / 4 rounds) best at
-// 8 / 16.  The bf16 rows, which quantize what they load, are best at 8 in all
-// four cases.
+// round, or 16 bytes for Q4's two-octet staging; all issued before the
+// weights), at least 2: K = 10240, N = 2560 with 2 / 4 rows (4 / 8 rounds)
+// 5.9 / 8.2 us at 8 units against 5.1 / 7.6 us at 16 / 32; K = 2560, N = 10240
+// with 2 / 4 rows on 320 threads (2 / 4 rounds) best at 8 / 16; Q4's pairs (1,
+// 2 or 4 rounds) best at 8, 8 and 16.  The bf16 rows, which quantize what
+// they load, are best at 8 in all four cases.
 template <int F>
 __host__ __device__ constexpr int m1_delay(bool exact, int ts, int ntt, int cpl, int mode, int mr, int pro) {
     return mode == M1_SWIGLU                                   ? M1_DELAY_PAIR
            : mr > 1 && pro == PRO_INT8
-               ? M1_DELAY_ROUND * (exact ? (mr * (m1_exact_k<F>(ts, cpl) / 8) + ntt - 1) / ntt : M1_XS_MR)
+               ? M1_DELAY_ROUND * (exact ? m1_max(2, (mr * (m1_exact_k<F>(ts, cpl) / m1_row_bytes<F>(ntt)) + ntt - 1) / ntt)
+                                         : M1_XS_MR)
            : mr > 1                                            ? M1_DELAY_MR
            : pro == PRO_INT8 && exact && ntt == 256            ? M1_DELAY_INT8_256
            : pro == PRO_INT8 && exact && ntt == 640            ? (F == 4 ? M1_DELAY_PAIR8_640 : M1_DELAY_INT8_640)
@@ -270,15 +277,17 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
                             (MODE == M1_SWIGLU && (PRO == PRO_BF16 || (PRO == PRO_RMSNORM && KX / 8 <= NTT - 64))));
     constexpr int A0 = SPARE ? 64 : 0;  // first staging thread
     constexpr int ANT = NTT - A0;       // staging threads
-    // Q4 from one int8 row on 320 or 640 threads (PAIR8): each staging thread
+    // Q4 from int8 rows on 320 or 640 threads (PAIR8): each staging thread
     // takes two octets with one 16-byte load and stores them with one 16-byte
-    // LDS write, a chunk's two lanes summing its correction; the waves past the
-    // row's K/16 pairs stage nothing and issue their weights at once.  Bit for
-    // bit the same LDS row as one octet per thread; K = 2560, N = 10240 4.06 ->
-    // 3.84 us, K = 10240, N = 2560 4.19 -> 4.09 us; on 256 threads (K = N =
-    // 2560) one octet per thread stays faster (2.54 against 2.64 us).
-    constexpr bool PAIR8 = PRE && MR == 1 && EXACT && F == 4 && !SPARE && (NTT == 320 || NTT == 640);
-    constexpr int XS = PAIR8 ? (KX / 16 + ANT - 1) / ANT
+    // LDS write, a chunk's two lanes summing its correction; with one row the
+    // waves past its K/16 pairs stage nothing and issue their weights at once.
+    // Bit for bit the same LDS rows as one octet per thread.  One row: K =
+    // 2560, N = 10240 4.06 -> 3.84 us, K = 10240, N = 2560 4.19 -> 4.09 us; 2 /
+    // 3 / 4 rows at K = 10240: 5.17 / 7.3 / 7.6 -> 4.85 / 6.55 / 6.85 us; on 256
+    // threads (K = N = 2560, one row) one octet per thread stays faster (2.54
+    // against 2.64 us).
+    constexpr bool PAIR8 = PRE && EXACT && F == 4 && !SPARE && (NTT == 320 || NTT == 640);
+    constexpr int XS = PAIR8 ? (MR * (KX / 16) + ANT - 1) / ANT
                        : EXACT ? (MR * (KX / 8) + ANT - 1) / ANT : MR > 1 ? M1_XS_MR : M1_XS;
     constexpr int ROWS = NTT / TS;
     const int M = MR == 1 ? 1 : e1;  // activation rows
@@ -368,8 +377,8 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // wait for its argument load then follows these requests instead of
     // preceding every load of the wave.
     const int at = tid - A0;  // staging thread index (negative on the spare wave)
-    const bool stager = PAIR8 ? (__builtin_amdgcn_readfirstlane(tid) & ~63) < KX / 16
-                              : (!SPARE || __builtin_amdgcn_readfirstlane(tid) >= A0);  // wave-uniform
+    const bool stager = PAIR8 && MR == 1 ? (__builtin_amdgcn_readfirstlane(tid) & ~63) < KX / 16
+                                         : (!SPARE || __builtin_amdgcn_readfirstlane(tid) >= A0);  // wave-uniform
     // int8 rows (MR > 1): every round is issued, the rounds past the rows
     // reading zeros through the buffers' ranges (M * K bytes, M * K / G
     // scales).  A branch per round (the row count is a run-time value) made
@@ -532,13 +541,14 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             // pair p = octets 2p, 2p + 1 as (ql, qh) nibble words; the chunk
             // (4 octets) is lanes 2c, 2c + 1, its scale loaded by the even one
             const int p = at + ANT * i;
-            if (wave0 + ANT * i < KX / 16 && stager) {
+            const int npair = MR == 1 ? KX / 16 : M * (K / 16);  // pairs of all rows
+            if (wave0 + ANT * i < npair && stager) {
                 const u32x4 v = xv[i];
                 const uint32_t ql0 = nibbles8(v.x, v.y), qh0 = nibbles8(v.x >> 4, v.y >> 4);
                 const uint32_t ql1 = nibbles8(v.z, v.w), qh1 = nibbles8(v.z >> 4, v.w >> 4);
                 int cs = (int)udot8(ql0, 0x11111111u, 0u) + (int)udot8(ql1, 0x11111111u, 0u);
                 cs += dpp_i<DPP_SWAP1>(cs);
-                if (p < KX / 16) {
+                if (p < npair) {
                     *(u32x4*)(lxq + (size_t)p * 16) = u32x4{ql0, qh0, ql1, qh1};
                     if ((p & 1) == 0) lcs[p >> 1] = u32x2{(uint32_t)(-8 * cs), av[i].x};
                 }
