@@ -271,7 +271,14 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // squares covers the same octets as without the spare wave and the row's
     // sum (wave sums in wave order, the spare wave's 0 first) is unchanged
     // bit for bit.
-    constexpr bool SPARE = EXACT && MR == 1 &&
+    // Q4 from one bf16 row on 256 threads (PAIRBF): each staging thread loads
+    // and quantizes two octets (16 values; the group's amax over its 4 lanes,
+    // the same maximum as over 8 lanes of one octet), so 160 threads stage a
+    // K = 2560 row and the fourth wave issues its weights at once; no spare
+    // wave.  The same LDS row bit for bit; K = N = 2560 2.51 -> 2.45 us (320
+    // threads, K = 2560, and 640, K = 10240: equal either way).
+    constexpr bool PAIRBF = PRO == PRO_BF16 && MODE == M1_PLAIN && MR == 1 && EXACT && F == 4 && NTT == 256;
+    constexpr bool SPARE = !PAIRBF && EXACT && MR == 1 &&
                            ((PRO == PRO_BF16 && MODE != M1_SWIGLU &&
                              (NTT == 256 || NTT == 320 || m1_wide<F>(EXACT, TS, NTT, CPL, MR))) ||
                             (MODE == M1_SWIGLU && (PRO == PRO_BF16 || (PRO == PRO_RMSNORM && KX / 8 <= NTT - 64))));
@@ -287,7 +294,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // threads (K = N = 2560, one row) one octet per thread stays faster (2.54
     // against 2.64 us).
     constexpr bool PAIR8 = PRE && EXACT && F == 4 && !SPARE && (NTT == 320 || NTT == 640);
-    constexpr int XS = PAIR8 ? (MR * (KX / 16) + ANT - 1) / ANT
+    constexpr int XS = (PAIR8 || PAIRBF) ? (MR * (KX / 16) + ANT - 1) / ANT
                        : EXACT ? (MR * (KX / 8) + ANT - 1) / ANT : MR > 1 ? M1_XS_MR : M1_XS;
     constexpr int ROWS = NTT / TS;
     const int M = MR == 1 ? 1 : e1;  // activation rows
@@ -377,7 +384,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // wait for its argument load then follows these requests instead of
     // preceding every load of the wave.
     const int at = tid - A0;  // staging thread index (negative on the spare wave)
-    const bool stager = PAIR8 && MR == 1 ? (__builtin_amdgcn_readfirstlane(tid) & ~63) < KX / 16
+    const bool stager = (PAIR8 || PAIRBF) && MR == 1 ? (__builtin_amdgcn_readfirstlane(tid) & ~63) < KX / 16
                                          : (!SPARE || __builtin_amdgcn_readfirstlane(tid) >= A0);  // wave-uniform
     // int8 rows (MR > 1): every round is issued, the rounds past the rows
     // reading zeros through the buffers' ranges (M * K bytes, M * K / G
@@ -391,7 +398,10 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         xv[i] = u32x4{0u, 0u, 0u, 0u};
         av[i] = xv[i];
         if (ALL_ROUNDS || ((i == 0 || ANT * i < noct) && stager)) {
-            if constexpr (PAIR8) {
+            if constexpr (PAIRBF) {  // octets 2p, 2p + 1 (bf16)
+                xv[i] = bload16(xr, (at + ANT * i) * 32);
+                av[i] = bload16(xr, (at + ANT * i) * 32 + 16);
+            } else if constexpr (PAIR8) {
                 xv[i] = bload16(xr, (at + ANT * i) * 16);  // octets 2p, 2p + 1
             } else if constexpr (PRE) {
                 const u32x2 q = bload8(xr, (at + ANT * i) * 8);
@@ -537,7 +547,22 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     const int wave0 = (tid & ~63) - A0;  // waves with no octet skip the quantize
 #pragma unroll
     for (int i = 0; i < XS; ++i) {
-        if constexpr (PAIR8) {
+        if constexpr (PAIRBF) {
+            const int p = at + ANT * i;
+            if (wave0 + ANT * i < KX / 16 && stager) {
+                uint32_t d0, d1, d2, d3;
+                float sc;
+                quantize_octet_pair<FT::G>(xv[i], av[i], d0, d1, d2, d3, sc);
+                const uint32_t ql0 = nibbles8(d0, d1), qh0 = nibbles8(d0 >> 4, d1 >> 4);
+                const uint32_t ql1 = nibbles8(d2, d3), qh1 = nibbles8(d2 >> 4, d3 >> 4);
+                int cs = (int)udot8(ql0, 0x11111111u, 0u) + (int)udot8(ql1, 0x11111111u, 0u);
+                cs += dpp_i<DPP_SWAP1>(cs);
+                if (p < KX / 16) {
+                    *(u32x4*)(lxq + (size_t)p * 16) = u32x4{ql0, qh0, ql1, qh1};
+                    if ((p & 1) == 0) lcs[p >> 1] = u32x2{(uint32_t)(-8 * cs), __float_as_uint(sc)};
+                }
+            }
+        } else if constexpr (PAIR8) {
             // pair p = octets 2p, 2p + 1 as (ql, qh) nibble words; the chunk
             // (4 octets) is lanes 2c, 2c + 1, its scale loaded by the even one
             const int p = at + ANT * i;
@@ -565,7 +590,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             }
         }
     }
-    if constexpr (!TWO && MR == 1 && !PAIR8) {
+    if constexpr (!TWO && MR == 1 && !PAIR8 && !PAIRBF) {
         if (__builtin_expect(xiters > XS, 0))
             for (int i = XS; i < xiters; ++i)
                 if (stager && wave0 + ANT * i < noct) quant_store(at + ANT * i, load_x(at + ANT * i));
