@@ -59,10 +59,6 @@ constexpr int M1_DELAY_WIDE = 10; // the same for a wide launch with the bf16 pr
 template <int F>
 __host__ __device__ constexpr int m1_exact_k(int ts, int cpl) { return Fmt<F>::CK * ts * cpl; }
 __host__ __device__ constexpr int m1_max(int a, int b) { return a > b ? a : b; }
-// Activation bytes (int8) a staging thread loads per round for int8 rows: 16
-// for Q4 on 320 or 640 threads (two octets), else 8.
-template <int F>
-__host__ __device__ constexpr int m1_row_bytes(int ntt) { return F == 4 && (ntt == 320 || ntt == 640) ? 16 : 8; }
 
 // Kernel modes: plain, with the int32 group dots (test entry point), or the
 // gate/up pair with the swiglu epilogue (M1_SWIGLU): the first NTT/2 threads
@@ -83,6 +79,17 @@ __host__ __device__ constexpr bool m1_wide(bool exact, int ts, int ntt, int cpl,
     return exact && mr * (m1_exact_k<F>(ts, cpl) / 8) <= ntt / 2;
 }
 
+// Launches whose staging threads take two octets each (Q4, exact tilings):
+// one int8 row on 320 or 640 threads, one bf16 row on 256, and 2-4 rows of
+// either on 640 (on 320 threads 2 rows were equal either way).
+template <int F>
+__host__ __device__ constexpr bool m1_pairs(bool exact, int ntt, int mr, int pro) {
+    return F == 4 && exact &&
+           (pro == PRO_INT8   ? (mr == 1 ? (ntt == 320 || ntt == 640) : ntt == 640)
+            : pro == PRO_BF16 ? (mr == 1 ? ntt == 256 : ntt == 640)
+                              : false);
+}
+
 // Weight-issue delay of a launch kind (s_sleep units).  Int8 rows (MR > 1)
 // wait in proportion to their staging rounds (one 8-byte load per thread and
 // round, or 16 bytes for Q4's two-octet staging; all issued before the
@@ -90,13 +97,17 @@ __host__ __device__ constexpr bool m1_wide(bool exact, int ts, int ntt, int cpl,
 // 5.9 / 8.2 us at 8 units against 5.1 / 7.6 us at 16 / 32; K = 2560, N = 10240
 // with 2 / 4 rows on 320 threads (2 / 4 rounds) best at 8 / 16; Q4's pairs (1,
 // 2 or 4 rounds) best at 8, 8 and 16.  The bf16 rows, which quantize what
-// they load, are best at 8 in all four cases.
+// they load, are best at 8 in all four cases one octet per thread; Q4's
+// two-octet bf16 rows follow the int8 rule (1, 2 or 4 rounds: 8, 8, 16).
 template <int F>
 __host__ __device__ constexpr int m1_delay(bool exact, int ts, int ntt, int cpl, int mode, int mr, int pro) {
     return mode == M1_SWIGLU                                   ? M1_DELAY_PAIR
            : mr > 1 && pro == PRO_INT8
-               ? M1_DELAY_ROUND * (exact ? m1_max(2, (mr * (m1_exact_k<F>(ts, cpl) / m1_row_bytes<F>(ntt)) + ntt - 1) / ntt)
+               ? M1_DELAY_ROUND * (exact ? m1_max(2, (mr * (m1_exact_k<F>(ts, cpl) /
+                                                             (m1_pairs<F>(exact, ntt, mr, pro) ? 16 : 8)) + ntt - 1) / ntt)
                                          : M1_XS_MR)
+           : mr > 1 && mode == M1_PLAIN && m1_pairs<F>(exact, ntt, mr, pro)
+               ? M1_DELAY_ROUND * m1_max(2, (mr * (m1_exact_k<F>(ts, cpl) / 16) + ntt - 1) / ntt)
            : mr > 1                                            ? M1_DELAY_MR
            : pro == PRO_INT8 && exact && ntt == 256            ? M1_DELAY_INT8_256
            : pro == PRO_INT8 && exact && ntt == 640            ? (F == 4 ? M1_DELAY_PAIR8_640 : M1_DELAY_INT8_640)
@@ -271,20 +282,25 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // squares covers the same octets as without the spare wave and the row's
     // sum (wave sums in wave order, the spare wave's 0 first) is unchanged
     // bit for bit.
-    // Q4 from one bf16 row on 256 threads (PAIRBF): each staging thread loads
-    // and quantizes two octets (16 values; the group's amax over its 4 lanes,
-    // the same maximum as over 8 lanes of one octet), so 160 threads stage a
-    // K = 2560 row and the fourth wave issues its weights at once; no spare
-    // wave.  The same LDS row bit for bit; K = N = 2560 2.51 -> 2.45 us (320
-    // threads, K = 2560, and 640, K = 10240: equal either way).
-    constexpr bool PAIRBF = PRO == PRO_BF16 && MODE == M1_PLAIN && MR == 1 && EXACT && F == 4 && NTT == 256;
+    // Q4 from bf16 rows (PAIRBF): each staging thread loads and quantizes two
+    // octets (16 values; the group's amax over its 4 lanes, the same maximum
+    // as over 8 lanes of one octet).  One row on 256 threads: 160 threads
+    // stage a K = 2560 row and the fourth wave issues its weights at once, no
+    // spare wave; K = N = 2560 2.51 -> 2.45 us (one row on 320 and 640
+    // threads: equal either way, not used).  2-4 rows on 640 threads: half the
+    // rounds; K = 10240, N = 2560 with 2 / 3 / 4 rows 5.8 / 8.2 / 9.7 -> 5.2 /
+    // 7.5 / 8.4 us, K = 2560, N = 10240 with 3 / 4 rows 5.85 / 6.1 -> 5.65 /
+    // 5.95 us (2 rows on 320 threads: equal, not used).  The same LDS rows bit
+    // for bit.
+    constexpr bool PAIRBF = PRO == PRO_BF16 && MODE == M1_PLAIN && m1_pairs<F>(EXACT, NTT, MR, PRO);
     constexpr bool SPARE = !PAIRBF && EXACT && MR == 1 &&
                            ((PRO == PRO_BF16 && MODE != M1_SWIGLU &&
                              (NTT == 256 || NTT == 320 || m1_wide<F>(EXACT, TS, NTT, CPL, MR))) ||
                             (MODE == M1_SWIGLU && (PRO == PRO_BF16 || (PRO == PRO_RMSNORM && KX / 8 <= NTT - 64))));
     constexpr int A0 = SPARE ? 64 : 0;  // first staging thread
     constexpr int ANT = NTT - A0;       // staging threads
-    // Q4 from int8 rows on 320 or 640 threads (PAIR8): each staging thread
+    // Q4 from int8 rows (PAIR8; one row on 320 or 640 threads, 2-4 rows on
+    // 640, m1_pairs): each staging thread
     // takes two octets with one 16-byte load and stores them with one 16-byte
     // LDS write, a chunk's two lanes summing its correction; with one row the
     // waves past its K/16 pairs stage nothing and issue their weights at once.
@@ -293,7 +309,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // 3 / 4 rows at K = 10240: 5.17 / 7.3 / 7.6 -> 4.85 / 6.55 / 6.85 us; on 256
     // threads (K = N = 2560, one row) one octet per thread stays faster (2.54
     // against 2.64 us).
-    constexpr bool PAIR8 = PRE && EXACT && F == 4 && !SPARE && (NTT == 320 || NTT == 640);
+    constexpr bool PAIR8 = PRE && !SPARE && m1_pairs<F>(EXACT, NTT, MR, PRO);
     constexpr int XS = (PAIR8 || PAIRBF) ? (MR * (KX / 16) + ANT - 1) / ANT
                        : EXACT ? (MR * (KX / 8) + ANT - 1) / ANT : MR > 1 ? M1_XS_MR : M1_XS;
     constexpr int ROWS = NTT / TS;
@@ -397,7 +413,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     for (int i = 0; i < XS; ++i) {
         xv[i] = u32x4{0u, 0u, 0u, 0u};
         av[i] = xv[i];
-        if (ALL_ROUNDS || ((i == 0 || ANT * i < noct) && stager)) {
+        if (ALL_ROUNDS || ((i == 0 || ANT * i < (PAIRBF ? noct / 2 : noct)) && stager)) {
             if constexpr (PAIRBF) {  // octets 2p, 2p + 1 (bf16)
                 xv[i] = bload16(xr, (at + ANT * i) * 32);
                 av[i] = bload16(xr, (at + ANT * i) * 32 + 16);
@@ -549,7 +565,8 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     for (int i = 0; i < XS; ++i) {
         if constexpr (PAIRBF) {
             const int p = at + ANT * i;
-            if (wave0 + ANT * i < KX / 16 && stager) {
+            const int npair = MR == 1 ? KX / 16 : M * (K / 16);  // pairs of all rows
+            if (wave0 + ANT * i < npair && stager) {
                 uint32_t d0, d1, d2, d3;
                 float sc;
                 quantize_octet_pair<FT::G>(xv[i], av[i], d0, d1, d2, d3, sc);
@@ -557,7 +574,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
                 const uint32_t ql1 = nibbles8(d2, d3), qh1 = nibbles8(d2 >> 4, d3 >> 4);
                 int cs = (int)udot8(ql0, 0x11111111u, 0u) + (int)udot8(ql1, 0x11111111u, 0u);
                 cs += dpp_i<DPP_SWAP1>(cs);
-                if (p < KX / 16) {
+                if (p < npair) {
                     *(u32x4*)(lxq + (size_t)p * 16) = u32x4{ql0, qh0, ql1, qh1};
                     if ((p & 1) == 0) lcs[p >> 1] = u32x2{(uint32_t)(-8 * cs), __float_as_uint(sc)};
                 }

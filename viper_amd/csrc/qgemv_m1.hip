@@ -125,6 +125,15 @@ bool m1_rows_ok(int qtype, int K, int M) {
     return sh.ntt != 0 && lds_m1_launch(qtype, K, 0, false, m1_mr(M)) + kBlockMax <= (size_t)LDS_MAX;
 }
 
+bool m1_rows_pair(int qtype, int K, int M) {
+    // the multi-row shape stages its rows two octets per thread (m1_pairs)
+    if (qtype != VIPER_QTYPE_Q4_G64 || !m1_rows_ok(qtype, K, M)) return false;
+    const int noct = M * (K / 8);
+    const M1Shape sh = m1_shape(K / 32, 1 << 14, device_cus(), (noct + M1_XS_MR - 1) / M1_XS_MR, noct, false, m1_mr(M));
+    const bool exact = (K / 32) == sh.ts * sh.cpl && (K / 64) % 8 == 0;
+    return m1_pairs<4>(exact, sh.ntt, m1_mr(M), PRO_BF16);
+}
+
 bool m1_folded_ok(int qtype, int K, int N) {
     const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32;
     const int noct = K / 8;

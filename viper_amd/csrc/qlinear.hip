@@ -308,7 +308,11 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     // 3 or 4 rows of one matrix take the multi-row dot kernel below in every
     // format (Q4 at K = 2560, N = 10240: 4 rows 6.03 against 6.29 us here).
     const bool hi = qtype == VIPER_QTYPE_Q5_G64 || qtype == VIPER_QTYPE_Q6_G64;
-    const bool rows_ok = b.w == nullptr && m1_rows_ok(qtype, K, M) && (long)M * K <= 32768;
+    // (Q4 rows staged two octets per thread also past that size: down shape
+    // K = 10240, 4 rows 8.4 us against 9.0-9.1 us for two launches with the K
+    // split)
+    const bool rows_ok = b.w == nullptr && m1_rows_ok(qtype, K, M) &&
+                         ((long)M * K <= 32768 || m1_rows_pair(qtype, K, M));
     const bool bf_ok = mf && M >= 3 && M <= (hi ? 7 : 8) && !split_ok && rc_bf16_ok(qtype, N, K, M, b.w != nullptr);
     if (bf_ok && (M > 4 || !rows_ok))
         return launch_rc(qtype, w, s, senc, N, K, x, nullptr, RC_BF16, M, y, res, part, b.w, b.s, b.y, st);

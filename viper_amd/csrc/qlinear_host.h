@@ -96,6 +96,9 @@ bool m1_folded_ok(int qtype, int K, int N);
 int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa, float eps, void* xout,
               const M1Out* outs, int nouts, const void* res, int32_t* part, hipStream_t st, int M = 1);
 bool m1_rows_ok(int qtype, int K, int M);
+// m1_rows_ok and the bf16 rows are staged two octets per thread (Q4, exact
+// tiling on 640 threads).
+bool m1_rows_pair(int qtype, int K, int M);
 // The M = 1 GEMV (bf16 x, exact tilings) with its per-wave timeline.
 int launch_m1_timeline(int qtype, int senc, int K, const void* x, const void* w, const void* s, void* y, int N,
                        uint64_t* stamps, size_t stamp_bytes, int* workgroups, int* waves, hipStream_t st);
