@@ -187,12 +187,20 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     constexpr int NTT = 64 * W;
     const int KO = K / 8, noct = M * KO;  // RC_BF16: octets of all rows
     u32x4 xv[XBF ? RC_XR : 1];
+    // 64-groups (16-byte fragment slots): each thread takes two consecutive
+    // octets of a group, which share one slot (XP); 32-groups one octet
+    constexpr bool XP = XBF && FM::QB == 16;
     if constexpr (XBF) {
         // every octet this thread quantizes, before any weight request
 #pragma unroll
         for (int i = 0; i < RC_XR; ++i) {
             xv[i] = u32x4{0u, 0u, 0u, 0u};
-            if (i == 0 || NTT * i < noct) xv[i] = bload16(xr, (tid + NTT * i) * 16);
+            if constexpr (XP) {
+                const int r = i >> 1;  // pair round; octet 2p + (i & 1) of pair p
+                if (r == 0 || NTT * r < noct / 2) xv[i] = bload16(xr, ((tid + NTT * r) * 2 + (i & 1)) * 16);
+            } else {
+                if (i == 0 || NTT * i < noct) xv[i] = bload16(xr, (tid + NTT * i) * 16);
+            }
         }
         issue_fence();
     }
@@ -419,6 +427,28 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     // reduction sees whole groups.
     auto quantize = [&] {
         const int wave0 = tid & ~63;
+        if constexpr (XP) {
+            // pair p = octets 2p, 2p + 1 (j, j + 1 of a group, j even): the
+            // group's amax over its 4 lanes, both octets in one 16-byte store
+#pragma unroll
+            for (int r = 0; r < RC_XR / 2; ++r) {
+                if (wave0 + NTT * r < noct / 2) {
+                    const int p = tid + NTT * r;
+                    uint32_t d0, d1, d2, d3;
+                    float sc;
+                    quantize_octet_pair<G, true>(xv[2 * r], xv[2 * r + 1], d0, d1, d2, d3, sc);
+                    if (p < noct / 2) {
+                        const int o = 2 * p, m = o / KO, k8 = o - m * KO;
+                        const int g = k8 / 8, q = (k8 % 8) >> 1;
+                        const int slot = ((q & 1) << 1) | (q >> 1);
+                        *(u32x4*)(lxq + ((size_t)g * 64 + 16 * slot + m) * 16) = u32x4{d0, d1, d2, d3};
+                        if (k8 % 8 == 0) lxs[g * 16 + m] = sc;
+                    }
+                }
+            }
+            lds_barrier();
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < RC_XR; ++i) {
             if (wave0 + NTT * i < noct) {

@@ -177,8 +177,9 @@ __device__ __forceinline__ void quantize_octet(const u32x4& v, uint32_t& d0, uin
 
 // Two consecutive octets of one lane (16 bf16 values of a group held by
 // G / 16 lanes): the same group amax, scale and bytes as quantize_octet on
-// each octet, in k order (d0, d1 the first octet, d2, d3 the second).
-template <int G>
+// each octet (d0, d1 the first octet, d2, d3 the second; PERM: even k then
+// odd k within each octet, as quantize_octet<G, true>).
+template <int G, bool PERM = false>
 __device__ __forceinline__ void quantize_octet_pair(const u32x4& v0, const u32x4& v1, uint32_t& d0, uint32_t& d1,
                                                     uint32_t& d2, uint32_t& d3, float& s) {
     const uint32_t wd[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
@@ -195,10 +196,17 @@ __device__ __forceinline__ void quantize_octet_pair(const u32x4& v0, const u32x4
     uint32_t t[16];
 #pragma unroll
     for (int e = 0; e < 16; ++e) t[e] = qbits(f[e], s, r);
-    d0 = bytes4(t[0], t[1], t[2], t[3]);
-    d1 = bytes4(t[4], t[5], t[6], t[7]);
-    d2 = bytes4(t[8], t[9], t[10], t[11]);
-    d3 = bytes4(t[12], t[13], t[14], t[15]);
+    if constexpr (PERM) {
+        d0 = bytes4(t[0], t[2], t[4], t[6]);
+        d1 = bytes4(t[1], t[3], t[5], t[7]);
+        d2 = bytes4(t[8], t[10], t[12], t[14]);
+        d3 = bytes4(t[9], t[11], t[13], t[15]);
+    } else {
+        d0 = bytes4(t[0], t[1], t[2], t[3]);
+        d1 = bytes4(t[4], t[5], t[6], t[7]);
+        d2 = bytes4(t[8], t[9], t[10], t[11]);
+        d3 = bytes4(t[12], t[13], t[14], t[15]);
+    }
 }
 
 // Sum of the 8 int8 values held in two packed words.
