@@ -300,21 +300,25 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     // (long K splits over workgroups in the two-launch path instead: down
     // shape K = 10240, 4 rows 9.5 us against 10.3 us)
     const bool split_ok = mf && b.w == nullptr && rc_split_ok(qtype, K);
-    // Q5/Q6/W8 (K = 2560, N = 10240, 5% outlier channels): 3 or 4 rows run
-    // faster on the dot kernel below (Q5 4 rows 7.86 against 8.10 us) or in
-    // two launches (W8 3 rows 8.37 against 9.23 us), and Q5/Q6 8 rows in two
-    // launches (8.65 / 8.89 against 9.01 / 9.10 us); 6 rows of every format
-    // and 8 of W8 stay here.
-    // 3 or 4 rows of one matrix take the multi-row dot kernel below in every
-    // format (Q4 at K = 2560, N = 10240: 4 rows 6.03 against 6.29 us here).
-    const bool hi = qtype == VIPER_QTYPE_Q5_G64 || qtype == VIPER_QTYPE_Q6_G64;
+    // Q5/Q6/W8 (K = 2560, N = 10240, 5% outlier channels): 3 or 4 rows of one
+    // matrix run faster on the multi-row dot kernel below (Q5 4 rows 7.86
+    // against 8.10 us; W8 3 / 4 rows 7.47 / 7.77 against 8.9 / 9.17 us); 5-8
+    // rows of every format stay on the one-launch path.
     // (Q4 rows staged two octets per thread also past that size: down shape
     // K = 10240, 4 rows 8.4 us against 9.0-9.1 us for two launches with the K
     // split)
     const bool rows_ok = b.w == nullptr && m1_rows_ok(qtype, K, M) &&
                          ((long)M * K <= 32768 || m1_rows_pair(qtype, K, M));
-    const bool bf_ok = mf && M >= 3 && M <= (hi ? 7 : 8) && !split_ok && rc_bf16_ok(qtype, N, K, M, b.w != nullptr);
-    if (bf_ok && (M > 4 || !rows_ok))
+    // With the rows staged two octets per thread (64-groups), the one-launch
+    // path also wins for Q4 at 3-4 rows (5.45 / 5.74 against 5.6 / 5.9 us on the
+    // dot kernel) and 9-10 rows (6.76 / 7.00 against 7.27 us in two launches;
+    // 12 and 16 rows stay two launches: 7.5 / 8.2 against 7.3 us), and for
+    // Q5 / Q6 at 8 rows (7.90 / 8.22 against 8.37 / 8.58 us).  W8 (32-groups,
+    // one octet per thread) keeps the earlier bounds.
+    const bool q4 = qtype == VIPER_QTYPE_Q4_G64;
+    const int bf_max = q4 && b.w == nullptr ? 10 : 8;
+    const bool bf_ok = mf && M >= 3 && M <= bf_max && !split_ok && rc_bf16_ok(qtype, N, K, M, b.w != nullptr);
+    if (bf_ok && (M > 4 || !rows_ok || q4))
         return launch_rc(qtype, w, s, senc, N, K, x, nullptr, RC_BF16, M, y, res, part, b.w, b.s, b.y, st);
     // (3 or 4 rows here also where the LDS copy does not fit: while every
     // workgroup's share of the rows' quantize stays small; down shape
