@@ -187,9 +187,10 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     constexpr int NTT = 64 * W;
     const int KO = K / 8, noct = M * KO;  // RC_BF16: octets of all rows
     u32x4 xv[XBF ? RC_XR : 1];
-    // 64-groups (16-byte fragment slots): each thread takes two consecutive
-    // octets of a group, which share one slot (XP); 32-groups one octet
-    constexpr bool XP = XBF && FM::QB == 16;
+    // each thread takes two consecutive octets of a group (XP): with
+    // 64-groups (16-byte fragment slots) they share one slot, with 32-groups
+    // (W8, 8-byte slots) they go to two
+    constexpr bool XP = XBF;
     if constexpr (XBF) {
         // every octet this thread quantizes, before any weight request
 #pragma unroll
@@ -436,13 +437,21 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                     const int p = tid + NTT * r;
                     uint32_t d0, d1, d2, d3;
                     float sc;
-                    quantize_octet_pair<G, true>(xv[2 * r], xv[2 * r + 1], d0, d1, d2, d3, sc);
+                    quantize_octet_pair<G, (F != 8)>(xv[2 * r], xv[2 * r + 1], d0, d1, d2, d3, sc);
                     if (p < noct / 2) {
                         const int o = 2 * p, m = o / KO, k8 = o - m * KO;
-                        const int g = k8 / 8, q = (k8 % 8) >> 1;
-                        const int slot = ((q & 1) << 1) | (q >> 1);
-                        *(u32x4*)(lxq + ((size_t)g * 64 + 16 * slot + m) * 16) = u32x4{d0, d1, d2, d3};
-                        if (k8 % 8 == 0) lxs[g * 16 + m] = sc;
+                        if constexpr (G == 64) {
+                            const int g = k8 / 8, q = (k8 % 8) >> 1;
+                            const int slot = ((q & 1) << 1) | (q >> 1);
+                            *(u32x4*)(lxq + ((size_t)g * 64 + 16 * slot + m) * 16) = u32x4{d0, d1, d2, d3};
+                            if (k8 % 8 == 0) lxs[g * 16 + m] = sc;
+                        } else {
+                            const int g = k8 / 4, q0 = k8 % 4, q1 = q0 + 1;
+                            const int s0 = ((q0 & 1) << 1) | (q0 >> 1), s1 = ((q1 & 1) << 1) | (q1 >> 1);
+                            *(u32x2*)(lxq + ((size_t)g * 64 + 16 * s0 + m) * 8) = u32x2{d0, d1};
+                            *(u32x2*)(lxq + ((size_t)g * 64 + 16 * s1 + m) * 8) = u32x2{d2, d3};
+                            if (q0 == 0) lxs[g * 16 + m] = sc;
+                        }
                     }
                 }
             }

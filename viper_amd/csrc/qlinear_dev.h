@@ -72,11 +72,12 @@ __device__ __forceinline__ uint32_t bytes4(uint32_t a, uint32_t b, uint32_t c, u
     return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
-// Max / sum over the LANES (4 or 8) consecutive lanes that hold one group.
+// Max / sum over the LANES (2, 4 or 8; sums 4 or 8) consecutive lanes that
+// hold one group.
 template <int LANES>
 __device__ __forceinline__ float group_max(float v) {
     v = fmaxf(v, dpp_f<DPP_SWAP1>(v));
-    v = fmaxf(v, dpp_f<DPP_SWAP2>(v));
+    if constexpr (LANES >= 4) v = fmaxf(v, dpp_f<DPP_SWAP2>(v));
     if constexpr (LANES == 8) v = fmaxf(v, dpp_f<DPP_HALF_MIRROR>(v));
     return v;
 }
