@@ -126,8 +126,9 @@ def test_m1_fused(torch_dev, qtype, scale_enc, N, K):
 
 
 @pytest.mark.parametrize("qtype", FORMATS)
-@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 16])
+@pytest.mark.parametrize("M", [2, 3, 4, 5, 8, 9, 10, 16])
 def test_multi_row(torch_dev, qtype, M):
+    # (Q4 9 and 10 rows at K = 2560: the one-launch bf16-row path, staged in pairs)
     K = 2048 if M <= 8 else 2560
     run_case(torch_dev, qtype, 77, K, M, seed=2000 + M, residual=(M % 2 == 0))
 
