@@ -139,7 +139,7 @@ def test_multi_row(torch_dev, qtype, M):
 # prequantized entry takes 4 rows at K = 10240 through all eight staging
 # rounds of a 640-thread workgroup: test_prequantized_entry.)
 @pytest.mark.parametrize("qtype", FORMATS)
-@pytest.mark.parametrize("M,K", [(2, 10240), (4, 10240), (3, 12288), (4, 16384)])
+@pytest.mark.parametrize("M,K", [(2, 10240), (3, 10240), (4, 10240), (3, 12288), (4, 16384)])
 def test_multi_row_long_k(torch_dev, qtype, M, K):
     run_case(torch_dev, qtype, 45, K, M, seed=2100 + M + K, residual=(M == 4))
 
@@ -507,7 +507,8 @@ def test_bf16_rows_match_prequantized(torch_dev, qtype, N, K, M):
 
 
 @pytest.mark.parametrize("N,K,M", [(200, 2560, 3), (70, 10240, 16), (40, 192, 2), (6001, 4096, 16), (45, 10240, 4),
-                                   (300, 10240, 3), (130, 7680, 2), (90, 7680, 3), (90, 7680, 4)])
+                                   (300, 10240, 3), (130, 7680, 2), (90, 7680, 3), (90, 7680, 4),
+                                   (47, 10240, 3)])
 def test_prequantized_entry(torch_dev, N, K, M):
     # activations in viper_hip_quantize_act's layout ([M][K] int8, [M][K/G] fp32)
     torch = torch_dev
