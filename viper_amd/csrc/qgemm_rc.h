@@ -187,21 +187,16 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     constexpr int NTT = 64 * W;
     const int KO = K / 8, noct = M * KO;  // RC_BF16: octets of all rows
     u32x4 xv[XBF ? RC_XR : 1];
-    // each thread takes two consecutive octets of a group (XP): with
-    // 64-groups (16-byte fragment slots) they share one slot, with 32-groups
-    // (W8, 8-byte slots) they go to two
-    constexpr bool XP = XBF;
     if constexpr (XBF) {
-        // every octet this thread quantizes, before any weight request
+        // every octet this thread quantizes, before any weight request: two
+        // consecutive octets of a group per round (pair p = octets 2p, 2p + 1;
+        // with 64-groups, 16-byte fragment slots, they share one slot, with
+        // 32-groups, W8's 8-byte slots, they go to two)
 #pragma unroll
         for (int i = 0; i < RC_XR; ++i) {
             xv[i] = u32x4{0u, 0u, 0u, 0u};
-            if constexpr (XP) {
-                const int r = i >> 1;  // pair round; octet 2p + (i & 1) of pair p
-                if (r == 0 || NTT * r < noct / 2) xv[i] = bload16(xr, ((tid + NTT * r) * 2 + (i & 1)) * 16);
-            } else {
-                if (i == 0 || NTT * i < noct) xv[i] = bload16(xr, (tid + NTT * i) * 16);
-            }
+            const int r = i >> 1;  // pair round; octet 2p + (i & 1) of pair p
+            if (r == 0 || NTT * r < noct / 2) xv[i] = bload16(xr, ((tid + NTT * r) * 2 + (i & 1)) * 16);
         }
         issue_fence();
     }
@@ -428,51 +423,30 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     // reduction sees whole groups.
     auto quantize = [&] {
         const int wave0 = tid & ~63;
-        if constexpr (XP) {
-            // pair p = octets 2p, 2p + 1 (j, j + 1 of a group, j even): the
-            // group's amax over its 4 lanes, both octets in one 16-byte store
+        // pair p = octets 2p, 2p + 1 (j, j + 1 of a group, j even): the
+        // group's amax over its G / 16 lanes, the same bytes as one octet per
+        // thread (quantize_octet_pair)
 #pragma unroll
-            for (int r = 0; r < RC_XR / 2; ++r) {
-                if (wave0 + NTT * r < noct / 2) {
-                    const int p = tid + NTT * r;
-                    uint32_t d0, d1, d2, d3;
-                    float sc;
-                    quantize_octet_pair<G, (F != 8)>(xv[2 * r], xv[2 * r + 1], d0, d1, d2, d3, sc);
-                    if (p < noct / 2) {
-                        const int o = 2 * p, m = o / KO, k8 = o - m * KO;
-                        if constexpr (G == 64) {
-                            const int g = k8 / 8, q = (k8 % 8) >> 1;
-                            const int slot = ((q & 1) << 1) | (q >> 1);
-                            *(u32x4*)(lxq + ((size_t)g * 64 + 16 * slot + m) * 16) = u32x4{d0, d1, d2, d3};
-                            if (k8 % 8 == 0) lxs[g * 16 + m] = sc;
-                        } else {
-                            const int g = k8 / 4, q0 = k8 % 4, q1 = q0 + 1;
-                            const int s0 = ((q0 & 1) << 1) | (q0 >> 1), s1 = ((q1 & 1) << 1) | (q1 >> 1);
-                            *(u32x2*)(lxq + ((size_t)g * 64 + 16 * s0 + m) * 8) = u32x2{d0, d1};
-                            *(u32x2*)(lxq + ((size_t)g * 64 + 16 * s1 + m) * 8) = u32x2{d2, d3};
-                            if (q0 == 0) lxs[g * 16 + m] = sc;
-                        }
-                    }
-                }
-            }
-            lds_barrier();
-            return;
-        }
-#pragma unroll
-        for (int i = 0; i < RC_XR; ++i) {
-            if (wave0 + NTT * i < noct) {
-                const int o = tid + NTT * i;
-                uint32_t d0, d1;
+        for (int r = 0; r < RC_XR / 2; ++r) {
+            if (wave0 + NTT * r < noct / 2) {
+                const int p = tid + NTT * r;
+                uint32_t d0, d1, d2, d3;
                 float sc;
-                quantize_octet<G, (F != 8)>(xv[i], d0, d1, sc);
-                if (o < noct) {
-                    const int m = o / KO, k8 = o - m * KO;
-                    const int g = k8 / (G / 8), j = k8 % (G / 8);
-                    const int q = G == 64 ? j >> 1 : j;
-                    const int slot = ((q & 1) << 1) | (q >> 1);
-                    *(u32x2*)(lxq + ((size_t)g * 64 + 16 * slot + m) * FM::QB + (G == 64 ? (j & 1) * 8 : 0)) =
-                        u32x2{d0, d1};
-                    if (j == 0) lxs[g * 16 + m] = sc;
+                quantize_octet_pair<G, (F != 8)>(xv[2 * r], xv[2 * r + 1], d0, d1, d2, d3, sc);
+                if (p < noct / 2) {
+                    const int o = 2 * p, m = o / KO, k8 = o - m * KO;
+                    if constexpr (G == 64) {  // one 16-byte slot
+                        const int g = k8 / 8, q = (k8 % 8) >> 1;
+                        const int slot = ((q & 1) << 1) | (q >> 1);
+                        *(u32x4*)(lxq + ((size_t)g * 64 + 16 * slot + m) * 16) = u32x4{d0, d1, d2, d3};
+                        if (k8 % 8 == 0) lxs[g * 16 + m] = sc;
+                    } else {  // two 8-byte slots
+                        const int g = k8 / 4, q0 = k8 % 4, q1 = q0 + 1;
+                        const int s0 = ((q0 & 1) << 1) | (q0 >> 1), s1 = ((q1 & 1) << 1) | (q1 >> 1);
+                        *(u32x2*)(lxq + ((size_t)g * 64 + 16 * s0 + m) * 8) = u32x2{d0, d1};
+                        *(u32x2*)(lxq + ((size_t)g * 64 + 16 * s1 + m) * 8) = u32x2{d2, d3};
+                        if (q0 == 0) lxs[g * 16 + m] = sc;
+                    }
                 }
             }
         }

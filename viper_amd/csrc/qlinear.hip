@@ -313,8 +313,8 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     // path also wins for Q4 at 3-4 rows (5.45 / 5.74 against 5.6 / 5.9 us on the
     // dot kernel) and 9-10 rows (6.76 / 7.00 against 7.27 us in two launches;
     // 12 and 16 rows stay two launches: 7.5 / 8.2 against 7.3 us), and for
-    // Q5 / Q6 at 8 rows (7.90 / 8.22 against 8.37 / 8.58 us).  W8 (32-groups,
-    // one octet per thread) keeps the earlier bounds.
+    // Q5 / Q6 at 8 rows (7.90 / 8.22 against 8.37 / 8.58 us).  W8 keeps 3-4
+    // rows on the dot kernel and 5-8 here.
     const bool q4 = qtype == VIPER_QTYPE_Q4_G64;
     const int bf_max = q4 && b.w == nullptr ? 10 : 8;
     const bool bf_ok = mf && M >= 3 && M <= bf_max && !split_ok && rc_bf16_ok(qtype, N, K, M, b.w != nullptr);
