@@ -77,7 +77,7 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False, prequa
     x = xf.to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     nws = L.viper_hip_qlinear_workspace_bytes(qtype, N, K, M)
-    ws = torch.empty(max(nws, 16), dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda")   # zero before first use
     if prequantized:
         xq = torch.empty(M * K, dtype=torch.int8, device="cuda")
         xs = torch.empty(M * (K // G), dtype=torch.float32, device="cuda")
@@ -535,7 +535,7 @@ def main():
         x16 = torch.randn((M16, K), device="cuda", generator=gen).to(torch.bfloat16)
         y16 = torch.empty((M16, N), dtype=torch.bfloat16, device="cuda")
         nws = va.workspace_bytes(qtype, N, K, M16)
-        ws16 = torch.empty(nws, dtype=torch.uint8, device="cuda")
+        ws16 = torch.zeros(nws, dtype=torch.uint8, device="cuda")
 
         def launch16(i):
             c = i % copies

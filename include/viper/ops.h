@@ -15,7 +15,8 @@ namespace viper::ops {
 
 struct LinearOptions {
     const Tensor* residual = nullptr;  // [M, N] bf16 added in fp32 before the bf16 round
-    void* workspace = nullptr;         // device scratch for M > 1 (see linear_workspace_bytes)
+    void* workspace = nullptr;         // device scratch for M > 1 (see linear_workspace_bytes), zero-filled
+                                       // before its first use, then reused without clearing
     usize workspace_bytes = 0;
     void* stream = nullptr;
 };

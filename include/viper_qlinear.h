@@ -109,8 +109,11 @@ extern "C" {
 #define VIPER_SCALE_BF16 1
 
 #define VIPER_QLINEAR_MAX_M 16
-/* 5: weight scales must be 16-byte aligned (4 accepted 2-byte aligned scales) */
-#define VIPER_QLINEAR_ABI_VERSION 5
+/* 6: the M > 1 workspace is zero-filled before its first use and keeps the
+ *    K split's control words at offset 0 (5 needed no initialisation);
+ *    viper_hip_qlinear_workspace_layout.
+ * 5: weight scales must be 16-byte aligned (4 accepted 2-byte aligned scales) */
+#define VIPER_QLINEAR_ABI_VERSION 6
 
 int viper_hip_abi_version(void);
 
@@ -120,10 +123,25 @@ int viper_hip_group_size(int qtype);
 /* Bytes of caller workspace viper_hip_qlinear needs for this shape; 0 when
  * the activation quantize is fused into the GEMV (M == 1).  It holds the
  * int8 activations and their scales, and for long K on the matrix cores
- * (K of more than 20 quads of 4 groups) the K split's fp32 part sums and
- * per-block counters.  Its contents need no initialisation; calls that use
- * one workspace concurrently race. */
+ * (K of more than 20 quads of 4 groups) the K split's control words, block
+ * counters and fp32 part sums.  A workspace is zero-filled before its first
+ * use (hipMemset, torch.zeros); after that it serves any sequence of shapes
+ * that fit it with no clearing (each call leaves it valid for the next), as
+ * long as nothing else writes it.  Calls that use one workspace
+ * concurrently race. */
 size_t viper_hip_qlinear_workspace_bytes(int qtype, int N, int K, int M);
+
+/* The workspace's layout for this shape (no counterpart in the reference;
+ * tests and debugging).  Returns viper_hip_qlinear_workspace_bytes() and,
+ * when offsets is not NULL, writes six byte offsets into the workspace
+ * (SIZE_MAX where the shape has no such part):
+ *   [0] the K split's generation word (uint32; 0 for every shape),
+ *   [1] the count of K-split sums that did not arrive within the kernel's
+ *       bounded wait (uint32 at 4 for every shape; such outputs are NaN;
+ *       the library never clears it, so a caller can check it stayed 0),
+ *   [2] the K split's block counters, [3] xq, [4] xs, [5] the K split's
+ *       part sums (64-bit slots). */
+size_t viper_hip_qlinear_workspace_layout(int qtype, int N, int K, int M, size_t* offsets);
 
 /* y[M][N] = linear(w, x) with x[M][K] bf16 quantized per row and group.
  * residual (may be NULL) is added in fp32 before the bf16 round.  group must
@@ -234,11 +252,10 @@ int viper_hip_sampling_greedy_split(const void* logits_bf16, int32_t* out_token,
 
 /* viper_hip_qlinear without a workspace argument, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc).  No counterpart in the reference (whose
- * multi-row path hides a lazily cudaMalloc'd static buffer,
- * kernels/ops/linear_multim.cu:133-146).  The workspace is a static device
- * array of VIPER_QLINEAR_STATIC_SCRATCH_BYTES per GPU, held until the process
- * ends; the call allocates nothing.  Shapes whose
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is a static device array of VIPER_QLINEAR_STATIC_SCRATCH_BYTES
+ * per GPU (zero when the library is loaded), held until the process ends;
+ * the call allocates nothing.  Shapes whose
  * viper_hip_qlinear_workspace_bytes() exceeds it return INVALID_ARGUMENT.
  * Every call on one GPU shares that GPU's array: calls that overlap on one
  * GPU (concurrent streams or host threads) race; calls ordered on one stream

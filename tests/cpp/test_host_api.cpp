@@ -81,7 +81,7 @@ int main() {
     Tensor y4(fake, DType::BF16, {4, 64});
     EXPECT(code(w, x4, y4) == StatusCode::INVALID_ARGUMENT);  // no workspace
     EXPECT(ops::linear_workspace_bytes(w, 1) == 0);
-    EXPECT(ops::linear_workspace_bytes(w, 4) == 16 * 128 + 2 * 16 * 4);  // xq, xs for 16 rows
+    EXPECT(ops::linear_workspace_bytes(w, 4) == 16 + 16 * 128 + 2 * 16 * 4);  // control words, xq, xs for 16 rows
     Tensor misaligned(reinterpret_cast<void*>(0x10008), DType::BF16, {128});
     EXPECT(code(w, misaligned, y) == StatusCode::INVALID_ARGUMENT);
     // lossy dtypes through the Tensor overload: UNIMPLEMENTED, as the
@@ -155,6 +155,28 @@ int main() {
             const uint32_t big[10] = {1, 1, 1, 0x80000000u, 64, 1, 1, 64, 64, 16};  // hidden > INT32_MAX
             std::memcpy(bad.data() + 16, big, sizeof big);
             EXPECT(A::parse(bad.data(), bad.size(), &idx).code() == StatusCode::INVALID_ARGUMENT);
+        }
+        // untrusted layer / pass counts: a bare 56-byte header (and one with a
+        // few KB after it) claiming 2^32 - 1 layers must come back as a
+        // Status before anything is sized by that count (no throw)
+        {
+            const uint32_t many[10] = {1, 0xFFFFFFFFu, 1, 128, 256, 2, 1, 64, 300, 16};
+            const uint32_t passes[10] = {1, 2, 0xFFFFFFFFu, 128, 256, 2, 1, 64, 300, 16};
+            for (const uint32_t* h : {many, passes})
+                for (const size_t extra : {(size_t)0, (size_t)8192}) {
+                    std::vector<uint8_t> bad(A::kHeaderBytes + extra, 0);
+                    std::memcpy(bad.data(), "VIPER", 5);
+                    std::memcpy(bad.data() + 16, h, 40);
+                    bool threw = false;
+                    StatusCode c = StatusCode::OK;
+                    try {
+                        c = A::parse(bad.data(), bad.size(), &idx).code();
+                    } catch (...) {
+                        threw = true;
+                    }
+                    EXPECT(!threw && c == StatusCode::IO_ERROR);
+                    EXPECT(idx.layers.empty() && idx.norms.empty());
+                }
         }
         ArtifactDims odd = d;
         odd.hidden = 96;  // not a multiple of the 64-group

@@ -85,7 +85,10 @@ static int run_case(int qt, int senc, int N, int K, int M, uint64_t seed) {
     Tensor tr = M == 1 ? Tensor(dr, DType::BF16, {N}) : Tensor(dr, DType::BF16, {M, N});
     const usize nws = ops::linear_workspace_bytes(w, M);
     void* dws = nullptr;
-    if (nws) CHECK_HIP(hipMalloc(&dws, nws));
+    if (nws) {
+        CHECK_HIP(hipMalloc(&dws, nws));
+        CHECK_HIP(hipMemset(dws, 0, nws));  // zero before first use
+    }
     ops::LinearOptions opt;
     opt.workspace = dws;
     opt.workspace_bytes = nws;
@@ -271,7 +274,10 @@ int reference_fields_case(int qt, int M) {
     Tensor tx(dx, DType::BF16, {M, K}), ty(dy, DType::BF16, {M, N});
     ops::LinearOptions opt;
     opt.workspace_bytes = ops::linear_workspace_bytes(w, M);
-    if (opt.workspace_bytes) CHECK_HIP(hipMalloc(&opt.workspace, opt.workspace_bytes));
+    if (opt.workspace_bytes) {
+        CHECK_HIP(hipMalloc(&opt.workspace, opt.workspace_bytes));
+        CHECK_HIP(hipMemset(opt.workspace, 0, opt.workspace_bytes));  // zero before first use
+    }
     char what[96];
     std::snprintf(what, sizeof what, "reference fields q%d M%d (bf16 scales)", qt, M);
     std::printf("case %s\n", what);

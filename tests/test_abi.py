@@ -28,23 +28,84 @@ def test_header_symbols_exported():
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(ql._SYMBOLS)
-    assert L.viper_hip_abi_version() == 5
+    assert L.viper_hip_abi_version() == 6
 
 
 def test_group_sizes_and_workspace():
     L = va.lib()
     assert [L.viper_hip_group_size(q) for q in (4, 5, 6, 8, 0, 1, 7)] == [64, 64, 64, 32, 0, 0, 0]
     assert va.workspace_bytes(4, 10240, 2560, 1) == 0
-    # int8 activations with room for 16 rows, then fp32 scales for 16 rows per group
-    assert va.workspace_bytes(4, 10240, 2560, 4) == 16 * 2560 + 40 * 16 * 4
-    assert va.workspace_bytes(8, 10, 2560, 3) == 16 * 2560 + 80 * 16 * 4
-    assert va.workspace_bytes(6, 10, 2496, 3) == 16 * 2496 + 39 * 16 * 4
-    # long K (the K split in 4 parts): then the part sums [4][M][N] as 64-bit
-    # {generation, fp32} slots, one counter per 8 rows and the generation word
-    # (16-byte aligned)
-    assert va.workspace_bytes(4, 2560, 10240, 16) == 16 * 10240 + 160 * 16 * 4 + 4 * 16 * 2560 * 8 + 1296
-    assert va.workspace_bytes(8, 2560, 10240, 3) == 16 * 10240 + 320 * 16 * 4 + 4 * 3 * 2560 * 8 + 1296
-    assert va.workspace_bytes(4, 2560, 5120, 16) == 16 * 5120 + 80 * 16 * 4   # one segment: no split
+    # 16 bytes of control words, int8 activations with room for 16 rows, then
+    # fp32 scales for 16 rows per group
+    assert va.workspace_bytes(4, 10240, 2560, 4) == 16 + 16 * 2560 + 40 * 16 * 4
+    assert va.workspace_bytes(8, 10, 2560, 3) == 16 + 16 * 2560 + 80 * 16 * 4
+    assert va.workspace_bytes(6, 10, 2496, 3) == 16 + 16 * 2496 + 39 * 16 * 4
+    # long K (the K split in 4 parts): also one counter per 8 rows (16-byte
+    # aligned, after the control words) and the part sums [4][M][N] as 64-bit
+    # {tag, fp32} slots
+    assert va.workspace_bytes(4, 2560, 10240, 16) == 16 + 1280 + 16 * 10240 + 160 * 16 * 4 + 4 * 16 * 2560 * 8
+    assert va.workspace_bytes(8, 2560, 10240, 3) == 16 + 1280 + 16 * 10240 + 320 * 16 * 4 + 4 * 3 * 2560 * 8
+    assert va.workspace_bytes(4, 2560, 5120, 16) == 16 + 16 * 5120 + 80 * 16 * 4   # one segment: no split
+
+
+def _split_shapes():
+    for qtype in (4, 5, 6, 8):
+        for K in (6144, 10240, 12288, 20480):
+            for M in (5, 6, 9, 12, 16):
+                for N in (64, 640, 1000, 2048, 2560, 10240):
+                    yield qtype, N, K, M
+
+
+def test_split_control_words_fixed_for_every_shape():
+    # The K split's generation word sits at offset 0 whatever the shape, so
+    # every call on one workspace draws a new generation; no other part of
+    # any shape's layout covers the 16 bytes of control words, and the parts
+    # of one shape do not overlap.
+    seen = 0
+    for qtype, N, K, M in _split_shapes():
+        lay = va.workspace_layout(qtype, N, K, M)
+        if lay["sums"] is None:
+            continue
+        seen += 1
+        assert lay["generation"] == 0 and lay["missed"] == 4, (qtype, N, K, M)
+        assert lay["counters"] == 16
+        n_blocks = (N + 7) // 8
+        assert lay["counters"] + 4 * n_blocks <= lay["xq"]
+        assert lay["xq"] % 16 == 0 and lay["xs"] % 16 == 0 and lay["sums"] % 16 == 0
+        assert lay["xq"] + 16 * K <= lay["xs"]
+        G = 32 if qtype == 8 else 64
+        assert lay["xs"] + (K // G) * 16 * 4 <= lay["sums"]
+        assert lay["sums"] + 4 * M * N * 8 == lay["total"] == va.workspace_bytes(qtype, N, K, M)
+    assert seen > 300
+    # shapes without the split keep the control words too (xq at 16)
+    lay = va.workspace_layout(4, 10240, 2560, 8)
+    assert lay["xq"] == 16 and lay["sums"] is None and lay["counters"] is None
+    assert va.workspace_layout(4, 10240, 2560, 1)["total"] == 0
+
+
+def test_split_tag_cannot_match_library_words():
+    # A slot is accepted when its high word equals the call's tag, whose top
+    # byte is 0x80.  The other words the library stores in a workspace are
+    # int8 activations, fp32 activation scales and counters (at most 4): the
+    # quantizer's bytes never include 0x80 (|q| <= 127, also for groups
+    # holding the largest finite bf16 values, and the device quantizer equals
+    # the oracle's on every finite bf16 pair, test_device_quantizer_exhaustive)
+    # and its scales are positive (bit 31 clear, unlike every tag).
+    import numpy as np
+    import oracle as O
+    rng = np.random.default_rng(0x7A6)
+    x = (rng.standard_normal((4, 4096)) * np.exp(rng.uniform(-30, 30, (4, 1)))).astype(np.float32)
+    x[0, :64] = np.float32(3.3895e38)                      # the largest bf16 magnitudes
+    x[1, 64:128] = -np.float32(3.3895e38)
+    x[2, 128:192] = 0.0
+    x[3, 192:256] = np.float32(1e-38)
+    xb = O.f32_to_bf16(x)
+    for G in (64, 32):
+        q, s = O.quantize_act(xb, G)
+        assert 0x80 not in set(np.asarray(q, dtype=np.int8).view(np.uint8).ravel().tolist())
+        sb = np.asarray(s, dtype=np.float32).view(np.uint32)
+        assert np.all((sb & np.uint32(0x80000000)) == 0)
+    assert all((0x80000000 | (g & 0xFFFFFF)) >> 24 == 0x80 for g in (0, 1, 0xFFFFFF, 0x1000000, 0xFFFFFFFF))
 
 
 FAKE = 0x10000  # never dereferenced: every call below fails validation first

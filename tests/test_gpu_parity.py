@@ -165,9 +165,9 @@ def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
 
 # Long K on the matrix cores (K of 24..80 quads of 4 groups, a multiple of 4
 # quads) splits K in 4 parts, one workgroup each; the last part of a row block
-# to finish adds the parts' sums in part order.  The workspace starts as
-# garbage (the quantize launch clears the counters) and serves a second call
-# with another row count; a repeated call must give the same bits.
+# to finish adds the parts' sums in part order.  The workspace starts zeroed
+# (the contract) and serves a second call with another row count; a repeated
+# call must give the same bits.
 @pytest.mark.parametrize("qtype", FORMATS)
 @pytest.mark.parametrize("N,K,M,M2,senc", [
     (2560, 10240, 16, 4, O.SCALE_FP16),   # down shape
@@ -182,7 +182,7 @@ def test_k_split(torch_dev, qtype, N, K, M, M2, senc):
     w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G,
                            va.ScaleEnc(senc))
     nws = max(va.workspace_bytes(qtype, N, K, m) for m in (M, M2))
-    ws = torch.full((nws,), 255, dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
     for m, residual in ((M, True), (M2, False)):
         note(f"case qtype={qtype} N={N} K={K} M={m} senc={senc} res={residual}")
         x = O.gen_act(m, K, 5200 + m)
@@ -197,6 +197,7 @@ def test_k_split(torch_dev, qtype, N, K, M, M2, senc):
             outs.append(host(yd, np.uint16))
         O.assert_bf16_close(outs[0], y_ref, absterm, rel=REL_TOL)
         np.testing.assert_array_equal(outs[1], outs[0])
+    assert missed_sums(ws) == 0
 
 
 # Seeded random shapes on the K split: K of 24..80 quads (every multiple of
@@ -233,7 +234,7 @@ def test_k_split_alternating_inputs(torch_dev):
                            va.ScaleEnc(O.SCALE_FP16))
     xs = [O.gen_act(M, K, 5601), O.gen_act(M, K, 5602)]
     refs = [O.qlinear(qtype, packed, scales, O.SCALE_FP16, N, K, x) for x in xs]
-    ws = torch.full((va.workspace_bytes(qtype, N, K, M),), 255, dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(va.workspace_bytes(qtype, N, K, M), dtype=torch.uint8, device="cuda")
     xds = [dev(torch, x) for x in xs]
     for i in range(6):
         note(f"alternating call {i}")
@@ -242,6 +243,69 @@ def test_k_split_alternating_inputs(torch_dev):
         torch.cuda.synchronize()
         y_ref, _, absterm = refs[i % 2]
         O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
+    assert missed_sums(ws) == 0
+
+
+def missed_sums(ws):
+    """The workspace's count of K-split sums that never arrived (offset 4)."""
+    return int(ws[4:8].cpu().numpy().view(np.uint32)[0])
+
+
+def _split_case(torch, qtype, N, K, M, seed, senc=O.SCALE_FP16, residual=False):
+    G = O.group_size(qtype)
+    packed, scales = O.gen_weights(qtype, N, K, seed, senc)
+    x = O.gen_act(M, K, seed + 1)
+    res = O.gen_act(M, N, seed + 2) if residual else None
+    y_ref, _, absterm = O.qlinear(qtype, packed, scales, senc, N, K, x, residual=res)
+    xq, _ = O.quantize_act(x, G)
+    D_ref = O.group_dots(qtype, packed, N, K, xq)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, va.ScaleEnc(senc))
+    return dict(shape=(qtype, N, K, M), w=w, x=dev(torch, x), res=None if res is None else dev(torch, res),
+                y_ref=y_ref, absterm=absterm, D_ref=D_ref)
+
+
+def _run_split_case(torch, c, ws, i):
+    qtype, N, K, M = c["shape"]
+    note(f"call {i}: qtype={qtype} N={N} K={K} M={M}")
+    assert va.workspace_layout(qtype, N, K, M)["sums"] is not None        # this shape runs the K split
+    yd = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    pd = torch.full((M, N, K // O.group_size(qtype)), -7, dtype=torch.int32, device="cuda")
+    assert va.linear_partials(c["w"], c["x"], yd, pd, residual=c["res"], workspace=ws).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(pd, np.int32), c["D_ref"])
+    O.assert_bf16_close(host(yd, np.uint16), c["y_ref"], c["absterm"], rel=REL_TOL)
+
+
+# Split shapes of different sizes alternating on one zeroed workspace: the
+# generation word sits at offset 0 for every shape, so every call draws a new
+# one; with a shape-dependent generation word these two shapes would reuse
+# generation 5 from the 5th call on (the small call's word is a counter of
+# the large call's) and could accept the other call's sums.  Every call is
+# checked against the oracle (group dots bit-exact), and no sum may miss.
+def test_k_split_shapes_alternate_on_one_workspace(torch_dev):
+    torch = torch_dev
+    cases = [_split_case(torch, O.Q4_G64, 2048, 10240, 5, 0x5A10),
+             _split_case(torch, O.Q4_G64, 640, 10240, 16, 0x5A20, residual=True)]
+    nws = max(va.workspace_bytes(*c["shape"]) for c in cases)
+    ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
+    for i in range(10):
+        _run_split_case(torch, cases[i % 2], ws, i)
+    assert missed_sums(ws) == 0
+
+
+# Growing sequences on one zeroed workspace (each call's slot region covers
+# more of the workspace than the last): M = 5 -> 6 -> 16 at the down shape,
+# then N = 1000 -> 2560, then another format and K on the same bytes.
+def test_k_split_growing_sequence_one_workspace(torch_dev):
+    torch = torch_dev
+    shapes = [(O.Q4_G64, 2560, 10240, 5), (O.Q4_G64, 2560, 10240, 6), (O.Q4_G64, 2560, 10240, 16),
+              (O.Q4_G64, 1000, 10240, 16), (O.Q4_G64, 2560, 10240, 16), (O.W8_G32, 2048, 6144, 9),
+              (O.Q5_G64, 2560, 12288, 12), (O.Q4_G64, 1000, 10240, 5)]
+    nws = max(va.workspace_bytes(*s) for s in shapes)
+    ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
+    for i, (qtype, N, K, M) in enumerate(shapes):
+        _run_split_case(torch, _split_case(torch, qtype, N, K, M, 0x5B00 + 17 * i, residual=(i % 3 == 1)), ws, i)
+    assert missed_sums(ws) == 0
 
 
 def test_k_split_two_streams_concurrent(torch_dev):
@@ -256,7 +320,7 @@ def test_k_split_two_streams_concurrent(torch_dev):
         w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, 64,
                                va.ScaleEnc(O.SCALE_FP16))
         x = dev(torch, O.gen_act(M, K, seed + 1))
-        ws = torch.full((va.workspace_bytes(qtype, N, K, M),), 255, dtype=torch.uint8, device="cuda")
+        ws = torch.zeros(va.workspace_bytes(qtype, N, K, M), dtype=torch.uint8, device="cuda")
         y0 = torch.zeros((M, N), dtype=torch.int16, device="cuda")
         assert va.linear(w, x, y0, workspace=ws).ok()
         cases.append((w, x, ws, y0))
@@ -358,8 +422,7 @@ def test_k_split_graph_replays(torch_dev):
     x, x2 = O.gen_act(M, K, 5401), O.gen_act(M2, K, 5402)
     res = O.gen_act(M, N, 5403)
     xd, x2d, rd = dev(torch, x), dev(torch, x2), dev(torch, res)
-    ws = torch.full((max(va.workspace_bytes(qtype, N, K, m) for m in (M, M2)),), 255, dtype=torch.uint8,
-                    device="cuda")
+    ws = torch.zeros(max(va.workspace_bytes(qtype, N, K, m) for m in (M, M2)), dtype=torch.uint8, device="cuda")
     ye = torch.zeros((M, N), dtype=torch.int16, device="cuda")
     assert va.linear(w, xd, ye, residual=rd, workspace=ws).ok()
     torch.cuda.synchronize()

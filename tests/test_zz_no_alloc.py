@@ -1,10 +1,11 @@
 """The allocation-free entry point viper_hip_qlinear_static, through the C ABI.
 
 Its output must equal viper_hip_qlinear's (same kernels, caller workspace) bit
-for bit, on calls in a row on one GPU, each later call smaller than the one
-before (the static array keeps the previous call's contents: K-split counters
-and sums, activation fragments).  Shapes past the static array are rejected
-before any device work.
+for bit and the oracle's to the parity bar, on calls in a row on one GPU: the
+static array keeps the previous call's contents (K-split control words and
+sums, activation fragments), so sequences shrink, grow and alternate between
+K-split shapes.  Shapes past the static array are rejected before any device
+work.
 """
 import ctypes as C
 
@@ -38,7 +39,7 @@ def _call_pair(torch, L, qtype, N, K, M, seed, residual):
     wd, sd, xd = _dev(torch, packed), _dev(torch, scales), _dev(torch, x)
     rd = _dev(torch, O.gen_act(M, N, seed + 2)) if residual else None
     nws = L.viper_hip_qlinear_workspace_bytes(qtype, N, K, M)
-    ws = torch.full((max(nws, 16),), 255, dtype=torch.uint8, device="cuda")
+    ws = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda")
     y_ref = torch.zeros((M, N), dtype=torch.int16, device="cuda")
     y_st = torch.full((M, N), 7, dtype=torch.int16, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
@@ -51,18 +52,26 @@ def _call_pair(torch, L, qtype, N, K, M, seed, residual):
     assert rc == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(y_st.cpu().numpy(), y_ref.cpu().numpy())
+    res = None if rd is None else O.gen_act(M, N, seed + 2)
+    y_o, _, absterm = O.qlinear(qtype, packed, scales, O.SCALE_FP16, N, K, x, residual=res)
+    O.assert_bf16_close(y_st.cpu().numpy().view(np.uint16), y_o, absterm, rel=1e-5)
     return y_st
 
 
-# (qtype, N, K, M) sequences, each call smaller than the one before it:
-# the K split (long K) with its counters, sums and generation word, the
-# fragment quantize + matrix-core path, the multi-row path, and M = 1 (no
-# workspace at all).
+# (qtype, N, K, M) sequences: shrinking (the K split (long K) with its
+# control words and sums, the fragment quantize + matrix-core path, the
+# multi-row path, and M = 1 with no workspace at all), growing (each call's
+# K-split sums cover more of the array than the last) and two K-split shapes
+# alternating (with a shape-dependent generation word they would share
+# generation 5 from the 5th call on).
 SEQUENCES = [
     [(O.Q4_G64, 2560, 10240, 16), (O.Q4_G64, 1000, 10240, 5)],
     [(O.W8_G32, 2048, 10240, 12), (O.W8_G32, 777, 6144, 4)],
     [(O.Q5_G64, 10240, 2560, 16), (O.Q5_G64, 4000, 2560, 8)],
     [(O.Q4_G64, 10240, 2560, 8), (O.Q4_G64, 2560, 2560, 2), (O.Q4_G64, 2560, 2560, 1)],
+    [(O.Q4_G64, 2560, 10240, 5), (O.Q4_G64, 2560, 10240, 6), (O.Q4_G64, 2560, 10240, 16),
+     (O.Q4_G64, 1000, 10240, 16), (O.Q4_G64, 2560, 10240, 16)],
+    [(O.Q4_G64, 2048, 10240, 5), (O.Q4_G64, 640, 10240, 16)] * 5,
 ]
 
 

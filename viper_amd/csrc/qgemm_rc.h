@@ -107,25 +107,35 @@ struct RcSeg {
 // for the partials and natural-layout variants.  SK > 1 (fragment input
 // only): K split into SK equal parts, one workgroup per (row block, part),
 // blockIdx = SK * block + part; each part stores its fp32 sums to sp
-// [SK][M][N], and the last part of a block to arrive (counter sc[block],
-// zeroed by the fragment quantize launch) adds the SK sums in part order, so
-// the result does not depend on which part finishes last.  Partials (PART)
-// are written by each part for its own groups.  PR: the launch may carry a
-// fused pair (without it the matrix select is not compiled).
+// [SK][M][N], and the last part of a block to arrive (counter
+// sc[RC_CTL_CNT + block], zeroed by the fragment quantize launch) adds the SK
+// sums in part order, so the result does not depend on which part finishes
+// last.  Partials (PART) are written by each part for its own groups.  PR:
+// the launch may carry a fused pair (without it the matrix select is not
+// compiled).
 //
 // The exchange between the parts of a block.  Each sum travels in a 64-bit
-// slot {generation, fp32 bits}, written and read as agent-scope relaxed
-// atomics; the generation is the word after the counters, which the fragment
-// quantize launch increments once per call.  The last part accepts a slot
-// only when it carries the current generation and re-reads it otherwise
-// (bounded by RC_SPIN, then NaN).  So a sum from an earlier call on the same
-// workspace can never be consumed: the result depends only on the coherence
-// of the atomic accesses to each slot, not on any ordering between the
-// slots and the counter.  (An agent-scope release/acquire pair would order
-// them but costs a write-back and an invalidate of the XCD's L2 per
-// workgroup: 70 us on the down shape.)  A part counts as soon as its slot
-// stores are issued; the last part requests every slot at once, then
-// re-reads any that still holds an earlier generation.
+// slot {tag, fp32 bits}, written and read as agent-scope relaxed atomics.
+// sc points at the workspace's control words, at offset 0 for every shape:
+// sc[RC_CTL_GEN] is the generation, which the fragment quantize launch
+// increments once per call, so every call on one workspace, whatever its
+// shape, draws a new one; the tag is rc_tag(generation): top byte 0x80, the
+// generation's low 24 bits below it.  No other word the library stores in a
+// workspace can equal a tag: int8 activations are in [-127, 127] (never the
+// byte 0x80), fp32 activation scales are positive, counters are at most SK.
+// So in a workspace zero-filled before its first use, a slot that carries
+// this call's tag was written by this call (a slot written 2^24 calls
+// earlier and not rewritten since is the only exception).  The last part
+// accepts a slot only when it carries the current tag and re-reads it
+// otherwise (bounded by RC_SPIN; then the output is NaN and
+// sc[RC_CTL_MISS] is incremented, a count the library never clears).  So
+// the result depends only on the coherence of the atomic accesses to each
+// slot, not on any ordering between the slots and the counter.  (An
+// agent-scope release/acquire pair would order them but costs a write-back
+// and an invalidate of the XCD's L2 per workgroup: 70 us on the down shape.)
+// A part counts as soon as its slot stores are issued; the last part
+// requests every slot at once, then re-reads any that does not yet carry
+// the current tag.
 template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, int SK = 1, bool PR = true>
 __global__ void __launch_bounds__(64 * W)
 qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
@@ -503,12 +513,11 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     constexpr int MINE = (4 * T + W - 1) / W;
     float mine[MINE] = {};
     const int kpart = SK > 1 ? (int)(blockIdx.x % SK) : 0;
-    // K split: this call's generation (the word after the counters, written by
-    // the preceding quantize launch), read once the sums are formed: issued
-    // earlier as a vector load among the weights it cost 2 us of the
-    // down-shape launch
-    unsigned gen = 0;
-    if constexpr (SK > 1) gen = sc[(N + 7) / 8];
+    // K split: this call's tag (from the generation the preceding quantize
+    // launch wrote), read once the sums are formed: issued earlier as a
+    // vector load among the weights it cost 2 us of the down-shape launch
+    unsigned tag = 0;
+    if constexpr (SK > 1) tag = rc_tag(sc[RC_CTL_GEN]);
 #pragma unroll
     for (int i = 0; i < MINE; ++i) {
         const int sl = wave + i * W;
@@ -522,7 +531,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         if (m < M && nl < nrows) {
             const size_t o = (size_t)m * N + row0 + nl;
             if constexpr (SK > 1) {
-                __hip_atomic_store(sp + (size_t)kpart * M * N + o, ((uint64_t)gen << 32) | __float_as_uint(v),
+                __hip_atomic_store(sp + (size_t)kpart * M * N + o, ((uint64_t)tag << 32) | __float_as_uint(v),
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
@@ -536,13 +545,13 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         // for the stores to complete before counting measured 0.4 us slower)
         lds_barrier();
         int* last = (int*)red;
-        if (tid == 0) last[0] = atomicAdd(sc + bid, 1u) == (unsigned)(SK - 1);
+        if (tid == 0) last[0] = atomicAdd(sc + RC_CTL_CNT + bid, 1u) == (unsigned)(SK - 1);
         lds_barrier();
         if (!last[0]) return;
         // every slot of the other parts is requested at once (a load that
         // waited for the previous one's tag would serialise the round trips:
         // 0.4 us of the down-shape launch), then the tags are checked and a
-        // slot still holding an earlier generation is re-read
+        // slot that does not carry this call's tag yet is re-read
         uint64_t u[MINE][SK];
 #pragma unroll
         for (int i = 0; i < MINE; ++i) {
@@ -553,7 +562,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
             const size_t o = (size_t)m * N + row0 + nl;
 #pragma unroll
             for (int p = 0; p < SK; ++p) {
-                u[i][p] = ((uint64_t)gen << 32) | __float_as_uint(mine[i]);
+                u[i][p] = ((uint64_t)tag << 32) | __float_as_uint(mine[i]);
                 if (ok && p != kpart)
                     u[i][p] = __hip_atomic_load(sp + (size_t)p * M * N + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
@@ -570,12 +579,17 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
 #pragma unroll
                 for (int p = 0; p < SK; ++p) {
                     uint64_t w = u[i][p];
-                    if (__builtin_expect((unsigned)(w >> 32) != gen, 0)) {
+                    if (__builtin_expect((unsigned)(w >> 32) != tag, 0)) {
                         uint64_t* a = sp + (size_t)p * M * N + o;
-                        for (int it = 0; (unsigned)(w >> 32) != gen && it < RC_SPIN; ++it)
+                        for (int it = 0; (unsigned)(w >> 32) != tag && it < RC_SPIN; ++it)
                             w = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
-                    v += (unsigned)(w >> 32) == gen ? __uint_as_float((unsigned)w) : __builtin_nanf("");
+                    if (__builtin_expect((unsigned)(w >> 32) != tag, 0)) {
+                        __hip_atomic_fetch_add(sc + RC_CTL_MISS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        v += __builtin_nanf("");
+                    } else {
+                        v += __uint_as_float((unsigned)w);
+                    }
                 }
                 if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
                 y[o] = f2bf(v);

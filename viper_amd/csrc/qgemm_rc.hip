@@ -57,9 +57,7 @@ bool rc_split_ok(int qtype, int K) {
     return G != 0 && K % (4 * G) == 0 && rc_split_fits(K / G / 4);
 }
 
-size_t rc_split_bytes(int N, int M) {
-    return align16((size_t)RC_SK * M * N * 8) + align16((size_t)(rc_split_counters(N) + 1) * 4);
-}
+size_t rc_split_bytes(int N, int M) { return align16((size_t)RC_SK * M * N * 8); }
 
 bool rc_ok(int qtype, int K) {
     const int G = group_of(qtype);

@@ -65,31 +65,30 @@ static int scratch_address(void** out) {
 
 // ------------------------------------------------ standalone activation quantize
 
-// The K split's generation word (after its counters): one increment per
-// call, by one thread of the quantize launch that precedes the split launch
-// on the stream (so the split launch sees it).  Written through like the
-// counters.
-__device__ __forceinline__ void bump_generation(unsigned* gen) {
-    const unsigned v = __hip_atomic_load(gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(gen, v + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// The K split's control words (ctl, offset 0 of the workspace): the quantize
+// launch that precedes the split launch on the stream clears the ncnt block
+// counters and increments the generation once per call (one thread), so the
+// split launch sees both.  Written through.
+__device__ __forceinline__ void reset_split_control(unsigned* ctl, int ncnt, int i0, int stride) {
+    const auto cw = buf(ctl + RC_CTL_CNT, (uint32_t)ncnt * 4u);
+    for (int i = i0; i < ncnt; i += stride) bstore4<AUX_SC1>(cw, i * 4, 0u);
+    if (ncnt > 0 && i0 == 0) {
+        const unsigned v = __hip_atomic_load(ctl + RC_CTL_GEN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(ctl + RC_CTL_GEN, v + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 }
 
 // MF: the fragment order the matrix-core kernels read (xs transposed to
 // [K/G][16]; 64-groups use quantize_frag64_kernel); else xq [M][K] in k order
 // and xs [M][K/G].
-// Both fragment-order quantizers also clear the ncnt counters of a K-split
-// matrix-core launch that follows (written through, like their outputs).
+// Both fragment-order quantizers also reset the control words of a K-split
+// matrix-core launch that follows (ncnt > 0).
 template <int G, bool MF>
 __global__ void __launch_bounds__(NT)
 quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
-                    float* __restrict__ xs, int oct_total, int K, unsigned* __restrict__ cnt, int ncnt) {
+                    float* __restrict__ xs, int oct_total, int K, unsigned* __restrict__ ctl, int ncnt) {
     const int o = (int)blockIdx.x * NT + (int)threadIdx.x;
-    if constexpr (MF) {
-        const int stride = (oct_total + NT - 1) / NT * NT;
-        const auto cw = buf(cnt, (uint32_t)ncnt * 4u);
-        for (int i = o; i < ncnt; i += stride) bstore4<AUX_SC1>(cw, i * 4, 0u);
-        if (ncnt > 0 && o == 0) bump_generation(cnt + ncnt);
-    }
+    if constexpr (MF) reset_split_control(ctl, ncnt, o, (oct_total + NT - 1) / NT * NT);
     const bool ok = o < oct_total;
     u32x4 v = {0u, 0u, 0u, 0u};
     if (ok) v = *(const u32x4*)(x + (size_t)o * 8);
@@ -126,13 +125,9 @@ quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
 // m + 48).  Rows m >= M are neither read nor written.
 __global__ void __launch_bounds__(64)
 quantize_frag64_kernel(const uint16_t* x, int M, int K, int8_t* __restrict__ xq, float* __restrict__ xs,
-                       unsigned* __restrict__ cnt, int ncnt) {
+                       unsigned* __restrict__ ctl, int ncnt) {
     const int L = (int)threadIdx.x, g = (int)blockIdx.x;
-    {
-        const auto cw = buf(cnt, (uint32_t)ncnt * 4u);
-        for (int i = g * 64 + L; i < ncnt; i += K) bstore4<AUX_SC1>(cw, i * 4, 0u);  // K threads in the grid
-        if (ncnt > 0 && g == 0 && L == 0) bump_generation(cnt + ncnt);
-    }
+    reset_split_control(ctl, ncnt, g * 64 + L, K);  // K threads in the grid
     const int m = L & 15, kb = L >> 4, qi = ((kb & 1) << 1) | (kb >> 1);
     const bool ok = m < M;
     const auto xr = buf(x, (uint32_t)M * (uint32_t)K * 2u);
@@ -211,7 +206,7 @@ __global__ void __launch_bounds__(NT) check_quantizer_kernel(int ab0, int32_t* _
 }
 
 static int launch_quantize(int group, const void* x, int M, int K, void* xq, void* xs, bool mf,
-                           hipStream_t st, unsigned* cnt = nullptr, int ncnt = 0) {
+                           hipStream_t st, unsigned* ctl = nullptr, int ncnt = 0) {
     const int oct_total = M * K / 8;
     const unsigned grid = (unsigned)((oct_total + NT - 1) / NT);
     const uint16_t* a0 = (const uint16_t*)x;
@@ -219,11 +214,11 @@ static int launch_quantize(int group, const void* x, int M, int K, void* xq, voi
     float* a2 = (float*)xs;
     if (ncnt > 0 && !mf) return VIPER_INTERNAL;
     if (mf && group == 64) {
-        void* fargs[] = {&a0, &M, &K, &a1, &a2, &cnt, &ncnt};
+        void* fargs[] = {&a0, &M, &K, &a1, &a2, &ctl, &ncnt};
         launch((const void*)quantize_frag64_kernel, (unsigned)(K / 64), 64, 0, st, fargs);
         return status_of(hipGetLastError());
     }
-    void* args[] = {&a0, &a1, &a2, (void*)&oct_total, &K, &cnt, &ncnt};
+    void* args[] = {&a0, &a1, &a2, (void*)&oct_total, &K, &ctl, &ncnt};
     const void* fn;
     if (group == 64) fn = (const void*)quantize_act_kernel<64, false>;
     else fn = mf ? (const void*)quantize_act_kernel<32, true> : (const void*)quantize_act_kernel<32, false>;
@@ -237,20 +232,34 @@ static bool fused_ok(int qtype, int M, int K) {
     return M == 1 && lds_m1(qtype, K) <= (size_t)LDS_MAX;
 }
 
-// xq ([M][K], or fragment order with room for 16 rows), then xs ([M][K/G],
-// or [K/G][16]) fp32, then (long K on the matrix cores) the K split's part
-// sums and counters.
+// Workspace of a call with M > 1 (zero-filled before its first use): the
+// K split's control words at offset 0 for every shape (generation, missed
+// sums; 16 bytes), its block counters, then xq ([M][K], or fragment order
+// with room for 16 rows), xs ([M][K/G], or [K/G][16]) fp32 and (long K on
+// the matrix cores) the K split's part sums.  Offsets in bytes.
+struct WsLayout {
+    size_t cnt, xq, xs, sp, total;
+    bool split;
+};
+constexpr size_t WS_CTL_BYTES = 16;
 static size_t workspace_xq(int K) { return align16((size_t)16 * K); }
 static size_t workspace_xs(int qtype, int K) { return align16((size_t)(K / group_of(qtype)) * 16 * 4); }
 
-static size_t workspace_need(int qtype, int N, int K, int M) {
+static WsLayout workspace_layout(int qtype, int N, int K, int M) {
+    WsLayout l{0, 0, 0, 0, 0, false};
     const int G = group_of(qtype);
-    if (G == 0 || M <= 0 || K <= 0 || N <= 0) return 0;
-    if (fused_ok(qtype, M, K)) return 0;
-    size_t need = workspace_xq(K) + workspace_xs(qtype, K);
-    if (M >= 2 && M <= 16 && rc_split_ok(qtype, K)) need += rc_split_bytes(N, M);
-    return need;
+    if (G == 0 || M <= 0 || K <= 0 || N <= 0 || K % G != 0) return l;
+    if (fused_ok(qtype, M, K)) return l;
+    l.split = M >= 2 && M <= 16 && rc_split_ok(qtype, K);
+    l.cnt = (size_t)RC_CTL_CNT * 4;
+    l.xq = WS_CTL_BYTES + (l.split ? align16((size_t)rc_split_counters(N) * 4) : 0);
+    l.xs = l.xq + workspace_xq(K);
+    l.sp = l.xs + workspace_xs(qtype, K);
+    l.total = l.sp + (l.split ? rc_split_bytes(N, M) : 0);
+    return l;
 }
+
+static size_t workspace_need(int qtype, int N, int K, int M) { return workspace_layout(qtype, N, K, M).total; }
 
 // Optional second matrix of the same shape applied to the same activation in
 // the same launch (the reference's fused2: k and v, gate and up).
@@ -330,12 +339,15 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     }
     const bool staged = mf && mfma_staged(qtype, N, K);
     if (!mf && lds_pre(qtype, M, K) > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
-    uint8_t* xq = (uint8_t*)wsp;
-    float* xs = (float*)(xq + workspace_xq(K));
-    // long K on the matrix cores: the K split (parts' sums and counters after xs)
+    const WsLayout lay = workspace_layout(qtype, N, K, M);
+    if (split_ok && !lay.split) return VIPER_INTERNAL;
+    uint8_t* xq = (uint8_t*)wsp + lay.xq;
+    float* xs = (float*)((uint8_t*)wsp + lay.xs);
+    // long K on the matrix cores: the K split (control words at the
+    // workspace's start, part sums after xs)
     const bool split = split_ok;
-    uint64_t* sp = split ? (uint64_t*)((uint8_t*)xs + workspace_xs(qtype, K)) : nullptr;
-    unsigned* sc = split ? (unsigned*)((uint8_t*)sp + align16((size_t)RC_SK * M * N * 8)) : nullptr;
+    uint64_t* sp = split ? (uint64_t*)((uint8_t*)wsp + lay.sp) : nullptr;
+    unsigned* sc = split ? (unsigned*)wsp : nullptr;
     rc = launch_quantize(group, x, M, K, xq, xs, staged, st, sc, split ? rc_split_counters(N) : 0);
     if (rc != VIPER_OK) return rc;
     if (mf)
@@ -383,8 +395,20 @@ extern "C" int viper_hip_abi_version(void) { return VIPER_QLINEAR_ABI_VERSION; }
 extern "C" int viper_hip_group_size(int qtype) { return vq::group_of(qtype); }
 
 extern "C" size_t viper_hip_qlinear_workspace_bytes(int qtype, int N, int K, int M) {
-    (void)N;
     return vq::workspace_need(qtype, N, K, M);
+}
+
+extern "C" size_t viper_hip_qlinear_workspace_layout(int qtype, int N, int K, int M, size_t* offsets) {
+    const vq::WsLayout l = vq::workspace_layout(qtype, N, K, M);
+    if (offsets != nullptr) {
+        offsets[0] = (size_t)vq::RC_CTL_GEN * 4;
+        offsets[1] = (size_t)vq::RC_CTL_MISS * 4;
+        offsets[2] = l.split ? l.cnt : SIZE_MAX;
+        offsets[3] = l.total ? l.xq : SIZE_MAX;
+        offsets[4] = l.total ? l.xs : SIZE_MAX;
+        offsets[5] = l.split ? l.sp : SIZE_MAX;
+    }
+    return l.total;
 }
 
 extern "C" int viper_hip_qlinear(int qtype, const void* w_packed, const void* w_scales,

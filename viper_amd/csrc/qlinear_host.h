@@ -128,12 +128,19 @@ enum { RC_FRAG = 0, RC_NAT = 1, RC_BF16 = 2 };
 bool rc_ok(int qtype, int K);
 bool rc_bf16_ok(int qtype, int N, int K, int M, bool pair);
 // K split of the fragment-input launch (long K): sp = the parts' sums
-// [4][M][N] as 64-bit {generation, fp32} slots, sc = one counter per row
-// block (rc_split_counters(N) of them, zero when the launch starts) followed
-// by the generation word; the fragment quantize launch clears the counters
-// and increments the generation.  All in the caller's workspace,
-// rc_split_bytes(N, M) bytes.
+// [4][M][N] as 64-bit {tag, fp32} slots; sc = the workspace's control words
+// (at offset 0 of every workspace): sc[RC_CTL_GEN] the generation (one per
+// call), sc[RC_CTL_MISS] the count of sums that never arrived (outputs NaN;
+// never cleared by the library), then from sc[RC_CTL_CNT] one counter per row
+// block (rc_split_counters(N) of them, zero when the launch starts).  The
+// fragment quantize launch clears the counters and increments the
+// generation.  rc_split_bytes(N, M): the sums' bytes.
 constexpr int RC_SK = 4;  // parts of the K split
+constexpr int RC_CTL_GEN = 0, RC_CTL_MISS = 1, RC_CTL_CNT = 4;
+// The tag a call's slots carry: top byte 0x80 (no int8 activation byte, fp32
+// activation scale or counter the workspace holds can have it), then the
+// generation's low 24 bits.
+__host__ __device__ constexpr unsigned rc_tag(unsigned gen) { return 0x80000000u | (gen & 0x00FFFFFFu); }
 bool rc_split_ok(int qtype, int K);
 inline int rc_split_counters(int N) { return (N + 7) / 8; }
 size_t rc_split_bytes(int N, int M);

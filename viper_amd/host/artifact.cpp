@@ -15,6 +15,7 @@
 
 #include <climits>
 #include <cstring>
+#include <new>
 
 #include <hip/hip_runtime_api.h>
 
@@ -62,7 +63,23 @@ usize align_up(usize v) { return (v + kAlign - 1) / kAlign * kAlign; }
 
 }  // namespace
 
+static Status parse_sections(const u8* data, usize size, Index* out);
+
+// Host allocations (the index vectors, the messages) are the only thing that
+// can throw in here; the API returns Status and never throws.
 Status parse(const u8* data, usize size, Index* out) {
+    try {
+        return parse_sections(data, size, out);
+    } catch (const std::bad_alloc&) {
+        if (out != nullptr) *out = Index();
+        return Status(StatusCode::OUT_OF_MEMORY, "artifact: host allocation failed while indexing");
+    } catch (...) {
+        if (out != nullptr) *out = Index();
+        return Status(StatusCode::INTERNAL, "artifact: unexpected exception while indexing");
+    }
+}
+
+static Status parse_sections(const u8* data, usize size, Index* out) {
     if (out == nullptr || (data == nullptr && size != 0)) return invalid("null argument");
     *out = Index();
     if (size < kHeaderBytes) return io("shorter than the 56-byte header");
@@ -86,6 +103,23 @@ Status parse(const u8* data, usize size, Index* out) {
     if (H % 64 || I % 64 || nQ % 64) return invalid("hidden, intermediate and n_heads*head_dim must be multiples of 64");
     const u64 rows[N_LINEAR] = {nQ, nKV, nKV, H, I, I, H};
     const u64 cols[N_LINEAR] = {H, H, H, nQ, H, H, I};
+
+    // The header's layer and pass counts are untrusted: before anything is
+    // sized by them, the sections they imply must fit the file.  Per (layer,
+    // pass): 7 linears of two sections each and 2 norms, each section 8 bytes
+    // of size plus its data.
+    u64 per_layer = 2 * (8 + H * 2);
+    for (int i = 0; i < N_LINEAR; ++i) {
+        u64 np = 0, ns = 0;
+        if (!q4_packed(rows[i], cols[i], &np) || !q4_scales(rows[i], cols[i], &ns) ||
+            __builtin_add_overflow(per_layer, 16 + np + ns, &per_layer))
+            return invalid("layer size overflows");
+    }
+    u64 layer_passes = 0, layers_bytes = 0;
+    if (!mul_ok((u64)hd.n_layers, (u64)hd.n_passes, &layer_passes) || !mul_ok(layer_passes, per_layer, &layers_bytes) ||
+        layers_bytes > (u64)(size - kHeaderBytes))
+        return io("the header's " + std::to_string(hd.n_layers) + " layers x " + std::to_string(hd.n_passes) +
+                  " passes need more bytes than the file holds");
 
     Reader r{data, size, kHeaderBytes};
     out->layers.resize(hd.n_layers);

@@ -115,6 +115,7 @@ _SYMBOLS = (
     "viper_hip_abi_version",
     "viper_hip_group_size",
     "viper_hip_qlinear_workspace_bytes",
+    "viper_hip_qlinear_workspace_layout",
     "viper_hip_qlinear",
     "viper_hip_quantize_act",
     "viper_hip_qlinear_prequantized",
@@ -152,6 +153,8 @@ def lib():
     L.viper_hip_group_size.argtypes, L.viper_hip_group_size.restype = [i32], i32
     L.viper_hip_qlinear_workspace_bytes.argtypes = [i32, i32, i32, i32]
     L.viper_hip_qlinear_workspace_bytes.restype = sz
+    L.viper_hip_qlinear_workspace_layout.argtypes = [i32, i32, i32, i32, vp]
+    L.viper_hip_qlinear_workspace_layout.restype = sz
     L.viper_hip_qlinear.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     L.viper_hip_qlinear.restype = i32
     L.viper_hip_quantize_act.argtypes = [i32, vp, i32, i32, vp, vp, vp]
@@ -233,7 +236,23 @@ def _status(rc: int, what: str) -> Status:
 
 
 def workspace_bytes(qtype, N, K, M) -> int:
+    """Bytes of the M > 1 workspace (zero-filled before its first use); 0 at M = 1."""
     return int(lib().viper_hip_qlinear_workspace_bytes(int(qtype), N, K, M))
+
+
+WS_PARTS = ("generation", "missed", "counters", "xq", "xs", "sums")
+
+
+def workspace_layout(qtype, N, K, M) -> dict:
+    """Byte offsets of the workspace's parts for this shape (None where the shape has none) and its
+    total size: the K split's generation word and missed-sum count (offsets 0 and 4 for every shape),
+    its block counters, xq, xs and the K split's part sums."""
+    off = (C.c_size_t * 6)()
+    total = int(lib().viper_hip_qlinear_workspace_layout(int(qtype), N, K, M, C.cast(off, C.c_void_p)))
+    none = (1 << (8 * C.sizeof(C.c_size_t))) - 1
+    out = {k: (None if int(v) == none else int(v)) for k, v in zip(WS_PARTS, off)}
+    out["total"] = total
+    return out
 
 
 def qlinear_raw(qtype, w, s, scale_enc, group, N, K, x, M, y, residual=None, workspace=None,
