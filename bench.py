@@ -144,6 +144,79 @@ def time_graph(torch, graph, replays):
     return e0.elapsed_time(e1)
 
 
+def clock_period(torch, L, launch, counts=(40, 120), replays=10):
+    """us per launch of back-to-back launch(i) calls on the GPU's own 100 MHz clock, independent of
+    HIP events and of a profiler: for each n in counts one HIP graph [clock stamp, launch(0..n-1),
+    clock stamp] (viper_hip_clock_stamp), replayed once untimed and then `replays` times; span(n) =
+    median of (second stamp - first stamp).  The least-squares slope of span over n is the period;
+    the stamps' own launches and the graph's entry and exit fall into the intercept.  Returns
+    (period_us, intercept_us, [(n, span_us), ...])."""
+    stamps = torch.zeros(2, dtype=torch.int64, device="cuda")
+
+    def stamp(k):
+        if L.viper_hip_clock_stamp(stamps.data_ptr() + 8 * k, torch.cuda.current_stream().cuda_stream) != 0:
+            raise RuntimeError("viper_hip_clock_stamp failed")
+    rows = []
+    for n in counts:
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            stamp(0)
+            for i in range(n):
+                launch(i)
+            stamp(1)
+        spans = []
+        for r in range(replays + 1):
+            g.replay()
+            torch.cuda.synchronize()
+            t = stamps.cpu().tolist()
+            if r:
+                spans.append((t[1] - t[0]) * 0.01)   # 100 MHz ticks -> us
+        del g
+        spans.sort()
+        rows.append((n, spans[len(spans) // 2]))
+    k = len(rows)
+    mx = sum(n for n, _ in rows) / k
+    my = sum(v for _, v in rows) / k
+    sxx = sum((n - mx) ** 2 for n, _ in rows)
+    slope = sum((n - mx) * (v - my) for n, v in rows) / sxx
+    return slope, my - slope * mx, rows
+
+
+def trace_summary(path, steps, warmup, copies=40):
+    """Summary of a rocprofv3 kernel-trace CSV of `bench.py --no-cpu --no-extras --steps S --warmup W`:
+    per kernel of this library and grid, dispatch count and mean / median / min / max duration (ns);
+    then, for the north-star GEMV, the dispatches of the timed region (in dispatch order: W * copies
+    eager warm-up launches, one untimed replay of the captured graphs, then the S * copies timed ones),
+    their summed duration and the span from the first one's start to the last one's end."""
+    import csv
+    rows = {}
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if "vq::" not in name:
+                continue
+            key = (name, int(r["Grid_Size_X"]) // max(1, int(r["Workgroup_Size_X"])), int(r["Workgroup_Size_X"]))
+            rows.setdefault(key, []).append((int(r["Dispatch_Id"]), int(r["Start_Timestamp"]), int(r["End_Timestamp"])))
+    for (name, wgs, nt), d in sorted(rows.items(), key=lambda kv: -len(kv[1])):
+        d.sort()
+        dur = sorted(e - b for _, b, e in d)
+        print(json.dumps({"kernel": name[:120], "workgroups": wgs, "threads": nt, "dispatches": len(d),
+                          "mean_ns": round(sum(dur) / len(dur), 1), "median_ns": dur[len(dur) // 2],
+                          "min_ns": dur[0], "max_ns": dur[-1]}), flush=True)
+    ns = [v for (n, wgs, nt), v in rows.items() if "qgemv_m1_kernel<4" in n and wgs == 512 and nt == 320]
+    if ns:
+        d = sorted(ns[0])
+        lo = warmup * copies + steps * copies
+        timed = d[lo:lo + steps * copies]
+        dur = [e - b for _, b, e in timed]
+        gaps = sorted(timed[i + 1][1] - timed[i][2] for i in range(len(timed) - 1))
+        print(json.dumps({"timed_dispatches": len(timed), "sum_duration_us": round(sum(dur) / 1e3, 2),
+                          "mean_duration_ns": round(sum(dur) / len(dur), 1),
+                          "span_us": round((timed[-1][2] - timed[0][1]) / 1e3, 2),
+                          "median_gap_ns": gaps[len(gaps) // 2] if gaps else None}), flush=True)
+
+
 def cpu_baseline(N, K, reps_1t, reps_mt):
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -394,6 +467,13 @@ def main():
                          "entry, x quantized once outside the timed calls), q5_m1 / q6_m8 / w8_m1 ... "
                          "(config 4), config1 / "
                          "config1_2launch (MLP), config3 (fused step) or config3_ref (reference launch sequence)")
+    ap.add_argument("--clock-period", action="store_true",
+                    help="only the north-star dispatch period on the device clock: back-to-back sequences of "
+                         "10..200 launches between two clock stamps, span per length and the fitted slope "
+                         "(JSON lines)")
+    ap.add_argument("--trace-summary", default="", metavar="CSV",
+                    help="only summarise a rocprofv3 kernel-trace CSV of this bench run with the same --steps "
+                         "and --warmup (no GPU needed)")
     ap.add_argument("--verify-only", type=int, default=0, metavar="M",
                     help="only time the M-row verify (K=2560, N=10240) line (rocprofv3 runs)")
     args = ap.parse_args()
@@ -402,6 +482,10 @@ def main():
               "output rows, each GPU running the same kernel on its share of N). Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
+
+    if args.trace_summary:
+        trace_summary(args.trace_summary, max(1, args.steps), max(0, args.warmup))
+        return
 
     import torch
     import viper_amd as va
@@ -478,6 +562,20 @@ def main():
         if rc != 0:
             raise RuntimeError(f"viper_hip_qlinear failed: {rc}")
 
+    if args.clock_period:
+        for i in range(20 * copies):
+            launch(i)
+        counts = (10, 20, 40, 80, 120, 160, 200)
+        for rep in range(3):
+            per, icpt, rows = clock_period(torch, L, launch, counts=counts, replays=20)
+            for n, span in rows:
+                print(json.dumps({"rep": rep, "launches": n, "span_us": round(span, 3)}), flush=True)
+            print(json.dumps({"rep": rep, "fit": "span = intercept + period * launches",
+                              "period_us": round(per, 4), "intercept_us": round(icpt, 3),
+                              "gbs": round(alg / (per * 1e-6) / 1e9, 1),
+                              "frac": round(alg / (per * 1e-6) / 1e9 / PEAK_GBS, 4)}), flush=True)
+        return
+
     # exactly --steps steps of `copies` dispatches each, after --warmup eager steps
     steps, warmup = max(1, args.steps), max(0, args.warmup)
     for i in range(warmup * copies):
@@ -504,6 +602,9 @@ def main():
     us_per_gemv = job_ms * 1e3 / dispatches
     value = alg * dispatches / (job_ms * 1e-3) / 1e9
     achieved = value
+    # the same dispatch period on the device's clock (slope over back-to-back sequences of 40 and 120
+    # launches): a cross-check of the events that no profiler perturbs
+    clk_us, clk_icpt, _ = clock_period(torch, L, launch)
 
     extras = {}
     if not args.no_extras:
@@ -691,7 +792,9 @@ def main():
                                     f"after {warmup} eager warm-up steps")},
         "us_per_gemv": round(us_per_gemv, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic},
+                     "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic,
+                     "us_per_launch": round(us_per_gemv, 3), "device_clock_us_per_launch": round(clk_us, 3),
+                     "device_clock_frac": round(alg / (clk_us * 1e-6) / 1e9 / PEAK_GBS, 4)},
         "cpu_baseline": cpu,
     }
     out.update(extras)

@@ -59,6 +59,8 @@
  *                                   M = 1 GEMV's load pattern and a given launch
  *                                   shape (measurement: the floor of one
  *                                   streaming dispatch).
+ *   viper_hip_clock_stamp           no counterpart: a device-clock reading between
+ *                                   launches (measurement).
  *
  * Formats (qtype values are viper::quant::QType, include/viper/quant.h:19-26):
  *   Q4_G64 (4)  packed [N][K/2]; k even in the low nibble; nibble = w + 8.
@@ -316,6 +318,12 @@ int viper_hip_qlinear_timeline(int qtype, const void* w_packed, const void* w_sc
  * if the folded data equals a fixed word. */
 int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, const void* side, int side_bytes,
                           void* y_bf16, uint32_t* sink, void* stream);
+
+/* Measurement probe, no counterpart in the reference: one launch of one
+ * wave that writes the GPU's constant 100 MHz counter (s_memrealtime) to
+ * out[0] (uint64, 8-byte aligned).  Two of them around a sequence of
+ * launches on one stream time the sequence on the device's clock. */
+int viper_hip_clock_stamp(uint64_t* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -800,6 +800,25 @@ def test_quantizer_edge_cases_every_path(torch_dev, qtype, M):
     O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
 
 
+def test_clock_stamp_probe(torch_dev):
+    # two device-clock readings around some work on one stream: ordered, within a second (100 MHz
+    # ticks); null and misaligned outputs are rejected before any launch
+    torch = torch_dev
+    L = va.lib()
+    t = torch.zeros(2, dtype=torch.int64, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.viper_hip_clock_stamp(t.data_ptr(), st) == 0
+    a = torch.randn(1 << 22, device="cuda")
+    for _ in range(4):
+        a = a * 1.0001
+    assert L.viper_hip_clock_stamp(t.data_ptr() + 8, st) == 0
+    torch.cuda.synchronize()
+    t0, t1 = t.cpu().tolist()
+    assert 0 < t1 - t0 < 100_000_000
+    assert L.viper_hip_clock_stamp(None, st) == 2
+    assert L.viper_hip_clock_stamp(t.data_ptr() + 4, st) == 2
+
+
 def test_stream_read_probe(torch_dev):
     # the measurement probe reads every byte: a lane whose chunks fold to the
     # magic word writes it to the sink, zeros leave the sink alone; with y,

@@ -1,5 +1,6 @@
-// Measurement probe (no counterpart in the reference): the floor of one
-// dispatch that streams a buffer with the M = 1 GEMV's load pattern.
+// Measurement probes (no counterpart in the reference): the floor of one
+// dispatch that streams a buffer with the M = 1 GEMV's load pattern, and a
+// reading of the device clock between launches.
 #include "qlinear_host.h"
 
 namespace vq {
@@ -64,7 +65,22 @@ static probe_fn probe_kernel(int threads, int loads) {
     }
 }
 
+// One reading of the GPU's constant-rate 100 MHz counter (s_memrealtime)
+// into out[0].  Placed on a stream before and after a sequence of launches,
+// it times that sequence on the device's own clock.
+__global__ void __launch_bounds__(64) clock_stamp_kernel(uint64_t* out) {
+    const uint64_t t = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) out[0] = t;
+}
+
 }  // namespace vq
+
+extern "C" int viper_hip_clock_stamp(uint64_t* out, void* stream) {
+    if (out == nullptr || vq::misaligned(out, 8)) return VIPER_INVALID_ARGUMENT;
+    void* args[] = {&out};
+    vq::launch((const void*)vq::clock_stamp_kernel, 1, 64, 0, (hipStream_t)stream, args);
+    return vq::status_of(hipGetLastError());
+}
 
 extern "C" int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, const void* side,
                                      int side_bytes, void* y_bf16, uint32_t* sink, void* stream) {

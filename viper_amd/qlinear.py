@@ -135,6 +135,7 @@ _SYMBOLS = (
     "viper_hip_qlinear_static",
     "viper_hip_qlinear_timeline",
     "viper_hip_check_bf16_rounding",
+    "viper_hip_clock_stamp",
 )
 
 
@@ -173,6 +174,8 @@ def lib():
     L.viper_hip_check_quantizer.restype = i32
     L.viper_hip_stream_read.argtypes = [vp, sz, i32, i32, vp, i32, vp, vp, vp]
     L.viper_hip_stream_read.restype = i32
+    L.viper_hip_clock_stamp.argtypes = [vp, vp]
+    L.viper_hip_clock_stamp.restype = i32
     L.viper_hip_qlinear_fused2.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     L.viper_hip_qlinear_fused2.restype = i32
     L.viper_hip_qlinear_fused2_prequantized.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, i32,
