@@ -25,6 +25,7 @@ import ctypes as C
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -310,7 +311,7 @@ def read_sweep(torch, L, gen):
 
 
 def timeline(torch, L, gen, N, K, qt=4):
-    """Per-wave timeline of the M=1 GEMV of format qt at the north-star shape: percentiles of each
+    """Per-wave timeline of the M=1 GEMV of format qt at shape (K, N): percentiles of each
     stamp over all waves of one dispatch (the last of a back-to-back sequence over rotating weights),
     in us from the first wave's start."""
     G = GROUP[qt]
@@ -461,11 +462,13 @@ def main():
     ap.add_argument("--timeline", nargs="?", const="q4", default=None, choices=("q4", "q5", "q6", "w8"),
                     help="only the per-wave timeline of the M=1 GEMV at the north-star shape, Q4_G64 unless a "
                          "format is named (viper_hip_qlinear_timeline)")
+    ap.add_argument("--shape", type=int, nargs=2, default=None, metavar=("K", "N"),
+                    help="with --timeline: another shape than the north star's (one with an exact tiling)")
     ap.add_argument("--only", default="", metavar="LINE",
                     help="only one line (rocprofv3 runs): config0[_pre], down, verify_mM (K=2560 N=10240) or "
                          "verify_mM_down (K=10240 N=2560), pre_mM[_down] (the same through the prequantized "
                          "entry, x quantized once outside the timed calls), q5_m1 / q6_m8 / w8_m1 ... "
-                         "(config 4), config1 / "
+                         "(config 4), FMT_kK_nN_mM (any shape, e.g. q4_k3072_n6144_m1), config1 / "
                          "config1_2launch (MLP), config3 (fused step) or config3_ref (reference launch sequence)")
     ap.add_argument("--clock-period", action="store_true",
                     help="only the north-star dispatch period on the device clock: back-to-back sequences of "
@@ -519,6 +522,11 @@ def main():
             shape = (2560, 10240) if one.endswith("_down") else (10240, 2560)
             res = time_linear(torch, L, gen, qtype, shape[0], shape[1], Mv, steps=args.steps,
                               prequantized=one.startswith("pre_m"))
+        elif re.fullmatch(r"(q4|q5|q6|w8)_k\d+_n\d+_m\d+", one):
+            fmt, kk, nn, mm = one.split("_")
+            qt = {"q4": 4, "q5": 5, "q6": 6, "w8": 8}[fmt]
+            res = time_linear(torch, L, gen, qt, int(nn[1:]), int(kk[1:]), int(mm[1:]), steps=args.steps,
+                              outliers=qt != 4)
         elif one[:1] in "qw" and "_m" in one:
             fmt, mpart = one.split("_m")
             qt = {"q5": 5, "q6": 6, "w8": 8}[fmt]
@@ -539,7 +547,8 @@ def main():
         read_sweep(torch, L, gen)
         return
     if args.timeline:
-        timeline(torch, L, gen, N, K, {"q4": 4, "q5": 5, "q6": 6, "w8": 8}[args.timeline])
+        Kt, Nt = (args.shape[0], args.shape[1]) if args.shape else (K, N)
+        timeline(torch, L, gen, Nt, Kt, {"q4": 4, "q5": 5, "q6": 6, "w8": 8}[args.timeline])
         return
     if args.m16_only or args.verify_only:
         Mv = 16 if args.m16_only else args.verify_only
@@ -676,6 +685,15 @@ def main():
         for qt, nm in ((5, "q5"), (6, "q6"), (8, "w8")):
             for Mv in (1, 8):
                 us_v, gbs_v = time_linear(torch, L, gen, qt, N, K, Mv, outliers=True)
+                extras[f"{nm}_m{Mv}_us"], extras[f"{nm}_m{Mv}_gbs"] = us_v, gbs_v
+
+        # the reference engine's own linears (include/viper/model_impl.cuh:107-116: hidden 3072,
+        # intermediate 10752, 48 x 128 query heads): q 3072 -> 6144, o 6144 -> 3072, gate (and up)
+        # 3072 -> 10752, down 10752 -> 3072, one decode row and a 16-row verify
+        for nm, (Ne, Ke) in (("engine_q", (6144, 3072)), ("engine_o", (3072, 6144)),
+                             ("engine_gate", (10752, 3072)), ("engine_down", (3072, 10752))):
+            for Mv in (1, 16):
+                us_v, gbs_v = time_linear(torch, L, gen, qtype, Ne, Ke, Mv)
                 extras[f"{nm}_m{Mv}_us"], extras[f"{nm}_m{Mv}_gbs"] = us_v, gbs_v
 
         # down projection shape (K=10240, N=2560), M=1, fused quantize

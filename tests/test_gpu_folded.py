@@ -71,10 +71,11 @@ def test_rmsnorm_qkv_equals_two_launches(torch_dev):
         np.testing.assert_array_equal(u16(y), u16(r))
 
 
-def test_swiglu_down_residual_equals_two_launches(torch_dev):
-    # engine shape: down (K=10240, N=2560) from silu(gate) * up, residual in place
+@pytest.mark.parametrize("K,N", [(10240, 2560), (10752, 3072)])
+def test_swiglu_down_residual_equals_two_launches(torch_dev, K, N):
+    # engine shapes: down (K=10240, N=2560; the reference's K=10752, N=3072 on
+    # the masked tiling) from silu(gate) * up, residual in place
     torch = torch_dev
-    K, N = 10240, 2560
     w = weights(torch, O.Q4_G64, N, K, 520)[0]
     rng = np.random.default_rng(521)
     g = dev(torch, bf16(3.0 * rng.standard_normal((1, K))))
@@ -103,6 +104,8 @@ def test_swiglu_down_residual_equals_two_launches(torch_dev):
     (O.Q6_G64, 517, 4096, P.RMSNORM),
     (O.W8_G32, 777, 2560, P.BF16),
     (O.Q4_G64, 2560, 10240, P.BF16),
+    (O.Q4_G64, 10752, 3072, P.RMSNORM),   # the reference engine's gate / up (6-slot tiling)
+    (O.Q5_G64, 1000, 10752, P.BF16),      # masked tiling
 ])
 def test_gate_up_swiglu_equals_chain(torch_dev, qtype, N, K, pro):
     torch = torch_dev
@@ -156,10 +159,11 @@ def test_gate_up_swiglu_errors(torch_dev):
     assert va.linear_m1_swiglu(wg, wg, P.BF16, x, None, None).code == va.StatusCode.INVALID_ARGUMENT
 
 
+@pytest.mark.parametrize("K", [4096, 3072, 10752])
 @pytest.mark.parametrize("qtype", [O.Q4_G64, O.Q5_G64, O.Q6_G64, O.W8_G32])
-def test_rmsnorm_prologue_against_oracle(torch_dev, qtype):
+def test_rmsnorm_prologue_against_oracle(torch_dev, qtype, K):
     torch = torch_dev
-    K, eps = 4096, 1e-5
+    eps = 1e-5
     trip = [weights(torch, qtype, n, K, 530 + n, O.SCALE_BF16) for n in (300, 64)]
     ws = [t[0] for t in trip]
     x = O.gen_act(1, K, 531, outlier_frac=0.05)

@@ -451,6 +451,30 @@ def test_k_split_graph_replays(torch_dev):
         torch.cuda.synchronize()
 
 
+# The reference engine's own shapes (include/viper/model_impl.cuh:107-116:
+# hidden 3072, intermediate 10752, 48 x 128 query and 8 x 128 key/value
+# heads): q 3072 -> 6144, k / v 3072 -> 1024, o 6144 -> 3072 (+ residual),
+# gate / up 3072 -> 10752, down 10752 -> 3072 (+ residual), full size, one
+# decode row and a 16-row verify, group dots bit-exact.  At M = 1 they run the
+# 6-slot exact tilings (K = 3072: 16 lanes per row, 6144: 32) and the masked
+# one (K = 10752: 336 chunks in 64 x 6 slots).
+@pytest.mark.parametrize("M", [1, 16])
+@pytest.mark.parametrize("N,K", [(6144, 3072), (1024, 3072), (3072, 6144), (10752, 3072), (3072, 10752)])
+def test_engine_shapes_full_size(torch_dev, N, K, M):
+    run_case(torch_dev, O.Q4_G64, N, K, M, seed=0xE0000 + K + M, residual=(N == 3072))
+
+
+# Every format at the engine's K (ragged N, both scale encodings, outliers):
+# Q4 / Q5 / Q6 on the 6-slot and masked tilings, W8 on its own (K = 3072:
+# 32 lanes x 6, 6144: 64 x 6; 10752 on the general path).
+@pytest.mark.parametrize("qtype", FORMATS)
+@pytest.mark.parametrize("N,K,senc", [(1000, 3072, O.SCALE_FP16), (777, 6144, O.SCALE_BF16),
+                                      (1001, 10752, O.SCALE_FP16), (64, 10752, O.SCALE_BF16)])
+def test_engine_k_every_format(torch_dev, qtype, N, K, senc):
+    run_case(torch_dev, qtype, N, K, 1, seed=0xE1000 + N + qtype, scale_enc=senc, residual=(N % 2 == 1),
+             outlier=0.05)
+
+
 # Q4 with K a multiple of 256 runs the row-contiguous matrix-core kernel: rows
 # per workgroup 8..48 (one workgroup per CU where N allows), one or two
 # 4-group quads per wave (K up to 2560, up to 5120), 4-wave workgroups for
@@ -591,11 +615,13 @@ def test_prequantized_entry(torch_dev, N, K, M):
 
 
 @pytest.mark.parametrize("qtype", FORMATS)
-@pytest.mark.parametrize("N,K", [(2560, 2560), (61, 10240), (10240, 2560), (10010, 2560)])
+@pytest.mark.parametrize("N,K", [(2560, 2560), (61, 10240), (10240, 2560), (10010, 2560), (3072, 10752),
+                                 (6144, 3072), (3001, 6144)])
 def test_prequantized_m1(torch_dev, qtype, N, K):
     # M = 1 from int8 activations: the M = 1 kernel's prequantized prologue
     # (one octet per thread on 256 threads; Q4's two octets per thread on 320
-    # and 640, a ragged last workgroup at N = 10010)
+    # and 640, a ragged last workgroup at N = 10010; the reference engine's K
+    # on the 6-slot tilings and the masked K = 10752 one)
     torch = torch_dev
     G = O.group_size(qtype)
     packed, scales = O.gen_weights(qtype, N, K, 50 + qtype, O.SCALE_FP16)

@@ -243,7 +243,7 @@ __device__ __forceinline__ void m1_dots_rows(u32x4 (&wv)[CPL], uint32_t (&h0)[CP
 // (x [M][K], y and the residual [M][N]); every workgroup stages all M rows,
 // each lane decodes its weight chunk once and dots it with every row.  Small
 // verify batches then need no separate quantize launch.
-template <int F, int TS, int NTT, int CPL, int SENC, int MODE, bool EXACT, int PRO, int MR, int DELAY>
+template <int F, int TS, int NTT, int CPL, int SENC, int MODE, bool EXACT, int PRO, int MR, int DELAY, int KC = 0>
 __global__ void __launch_bounds__(NTT)
 qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* y0, int K, int n0, int e0,
                 int e1, const uint16_t* res, const void* xa, float eps, uint16_t* __restrict__ xout,
@@ -266,7 +266,13 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     // exact tilings: K is the tiling's row length and the argument slot
     // carries the grid size instead (for the XCD-aware block order); the
     // load rounds of one row are then exact
-    constexpr int KX = EXACT ? m1_exact_k<F>(TS, CPL) : 0;
+    // KC (masked exact tilings): the row has KC < TS * CPL chunks; K is still
+    // the constant, the scale block still staged, and the slots past the row
+    // read nothing (out of the buffer's range) and add nothing.
+    constexpr int KX = EXACT ? (KC ? Fmt<F>::CK * KC : m1_exact_k<F>(TS, CPL)) : 0;
+    constexpr bool MASK = EXACT && KC != 0 && KC != TS * CPL;
+    static_assert(!MASK || (MR == 1 && KC < TS * CPL), "masked tilings: one row, fewer chunks than slots");
+    constexpr bool FULL = EXACT && !MASK;  // every slot holds a chunk of the row
     const int grid = K;
     if constexpr (EXACT) K = KX;
     // SPARE: the first wave stages no activation and issues its weights at
@@ -457,7 +463,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = seg * segw + j * TS + l;
-            const bool in = EXACT || c < CPR;
+            const bool in = FULL || c < CPR;
             wv[j] = bload16<AUX_NT>(wr, in ? rt * (int)rbytes + c * 16 : OOB);
             // odd lanes and chunks past the row read scale 0, which zeroes
             // their term without any select
@@ -635,7 +641,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = seg * segw + j * TS + l;
-            const int cc = EXACT ? c : min(c, CPR - 1);
+            const int cc = FULL ? c : min(c, CPR - 1);
             CS[j] = lcs[cc];
             const u32x4* a = (const u32x4*)(lxq + (size_t)cc * FT::CK);
             A0[j] = a[0];
@@ -643,16 +649,18 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             if constexpr (EXACT) {
                 // read on every lane (in bounds), select after: no branch, no
                 // wait between the LDS reads, product formed before the weights
-                const uint32_t sraw = lsc[rr * NGR + (c >> 1)];
+                // (a masked slot's scale is 0: its dot of zero weights with the
+                // last chunk's activation adds nothing)
+                const uint32_t sraw = lsc[rr * NGR + (cc >> 1)];
                 const float wsf = SENC ? bf16f(sraw) : f16f(sraw);
-                SC[j] = (lead ? wsf : 0.0f) * __uint_as_float(CS[j].y);
+                SC[j] = ((lead && (FULL || c < CPR)) ? wsf : 0.0f) * __uint_as_float(CS[j].y);
             }
         }
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = seg * segw + j * TS + l;
-            const bool ok = EXACT || c < CPR;
-            const int cc = EXACT ? c : min(c, CPR - 1);
+            const bool ok = FULL || c < CPR;
+            const int cc = FULL ? c : min(c, CPR - 1);
             int dot;
             if constexpr (F == 4) dot = chunk_dot_q4(wv[j], A0[j], A1[j], (int)CS[j].x);
             else dot = chunk_dot<F>(wv[j], h0[j], h1[j], A0[j], A1[j], (int)CS[j].x);
@@ -705,53 +713,77 @@ typedef void (*m1_fn)(const void*, const uint8_t*, const uint16_t*, uint16_t*, i
 
 // Launch shapes instantiated for every format: (team size, workgroup size,
 // chunk slots per lane).
+// 5 slots tile K = 2560 (Q4/Q5/Q6: 16 lanes), 5120 and 10240; 6 slots tile
+// the reference engine's K = 3072 (16 lanes; W8: 32), 6144 (32; W8: 64) and
+// 12288 (64 lanes).
+// The 384-thread ones spread the engine's q (N = 6144) and o (N = 3072) over
+// exactly one workgroup per CU (24 / 12 rows), where 256 / 320 threads left
+// some CUs with twice the rows of others.
 constexpr int M1_SHAPES[][3] = {{8, 128, 10}, {8, 192, 10}, {8, 320, 10}, {16, 256, 10}, {16, 640, 10},
                                 {32, 320, 10}, {32, 640, 10}, {64, 640, 10}, {16, 256, 5}, {16, 320, 5},
-                                {16, 640, 5}, {32, 640, 5}, {64, 640, 5}};
+                                {16, 640, 5}, {32, 640, 5}, {64, 640, 5}, {16, 256, 6}, {16, 320, 6},
+                                {16, 384, 6}, {32, 320, 6}, {32, 384, 6}, {32, 640, 6}, {64, 640, 6}};
+// Masked exact tilings (team size, workgroup size, chunk slots per lane,
+// chunks per row): rows with no exact tiling of at most 10 slots per lane
+// keep K constant and the staged scale block, and mask the last slots.  336
+// chunks: the engine's K = 10752 (Q4/Q5/Q6), 64 lanes x 6 slots; 384 and 768
+// threads put the engine's N = 3072 on 512 / 256 workgroups (6 / 12 rows).
+constexpr int M1_MASKED[][4] = {{64, 320, 6, 336}, {64, 384, 6, 336}, {64, 640, 6, 336}, {64, 768, 6, 336}};
 
-// A shape of 5 chunk slots per lane is only ever an exact tiling (m1_shape
-// picks those by TS * CPL == chunks per row, and every such K tiles exactly;
-// rows that do not tile take 10 slots), so its non-exact variants are not
-// built.
+// Shapes of 5 or 6 chunk slots per lane are only ever exact tilings (m1_shape
+// picks those by TS * CPL == chunks per row, or a masked tiling's chunks per
+// row; other rows take 10 slots), so their non-exact variants are not built.
 template <int F, int SENC, int MODE, bool EXACT, int PRO, int MR>
-m1_fn m1_kernel_v(int ts, int ntt, int cpl) {
+m1_fn m1_kernel_v(int ts, int ntt, int cpl, int kc) {
 #define VQ_M1(TS_, NTT_, CPL_)                                                                      \
     if constexpr ((EXACT || CPL_ == 10) && (MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_)) &&          \
                   (MR == 1 || m1_mr_shape_ok(TS_, NTT_, CPL_)))                                     \
-        if (ts == TS_ && ntt == NTT_ && cpl == CPL_)                                                \
+        if (ts == TS_ && ntt == NTT_ && cpl == CPL_ && kc == 0)                                     \
             return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, MR,                          \
                                    m1_delay<F>(EXACT, TS_, NTT_, CPL_, MODE, MR, PRO)>;
     VQ_M1(8, 128, 10) VQ_M1(8, 192, 10) VQ_M1(8, 320, 10) VQ_M1(16, 256, 10) VQ_M1(16, 640, 10)
     VQ_M1(32, 320, 10) VQ_M1(32, 640, 10) VQ_M1(64, 640, 10) VQ_M1(16, 256, 5) VQ_M1(16, 320, 5)
-    VQ_M1(16, 640, 5) VQ_M1(32, 640, 5) VQ_M1(64, 640, 5)
+    VQ_M1(16, 640, 5) VQ_M1(32, 640, 5) VQ_M1(64, 640, 5) VQ_M1(16, 256, 6) VQ_M1(16, 320, 6)
+    VQ_M1(16, 384, 6) VQ_M1(32, 320, 6) VQ_M1(32, 384, 6) VQ_M1(32, 640, 6) VQ_M1(64, 640, 6)
 #undef VQ_M1
+    // masked exact tilings (KC_ chunks in TS_ * CPL_ slots), one row
+#define VQ_M1K(TS_, NTT_, CPL_, KC_)                                                                \
+    if constexpr (EXACT && MR == 1 && (MODE != M1_SWIGLU || m1_pair_ok(TS_, NTT_)))                  \
+        if (ts == TS_ && ntt == NTT_ && cpl == CPL_ && kc == KC_)                                   \
+            return qgemv_m1_kernel<F, TS_, NTT_, CPL_, SENC, MODE, EXACT, PRO, MR,                          \
+                                   m1_delay<F>(EXACT, TS_, NTT_, CPL_, MODE, MR, PRO), KC_>;
+    VQ_M1K(64, 320, 6, 336) VQ_M1K(64, 384, 6, 336) VQ_M1K(64, 640, 6, 336) VQ_M1K(64, 768, 6, 336)
+#undef VQ_M1K
     return nullptr;
 }
 
 template <int F, int PRO, int MODE, int MR>
-m1_fn m1_pick_mode(int ts, int ntt, int cpl, int senc, bool exact) {
+m1_fn m1_pick_mode(int ts, int ntt, int cpl, int kc, int senc, bool exact) {
     if (exact)
-        return senc ? m1_kernel_v<F, 1, MODE, true, PRO, MR>(ts, ntt, cpl) : m1_kernel_v<F, 0, MODE, true, PRO, MR>(ts, ntt, cpl);
-    return senc ? m1_kernel_v<F, 1, MODE, false, PRO, MR>(ts, ntt, cpl) : m1_kernel_v<F, 0, MODE, false, PRO, MR>(ts, ntt, cpl);
+        return senc ? m1_kernel_v<F, 1, MODE, true, PRO, MR>(ts, ntt, cpl, kc)
+                    : m1_kernel_v<F, 0, MODE, true, PRO, MR>(ts, ntt, cpl, kc);
+    if (kc != 0) return nullptr;
+    return senc ? m1_kernel_v<F, 1, MODE, false, PRO, MR>(ts, ntt, cpl, 0)
+                : m1_kernel_v<F, 0, MODE, false, PRO, MR>(ts, ntt, cpl, 0);
 }
 // The swiglu pair is built for the BF16 and RMSNORM prologues (the inputs of
 // the engine's gate/up projection); MR > 1 rows for BF16 and INT8; the
 // partials (test entry point viper_hip_qlinear_partials) for BF16 only, the
 // one prologue that entry point takes.
 template <int F, int PRO>
-m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, int mode, bool exact, int mr) {
+m1_fn m1_pick_pro(int ts, int ntt, int cpl, int kc, int senc, int mode, bool exact, int mr) {
     constexpr bool PART_OK = PRO == PRO_BF16;
     if constexpr (PRO == PRO_BF16 || PRO == PRO_INT8) {
         if (mr == 2) {
             if constexpr (PART_OK)
-                if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 2>(ts, ntt, cpl, senc, exact);
-            if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 2>(ts, ntt, cpl, senc, exact);
+                if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 2>(ts, ntt, cpl, kc, senc, exact);
+            if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 2>(ts, ntt, cpl, kc, senc, exact);
             return nullptr;
         }
         if (mr == 4) {
             if constexpr (PART_OK)
-                if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 4>(ts, ntt, cpl, senc, exact);
-            if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 4>(ts, ntt, cpl, senc, exact);
+                if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 4>(ts, ntt, cpl, kc, senc, exact);
+            if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 4>(ts, ntt, cpl, kc, senc, exact);
             return nullptr;
         }
     }
@@ -760,34 +792,34 @@ m1_fn m1_pick_pro(int ts, int ntt, int cpl, int senc, int mode, bool exact, int 
     if constexpr (PRO == PRO_BF16)
         if (mode == M1_TL)
             return !exact ? nullptr
-                          : senc ? m1_kernel_v<F, 1, M1_TL, true, PRO, 1>(ts, ntt, cpl)
-                                 : m1_kernel_v<F, 0, M1_TL, true, PRO, 1>(ts, ntt, cpl);
+                          : senc ? m1_kernel_v<F, 1, M1_TL, true, PRO, 1>(ts, ntt, cpl, kc)
+                                 : m1_kernel_v<F, 0, M1_TL, true, PRO, 1>(ts, ntt, cpl, kc);
     if constexpr (PART_OK)
-        if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 1>(ts, ntt, cpl, senc, exact);
+        if (mode == M1_PART) return m1_pick_mode<F, PRO, M1_PART, 1>(ts, ntt, cpl, kc, senc, exact);
     if constexpr (PRO == PRO_BF16 || PRO == PRO_RMSNORM)
-        if (mode == M1_SWIGLU) return m1_pick_mode<F, PRO, M1_SWIGLU, 1>(ts, ntt, cpl, senc, exact);
-    if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 1>(ts, ntt, cpl, senc, exact);
+        if (mode == M1_SWIGLU) return m1_pick_mode<F, PRO, M1_SWIGLU, 1>(ts, ntt, cpl, kc, senc, exact);
+    if (mode == M1_PLAIN) return m1_pick_mode<F, PRO, M1_PLAIN, 1>(ts, ntt, cpl, kc, senc, exact);
     return nullptr;
 }
 
 // Kernels of format F with the quantize / int8 prologues and with the folded
 // rmsnorm / swiglu prologues (each defined in its own translation unit).
 template <int F>
-m1_fn m1_pick_plain(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro, int mr);
+m1_fn m1_pick_plain(int ts, int ntt, int cpl, int kc, int senc, int mode, bool exact, int pro, int mr);
 template <int F>
-m1_fn m1_pick_folded(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro, int mr);
+m1_fn m1_pick_folded(int ts, int ntt, int cpl, int kc, int senc, int mode, bool exact, int pro, int mr);
 
-#define VQ_M1_PLAIN(F)                                                                                 \
-    template <>                                                                                        \
-    m1_fn m1_pick_plain<F>(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro, int mr) { \
-        return pro == PRO_INT8 ? m1_pick_pro<F, PRO_INT8>(ts, ntt, cpl, senc, mode, exact, mr)           \
-                               : m1_pick_pro<F, PRO_BF16>(ts, ntt, cpl, senc, mode, exact, mr);          \
+#define VQ_M1_PLAIN(F)                                                                                         \
+    template <>                                                                                                \
+    m1_fn m1_pick_plain<F>(int ts, int ntt, int cpl, int kc, int senc, int mode, bool exact, int pro, int mr) { \
+        return pro == PRO_INT8 ? m1_pick_pro<F, PRO_INT8>(ts, ntt, cpl, kc, senc, mode, exact, mr)               \
+                               : m1_pick_pro<F, PRO_BF16>(ts, ntt, cpl, kc, senc, mode, exact, mr);              \
     }
-#define VQ_M1_FOLDED(F)                                                                                \
-    template <>                                                                                        \
-    m1_fn m1_pick_folded<F>(int ts, int ntt, int cpl, int senc, int mode, bool exact, int pro, int mr) { \
-        return pro == PRO_SWIGLU ? m1_pick_pro<F, PRO_SWIGLU>(ts, ntt, cpl, senc, mode, exact, mr)         \
-                                 : m1_pick_pro<F, PRO_RMSNORM>(ts, ntt, cpl, senc, mode, exact, mr);       \
+#define VQ_M1_FOLDED(F)                                                                                         \
+    template <>                                                                                                 \
+    m1_fn m1_pick_folded<F>(int ts, int ntt, int cpl, int kc, int senc, int mode, bool exact, int pro, int mr) { \
+        return pro == PRO_SWIGLU ? m1_pick_pro<F, PRO_SWIGLU>(ts, ntt, cpl, kc, senc, mode, exact, mr)             \
+                                 : m1_pick_pro<F, PRO_RMSNORM>(ts, ntt, cpl, kc, senc, mode, exact, mr);           \
     }
 
 }  // namespace vq

@@ -3,27 +3,35 @@
 
 namespace vq {
 
+// kc: chunks per row of a masked exact tiling (M1_MASKED), else 0.
 struct M1Shape {
     int ts, ntt, cpl;
+    int kc = 0;
 };
 
 static m1_fn m1_kernel(int qtype, const M1Shape& sh, int senc, int mode, bool exact, int pro, int mr = 1) {
     const bool folded = pro == PRO_RMSNORM || pro == PRO_SWIGLU;
-    const int ts = sh.ts, ntt = sh.ntt, cpl = sh.cpl;
+    const int ts = sh.ts, ntt = sh.ntt, cpl = sh.cpl, kc = sh.kc;
     switch (qtype) {
         case VIPER_QTYPE_Q4_G64:
-            return folded ? m1_pick_folded<4>(ts, ntt, cpl, senc, mode, exact, pro, mr)
-                          : m1_pick_plain<4>(ts, ntt, cpl, senc, mode, exact, pro, mr);
+            return folded ? m1_pick_folded<4>(ts, ntt, cpl, kc, senc, mode, exact, pro, mr)
+                          : m1_pick_plain<4>(ts, ntt, cpl, kc, senc, mode, exact, pro, mr);
         case VIPER_QTYPE_Q5_G64:
-            return folded ? m1_pick_folded<5>(ts, ntt, cpl, senc, mode, exact, pro, mr)
-                          : m1_pick_plain<5>(ts, ntt, cpl, senc, mode, exact, pro, mr);
+            return folded ? m1_pick_folded<5>(ts, ntt, cpl, kc, senc, mode, exact, pro, mr)
+                          : m1_pick_plain<5>(ts, ntt, cpl, kc, senc, mode, exact, pro, mr);
         case VIPER_QTYPE_Q6_G64:
-            return folded ? m1_pick_folded<6>(ts, ntt, cpl, senc, mode, exact, pro, mr)
-                          : m1_pick_plain<6>(ts, ntt, cpl, senc, mode, exact, pro, mr);
+            return folded ? m1_pick_folded<6>(ts, ntt, cpl, kc, senc, mode, exact, pro, mr)
+                          : m1_pick_plain<6>(ts, ntt, cpl, kc, senc, mode, exact, pro, mr);
         default:
-            return folded ? m1_pick_folded<8>(ts, ntt, cpl, senc, mode, exact, pro, mr)
-                          : m1_pick_plain<8>(ts, ntt, cpl, senc, mode, exact, pro, mr);
+            return folded ? m1_pick_folded<8>(ts, ntt, cpl, kc, senc, mode, exact, pro, mr)
+                          : m1_pick_plain<8>(ts, ntt, cpl, kc, senc, mode, exact, pro, mr);
     }
+}
+
+// A launch shape takes the exact-tiling kernels: TS * CPL chunks per row, or
+// a masked tiling's chunks per row, and a row's scales in whole 16-byte words.
+static bool m1_exact(const M1Shape& sh, int cpr, int ngr) {
+    return (cpr == sh.ts * sh.cpl || (sh.kc != 0 && cpr == sh.kc)) && ngr % 8 == 0;
 }
 
 // Per-CU row load of a shape: ceil(ceil(N / rows) / CUs) * rows (rows per
@@ -57,10 +65,7 @@ static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct, bool pai
     M1Shape best{0, 0, 0};
     long best_load = -1;
     auto extra = [&](const M1Shape& c) { const int r = (noct + c.ntt - 1) / c.ntt; return r > 2 ? r - 2 : 0; };
-    for (const auto& s : M1_SHAPES) {
-        const M1Shape c{s[0], s[1], s[2]};
-        if (c.ntt < min_ntt || c.ts * c.cpl != cpr || (pair && !m1_pair_ok(c.ts, c.ntt))) continue;
-        if (mr > 1 && !m1_mr_shape_ok(c.ts, c.ntt, c.cpl)) continue;
+    auto consider = [&](const M1Shape& c) {
         const long load = m1_load(c, N, cus, pair);
         const bool one = mr == 1 && c.ntt >= noct, best_one = mr == 1 && best.ntt >= noct;
         const int xr = extra(c), bxr = best.ntt ? extra(best) : 0;
@@ -74,6 +79,19 @@ static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct, bool pai
             best = c;
             best_load = load;
         }
+    };
+    for (const auto& s : M1_SHAPES) {
+        const M1Shape c{s[0], s[1], s[2]};
+        if (c.ntt < min_ntt || c.ts * c.cpl != cpr || (pair && !m1_pair_ok(c.ts, c.ntt))) continue;
+        if (mr > 1 && !m1_mr_shape_ok(c.ts, c.ntt, c.cpl)) continue;
+        consider(c);
+    }
+    if (best.ntt != 0) return best;
+    // masked exact tilings (one row: not the multi-row shapes), in the same order
+    for (const auto& s : M1_MASKED) {
+        const M1Shape c{s[0], s[1], s[2], s[3]};
+        if (mr > 1 || c.kc != cpr || c.ntt < min_ntt || (pair && !m1_pair_ok(c.ts, c.ntt))) continue;
+        consider(c);
     }
     if (best.ntt != 0) return best;
     int ts = 8;
@@ -130,8 +148,7 @@ bool m1_rows_pair(int qtype, int K, int M) {
     if (qtype != VIPER_QTYPE_Q4_G64 || !m1_rows_ok(qtype, K, M)) return false;
     const int noct = M * (K / 8);
     const M1Shape sh = m1_shape(K / 32, 1 << 14, device_cus(), (noct + M1_XS_MR - 1) / M1_XS_MR, noct, false, m1_mr(M));
-    const bool exact = (K / 32) == sh.ts * sh.cpl && (K / 64) % 8 == 0;
-    return m1_pairs<4>(exact, sh.ntt, m1_mr(M), PRO_BF16);
+    return m1_pairs<4>(m1_exact(sh, K / 32, K / 64), sh.ntt, m1_mr(M), PRO_BF16);
 }
 
 bool m1_folded_ok(int qtype, int K, int N) {
@@ -165,7 +182,7 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     }
     if (sh.ntt == 0) return VIPER_INVALID_ARGUMENT;
     const int group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
-    const bool exact = (K / ck) == sh.ts * sh.cpl && (K / group) % 8 == 0;
+    const bool exact = m1_exact(sh, K / ck, K / group);
     const m1_fn fn = m1_kernel(qtype, sh, senc, part != nullptr ? M1_PART : M1_PLAIN, exact, pro, mr);
     if (fn == nullptr) return VIPER_INTERNAL;
     const int rows = sh.ntt / sh.ts;
@@ -195,7 +212,7 @@ int launch_m1_timeline(int qtype, int senc, int K, const void* x, const void* w,
     const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32, group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
     const int noct = K / 8;
     const M1Shape sh = m1_shape(K / ck, N, device_cus(), 0, noct);
-    if (sh.ntt == 0 || K != ck * sh.ts * sh.cpl || (K / group) % 8 != 0) return VIPER_INVALID_ARGUMENT;
+    if (sh.ntt == 0 || !m1_exact(sh, K / ck, K / group)) return VIPER_INVALID_ARGUMENT;
     const m1_fn fn = m1_kernel(qtype, sh, senc, M1_TL, true, PRO_BF16);
     if (fn == nullptr) return VIPER_INTERNAL;
     const int rows = sh.ntt / sh.ts;
@@ -233,7 +250,7 @@ int launch_m1_swiglu(int qtype, int senc, int K, int pro, const void* x, const v
     if (sh.ntt == 0) sh = m1_shape(K / ck, N, cus, pro == PRO_RMSNORM ? (noct + M1_XS - 1) / M1_XS : 0, noct, true);
     if (sh.ntt == 0) return VIPER_INVALID_ARGUMENT;
     const int group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
-    const bool exact = (K / ck) == sh.ts * sh.cpl && (K / group) % 8 == 0;
+    const bool exact = m1_exact(sh, K / ck, K / group);
     const m1_fn fn = m1_kernel(qtype, sh, senc, M1_SWIGLU, exact, pro);
     if (fn == nullptr) return VIPER_INTERNAL;
     const int rows = sh.ntt / sh.ts;

@@ -40,8 +40,8 @@ def demangle(names):
 
 
 def known(pretty):
-    # qgemv_m1_kernel<F, TS, NTT, CPL, SENC, MODE, EXACT, PRO, MR, DELAY>
-    m = re.search(r"qgemv_m1_kernel<(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (true|false), (\d+), (\d+), (\d+)>",
+    # qgemv_m1_kernel<F, TS, NTT, CPL, SENC, MODE, EXACT, PRO, MR, DELAY, KC>
+    m = re.search(r"qgemv_m1_kernel<(\d+), (\d+), (\d+), (\d+), (\d+), (\d+), (true|false), (\d+), (\d+), (\d+), (\d+)>",
                   pretty)
     if not m:
         return False
