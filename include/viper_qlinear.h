@@ -141,8 +141,8 @@ size_t viper_hip_qlinear_workspace_bytes(int qtype, int N, int K, int M);
  *   [1] the count of K-split sums that did not arrive within the kernel's
  *       bounded wait (uint32 at 4 for every shape; such outputs are NaN;
  *       the library never clears it, so a caller can check it stayed 0),
- *   [2] the K split's block counters, [3] xq, [4] xs, [5] the K split's
- *       part sums (64-bit slots). */
+ *   [2] the K split's block counters (from byte 256), [3] xq, [4] xs,
+ *       [5] the K split's part sums (64-bit slots). */
 size_t viper_hip_qlinear_workspace_layout(int qtype, int N, int K, int M, size_t* offsets);
 
 /* y[M][N] = linear(w, x) with x[M][K] bf16 quantized per row and group.

@@ -41,10 +41,10 @@ def test_group_sizes_and_workspace():
     assert va.workspace_bytes(8, 10, 2560, 3) == 16 + 16 * 2560 + 80 * 16 * 4
     assert va.workspace_bytes(6, 10, 2496, 3) == 16 + 16 * 2496 + 39 * 16 * 4
     # long K (the K split in 4 parts): also one counter per 8 rows (16-byte
-    # aligned, after the control words) and the part sums [4][M][N] as 64-bit
-    # {tag, fp32} slots
-    assert va.workspace_bytes(4, 2560, 10240, 16) == 16 + 1280 + 16 * 10240 + 160 * 16 * 4 + 4 * 16 * 2560 * 8
-    assert va.workspace_bytes(8, 2560, 10240, 3) == 16 + 1280 + 16 * 10240 + 320 * 16 * 4 + 4 * 3 * 2560 * 8
+    # aligned, from byte 256: a cache line apart from the control words) and
+    # the part sums [4][M][N] as 64-bit {tag, fp32} slots
+    assert va.workspace_bytes(4, 2560, 10240, 16) == 256 + 1280 + 16 * 10240 + 160 * 16 * 4 + 4 * 16 * 2560 * 8
+    assert va.workspace_bytes(8, 2560, 10240, 3) == 256 + 1280 + 16 * 10240 + 320 * 16 * 4 + 4 * 3 * 2560 * 8
     assert va.workspace_bytes(4, 2560, 5120, 16) == 16 + 16 * 5120 + 80 * 16 * 4   # one segment: no split
 
 
@@ -68,7 +68,7 @@ def test_split_control_words_fixed_for_every_shape():
             continue
         seen += 1
         assert lay["generation"] == 0 and lay["missed"] == 4, (qtype, N, K, M)
-        assert lay["counters"] == 16
+        assert lay["counters"] == 256
         n_blocks = (N + 7) // 8
         assert lay["counters"] + 4 * n_blocks <= lay["xq"]
         assert lay["xq"] % 16 == 0 and lay["xs"] % 16 == 0 and lay["sums"] % 16 == 0

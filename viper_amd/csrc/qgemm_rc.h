@@ -567,6 +567,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                     u[i][p] = __hip_atomic_load(sp + (size_t)p * M * N + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
         }
+        unsigned missed = 0;  // sums that never arrived (NaN in y), counted in the workspace
 #pragma unroll
         for (int i = 0; i < MINE; ++i) {
             const int sl = wave + i * W;
@@ -584,17 +585,16 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                         for (int it = 0; (unsigned)(w >> 32) != tag && it < RC_SPIN; ++it)
                             w = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
-                    if (__builtin_expect((unsigned)(w >> 32) != tag, 0)) {
-                        __hip_atomic_fetch_add(sc + RC_CTL_MISS, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        v += __builtin_nanf("");
-                    } else {
-                        v += __uint_as_float((unsigned)w);
-                    }
+                    const bool ok = (unsigned)(w >> 32) == tag;
+                    missed += !ok;
+                    v += ok ? __uint_as_float((unsigned)w) : __builtin_nanf("");
                 }
                 if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
                 y[o] = f2bf(v);
             }
         }
+        if (__builtin_expect(missed != 0, 0))
+            __hip_atomic_fetch_add(sc + RC_CTL_MISS, missed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 

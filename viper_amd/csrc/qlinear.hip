@@ -234,9 +234,10 @@ static bool fused_ok(int qtype, int M, int K) {
 
 // Workspace of a call with M > 1 (zero-filled before its first use): the
 // K split's control words at offset 0 for every shape (generation, missed
-// sums; 16 bytes), its block counters, then xq ([M][K], or fragment order
-// with room for 16 rows), xs ([M][K/G], or [K/G][16]) fp32 and (long K on
-// the matrix cores) the K split's part sums.  Offsets in bytes.
+// sums; 16 bytes, room up to byte 256 for the split), its block counters from
+// byte 256, then xq ([M][K], or fragment order with room for 16 rows), xs
+// ([M][K/G], or [K/G][16]) fp32 and (long K on the matrix cores) the K
+// split's part sums.  Offsets in bytes.
 struct WsLayout {
     size_t cnt, xq, xs, sp, total;
     bool split;
@@ -252,7 +253,7 @@ static WsLayout workspace_layout(int qtype, int N, int K, int M) {
     if (fused_ok(qtype, M, K)) return l;
     l.split = M >= 2 && M <= 16 && rc_split_ok(qtype, K);
     l.cnt = (size_t)RC_CTL_CNT * 4;
-    l.xq = WS_CTL_BYTES + (l.split ? align16((size_t)rc_split_counters(N) * 4) : 0);
+    l.xq = l.split ? l.cnt + align16((size_t)rc_split_counters(N) * 4) : WS_CTL_BYTES;
     l.xs = l.xq + workspace_xq(K);
     l.sp = l.xs + workspace_xs(qtype, K);
     l.total = l.sp + (l.split ? rc_split_bytes(N, M) : 0);
