@@ -61,11 +61,13 @@ ROW_BYTES = {4: lambda K: K // 2, 5: lambda K: K * 5 // 8, 6: lambda K: K * 6 //
 GROUP = {4: 64, 5: 64, 6: 64, 8: 32}
 
 
-def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False, prequantized=False):
+def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False, prequantized=False, frag=False):
     """us per call of viper_hip_qlinear (bf16 x, fused or separate quantize) over rotating weights;
     outliers: 5% of the activation channels (a fixed seeded set) scaled x20, as config 4 states;
     prequantized: x quantized once (viper_hip_quantize_act) outside the timed calls, each call
-    viper_hip_qlinear_prequantized (int8 rows and their fp32 group scales in, bf16 y out)."""
+    viper_hip_qlinear_prequantized (int8 rows and their fp32 group scales in, bf16 y out);
+    frag: the same with the rows in the matrix-core fragment order (viper_hip_rmsnorm_quantize_frag of
+    x with gamma = 1 outside the timed calls, each call viper_hip_qlinear_prequantized_frag)."""
     G = GROUP[qtype]
     rb = ROW_BYTES[qtype](K)
     copy_bytes = N * rb + N * (K // G) * 2
@@ -85,11 +87,21 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False, prequa
         if L.viper_hip_quantize_act(G, x.data_ptr(), M, K, xq.data_ptr(), xs.data_ptr(),
                                     torch.cuda.current_stream().cuda_stream) != 0:
             raise RuntimeError("quantize_act failed")
+    if frag:
+        xq = torch.empty(16 * K, dtype=torch.int8, device="cuda")
+        xs = torch.empty(16 * (K // G), dtype=torch.float32, device="cuda")
+        ones = torch.ones(K, dtype=torch.bfloat16, device="cuda")
+        if L.viper_hip_rmsnorm_quantize_frag(x.data_ptr(), ones.data_ptr(), 1e-6, M, K, G, None, xq.data_ptr(),
+                                             xs.data_ptr(), torch.cuda.current_stream().cuda_stream) != 0:
+            raise RuntimeError("rmsnorm_quantize_frag failed")
 
     def launch(i):
         c = i % copies
         st = torch.cuda.current_stream().cuda_stream
-        if prequantized:
+        if frag:
+            rc = L.viper_hip_qlinear_prequantized_frag(qtype, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K,
+                                                       xq.data_ptr(), xs.data_ptr(), M, y.data_ptr(), None, st)
+        elif prequantized:
             rc = L.viper_hip_qlinear_prequantized(qtype, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K,
                                                   xq.data_ptr(), xs.data_ptr(), M, y.data_ptr(), None, st)
         else:
@@ -102,7 +114,7 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False, prequa
     us = time_steps(torch, launch, max(steps, MIN_STEPS))
     del W, S
     alg = algorithmic_bytes(rb, N, K, M, G)
-    if prequantized:  # int8 rows + fp32 group scales in place of the bf16 rows
+    if prequantized or frag:  # int8 rows + fp32 group scales in place of the bf16 rows
         alg += M * K + M * (K // G) * 4 - 2 * M * K
     return round(us, 3), round(alg / (us * 1e-6) / 1e9, 1)
 
@@ -353,10 +365,11 @@ def timeline(torch, L, gen, N, K, qt=4):
                       "percentiles_us_p10_p50_p90_max": rows}), flush=True)
 
 
-def time_config3(torch, stk, fused, replays=10):
+def time_config3(torch, stk, fused, replays=10, prefetch=0):
     """us per config-3 decode step (one graph of the whole step, replayed), its weight + head GB/s,
-    and the launches per step."""
-    run = stk.step_fused if fused else stk.step
+    and the launches per step (prefetch > 0: the fused step with the next slot's weights warmed from a
+    second stream by that many workgroups)."""
+    run = (lambda: stk.step_fused(prefetch)) if fused else stk.step
     run()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
@@ -467,9 +480,12 @@ def main():
     ap.add_argument("--only", default="", metavar="LINE",
                     help="only one line (rocprofv3 runs): config0[_pre], down, verify_mM (K=2560 N=10240) or "
                          "verify_mM_down (K=10240 N=2560), pre_mM[_down] (the same through the prequantized "
-                         "entry, x quantized once outside the timed calls), q5_m1 / q6_m8 / w8_m1 ... "
+                         "entry, x quantized once outside the timed calls), frag_mM[_down] (the same from "
+                         "fragment-order rows), q5_m1 / q6_m8 / w8_m1 ... "
                          "(config 4), FMT_kK_nN_mM (any shape, e.g. q4_k3072_n6144_m1), config1 / "
-                         "config1_2launch (MLP), config3 (fused step) or config3_ref (reference launch sequence)")
+                         "config1_2launch (MLP), config3 (fused step), config3_prefetchW (the fused step with the next slot's "
+                         "weights warmed from a second stream by W workgroups) or config3_ref (reference launch "
+                         "sequence)")
     ap.add_argument("--clock-period", action="store_true",
                     help="only the north-star dispatch period on the device clock: back-to-back sequences of "
                          "10..200 launches between two clock stamps, span per length and the fitted slope "
@@ -517,11 +533,11 @@ def main():
                               prequantized=one == "config0_pre")
         elif one == "down":
             res = time_linear(torch, L, gen, qtype, 2560, 10240, 1, steps=args.steps)
-        elif one.startswith("verify_m") or one.startswith("pre_m"):
+        elif one.startswith("verify_m") or one.startswith("pre_m") or one.startswith("frag_m"):
             Mv = int(one.split("_m")[1].split("_")[0])
             shape = (2560, 10240) if one.endswith("_down") else (10240, 2560)
             res = time_linear(torch, L, gen, qtype, shape[0], shape[1], Mv, steps=args.steps,
-                              prequantized=one.startswith("pre_m"))
+                              prequantized=one.startswith("pre_m"), frag=one.startswith("frag_m"))
         elif re.fullmatch(r"(q4|q5|q6|w8)_k\d+_n\d+_m\d+", one):
             fmt, kk, nn, mm = one.split("_")
             qt = {"q4": 4, "q5": 5, "q6": 6, "w8": 8}[fmt]
@@ -535,9 +551,11 @@ def main():
             r = time_mlp(torch, L, gen, qtype, G, ("ref",) if one == "config1" else ("2launch",))
             key = "mlp_config1_us" if one == "config1" else "mlp_config1_2launch_us"
             res = (r[key], r[key.replace("_us", "_gbs")])
-        elif one in ("config3", "config3_ref"):
+        elif one in ("config3", "config3_ref") or one.startswith("config3_prefetch"):
             from viper_amd.stack import Stack
-            us, gbs, _ = time_config3(torch, Stack(torch), one == "config3", replays=max(10, args.steps // 100))
+            pf = int(one.split("config3_prefetch")[1] or 128) if one.startswith("config3_prefetch") else 0
+            us, gbs, _ = time_config3(torch, Stack(torch), one != "config3_ref", replays=max(10, args.steps // 100),
+                                      prefetch=pf)
             res = (us, gbs)
         else:
             raise SystemExit(f"unknown --only line {one}")

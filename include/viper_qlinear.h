@@ -40,6 +40,12 @@
  *   viper_hip_rmsnorm_quantize      rmsnorm_quantize_bf16 (kernels/ops/rmsnorm_quantize.cu:107-123,
  *                                   declared kernels/ops/rmsnorm_kernel.h), per row.
  *   viper_hip_swiglu_quantize       swiglu_quantize_bf16 (kernels/ops/swiglu_quantize.cu:81-96).
+ *   viper_hip_rmsnorm_quantize_frag, viper_hip_swiglu_quantize_frag
+ *                                   the same for M <= 16 rows in the matrix-core
+ *                                   fragment order (the engine's verify step).
+ *   viper_hip_qlinear_prequantized_frag, viper_hip_qlinear_fused2_prequantized_frag
+ *                                   linear_q4_dp4a_prequantized / dp4a_smem_gemv_fused2
+ *                                   at M = 2..16 from those fragments, one launch.
  *   viper_hip_linear_bf16           linear_bf16 (kernels/ops/linear_bf16_kernel.cu:57-70,
  *                                   declared kernels/ops/linear_bf16_kernel.h): the bf16 LM
  *                                   head GEMV (src/viper/model.cpp:300-304).
@@ -61,6 +67,8 @@
  *                                   streaming dispatch).
  *   viper_hip_clock_stamp           no counterpart: a device-clock reading between
  *                                   launches (measurement).
+ *   viper_hip_prefetch              no counterpart: warms a weight range into the
+ *                                   memory-side cache from a second stream.
  *
  * Formats (qtype values are viper::quant::QType, include/viper/quant.h:19-26):
  *   Q4_G64 (4)  packed [N][K/2]; k even in the low nibble; nibble = w + 8.
@@ -318,6 +326,49 @@ int viper_hip_qlinear_timeline(int qtype, const void* w_packed, const void* w_sc
  * if the folded data equals a fixed word. */
 int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, const void* side, int side_bytes,
                           void* y_bf16, uint32_t* sink, void* stream);
+
+/* Warms `bytes` (a multiple of 16, 16-byte aligned) at buf into the GPU's
+ * memory-side cache with plain loads, split over `workgroups` workgroups of
+ * 256 threads; sink (4 bytes) is written only if the folded data equals a
+ * fixed word.  For a second stream next to the one that runs the current
+ * launches: the next launches' weights then come from the cache.  No
+ * counterpart in the reference. */
+int viper_hip_prefetch(const void* buf, size_t bytes, int workgroups, uint32_t* sink, void* stream);
+
+/* Fragment order of 2..16 quantized activation rows: the matrix-core
+ * operand layout the verify path's GEMM reads directly.  For G = 64,
+ * xfrag [K/64][64 lanes][16 B]: lane 16 * kb + m of group g holds row m's
+ * quarter qi = ((kb & 1) << 1) | (kb >> 1) of the group (k = 64g + 16qi ..
+ * +15) as four 4-byte words: the even k of its first octet, the odd k of
+ * that octet, then the same for the second octet.  For G = 32, xfrag
+ * [K/32][4 kb][16 m][8 B]: row m's octet qi of group g in k order.  xsfrag
+ * [K/G][16] fp32: the scale of row m's group g at g * 16 + m.  Rows M..15 are
+ * never written and never used.  Both buffers 16-byte aligned, sized for 16
+ * rows (K and 4 * K / G * 16 bytes). */
+
+/* rmsnorm_quantize_bf16 / swiglu_quantize_bf16 (kernels/ops/rmsnorm_quantize.cu:107-123,
+ * kernels/ops/swiglu_quantize.cu:81-96) for M <= 16 rows, writing the int8
+ * rows and their scales in the fragment order above instead of [M][K] and
+ * [M][K/G]: the same bytes and scales as viper_hip_rmsnorm_quantize /
+ * viper_hip_swiglu_quantize, so the engine's verify step (M rows,
+ * include/viper/model_impl.cuh:585-607) feeds its linears without a
+ * quantize launch of their own. */
+int viper_hip_rmsnorm_quantize_frag(const void* x_bf16, const void* gamma_bf16, float eps, int M, int H,
+                                    int group, void* out_bf16, void* xfrag, void* xsfrag, void* stream);
+int viper_hip_swiglu_quantize_frag(const void* gate_bf16, const void* up_bf16, int M, int I, int group,
+                                   void* out_bf16, void* xfrag, void* xsfrag, void* stream);
+
+/* linear_q4_dp4a_prequantized{,_residual} (kernels/ops/linear_multim.h:30-41)
+ * and dp4a_smem_gemv_fused2 (kernels/ops/dp4a_smem_kernel.cu:141-152) at
+ * M = 2..16 over activations in the fragment order above: one launch of the
+ * matrix-core kernel, no workspace.  K must be a multiple of 4 groups. */
+int viper_hip_qlinear_prequantized_frag(int qtype, const void* w_packed, const void* w_scales, int scale_enc,
+                                        int group, int N, int K, const void* xfrag, const void* xsfrag, int M,
+                                        void* y_bf16, const void* residual_bf16, void* stream);
+int viper_hip_qlinear_fused2_prequantized_frag(int qtype, const void* w0_packed, const void* w0_scales,
+                                               const void* w1_packed, const void* w1_scales, int scale_enc,
+                                               int group, int N, int K, const void* xfrag, const void* xsfrag,
+                                               int M, void* y0_bf16, void* y1_bf16, void* stream);
 
 /* Measurement probe, no counterpart in the reference: one launch of one
  * wave that writes the GPU's constant 100 MHz counter (s_memrealtime) to

@@ -1,0 +1,206 @@
+"""The verify step's one-launch linears: producers writing the int8 rows in
+the matrix-core fragment order and the GEMM reading them.
+
+The fragment order is restated here from its description in
+include/viper_qlinear.h (to_frag below), so a producer that wrote bytes to the
+wrong lane, k-slot or octet half fails against the natural-layout producer.
+Bar: fragment bytes and scales bit-exact against the natural-layout producer
+(itself pinned against the oracle in test_gpu_producers.py); GEMM outputs
+within 1 bf16 ulp or 1e-5 * sum |group terms| of the oracle, and equal bit for
+bit to the natural-layout prequantized entry where that runs the same
+matrix-core kernel (more than 4 rows).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import viper_amd as va
+
+pytestmark = pytest.mark.gpu
+REL_TOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.fail("GPU tests need a ROCm GPU (run them on the MI355X box)")
+    return torch
+
+
+def dev(torch, a):
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a).to("cuda")
+
+
+def u16(t):
+    return t.cpu().numpy().view(np.uint16)
+
+
+def to_frag(xq, xs, G):
+    """Natural layout (xq [M][K] int8, xs [M][K/G] fp32) -> fragment order, 16 rows, as the header
+    states it; entries of rows M..15 are left at -1 (int8) / NaN (fp32) to mark "never written"."""
+    M, K = xq.shape
+    frag = np.full(K * 16, -1, dtype=np.int8)
+    sf = np.full((K // G) * 16, np.nan, dtype=np.float32)
+    for m in range(M):
+        for g in range(K // G):
+            sf[g * 16 + m] = xs[m, g]
+            if G == 64:
+                for kb in range(4):
+                    qi = ((kb & 1) << 1) | (kb >> 1)
+                    v = xq[m, g * 64 + 16 * qi: g * 64 + 16 * qi + 16]
+                    word = np.concatenate([v[0:8:2], v[1:8:2], v[8:16:2], v[9:16:2]])
+                    L = 16 * kb + m
+                    frag[(g * 64 + L) * 16:(g * 64 + L) * 16 + 16] = word
+            else:
+                for kb in range(4):
+                    qi = ((kb & 1) << 1) | (kb >> 1)
+                    v = xq[m, g * 32 + 8 * qi: g * 32 + 8 * qi + 8]
+                    off = ((g * 4 + kb) * 16 + m) * 8
+                    frag[off:off + 8] = v
+    return frag, sf
+
+
+def _frag_buffers(torch, K, G):
+    nq, ns = va.frag_bytes(K, G)
+    xf = torch.full((nq,), -1, dtype=torch.int8, device="cuda")
+    sf = torch.full((ns // 4,), float("nan"), dtype=torch.float32, device="cuda")
+    return xf, sf
+
+
+def _check_frag(xf, sf, want_q, want_s):
+    got_q = xf.cpu().numpy()
+    got_s = sf.cpu().numpy()
+    np.testing.assert_array_equal(got_q, want_q)
+    wrote = ~np.isnan(want_s)
+    np.testing.assert_array_equal(got_s[wrote].view(np.uint32), want_s[wrote].view(np.uint32))
+    assert np.isnan(got_s[~wrote]).all()          # rows M..15: never written
+
+
+def bf16(a):
+    return O.f32_to_bf16(np.asarray(a, dtype=np.float32))
+
+
+@pytest.mark.parametrize("G", [64, 32])
+@pytest.mark.parametrize("M,H", [(2, 2560), (5, 3072), (16, 2560), (9, 10240)])
+def test_rmsnorm_quantize_frag_equals_natural(torch_dev, M, H, G):
+    torch = torch_dev
+    print(f"rmsnorm frag M={M} H={H} G={G}", flush=True)
+    x = dev(torch, O.gen_act(M, H, 700 + M, outlier_frac=0.05))
+    rng = np.random.default_rng(701)
+    gamma = dev(torch, bf16(1.0 + 0.1 * rng.standard_normal(H)))
+    xq = torch.zeros((M, H), dtype=torch.int8, device="cuda")
+    xs = torch.zeros((M, H // G), dtype=torch.float32, device="cuda")
+    out = torch.zeros((M, H), dtype=torch.int16, device="cuda")
+    assert va.rmsnorm_quantize(x, gamma, 1e-6, G, xq, xs, out=out).ok()
+    xf, sf = _frag_buffers(torch, H, G)
+    out2 = torch.zeros_like(out)
+    assert va.rmsnorm_quantize_frag(x, gamma, 1e-6, G, xf, sf, out=out2).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(out2), u16(out))
+    want_q, want_s = to_frag(xq.cpu().numpy(), xs.cpu().numpy(), G)
+    _check_frag(xf, sf, want_q, want_s)
+
+
+@pytest.mark.parametrize("G", [64, 32])
+@pytest.mark.parametrize("M,I", [(3, 10240), (16, 2560), (8, 10752)])
+def test_swiglu_quantize_frag_equals_natural(torch_dev, M, I, G):
+    torch = torch_dev
+    print(f"swiglu frag M={M} I={I} G={G}", flush=True)
+    rng = np.random.default_rng(710 + M)
+    g = dev(torch, bf16(3.0 * rng.standard_normal((M, I))))
+    u = dev(torch, bf16(rng.standard_normal((M, I))))
+    xq = torch.zeros((M, I), dtype=torch.int8, device="cuda")
+    xs = torch.zeros((M, I // G), dtype=torch.float32, device="cuda")
+    h = torch.zeros((M, I), dtype=torch.int16, device="cuda")
+    assert va.swiglu_quantize(g, u, G, xq, xs, out=h).ok()
+    xf, sf = _frag_buffers(torch, I, G)
+    h2 = torch.zeros_like(h)
+    assert va.swiglu_quantize_frag(g, u, G, xf, sf, out=h2).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(h2), u16(h))
+    want_q, want_s = to_frag(xq.cpu().numpy(), xs.cpu().numpy(), G)
+    _check_frag(xf, sf, want_q, want_s)
+
+
+# The GEMM from fragments: every format, single-segment and long-K (segment
+# loop) shapes, the north-star verify at full size, the reference engine's q
+# and down shapes, residual, ragged N.
+@pytest.mark.parametrize("qtype,N,K,M", [
+    (O.Q4_G64, 10240, 2560, 16),
+    (O.Q4_G64, 2560, 10240, 8),
+    (O.Q4_G64, 6144, 3072, 16),
+    (O.Q4_G64, 3072, 10752, 5),
+    (O.Q5_G64, 1000, 2560, 7),
+    (O.Q6_G64, 777, 4096, 12),
+    (O.W8_G32, 1001, 2560, 16),
+    (O.W8_G32, 513, 6144, 3),
+])
+def test_prequantized_frag_against_oracle(torch_dev, qtype, N, K, M):
+    torch = torch_dev
+    print(f"frag gemm qtype={qtype} N={N} K={K} M={M}", flush=True)
+    G = O.group_size(qtype)
+    packed, scales = O.gen_weights(qtype, N, K, 720 + N, O.SCALE_FP16)
+    x = O.gen_act(M, K, 721, outlier_frac=0.05)
+    xq, xs = O.quantize_act(x, G)
+    res = O.gen_act(M, N, 722) if M % 2 == 1 else None
+    y_ref, _, absterm = O.qlinear_prequant(qtype, packed, scales, O.SCALE_FP16, N, K, xq, xs, residual=res)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, va.ScaleEnc.FP16)
+    fq, fs = to_frag(np.asarray(xq, dtype=np.int8).reshape(M, K), np.asarray(xs, dtype=np.float32).reshape(M, K // G), G)
+    xf, sf = dev(torch, fq), dev(torch, fs)
+    rd = None if res is None else dev(torch, res)
+    y = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    assert va.linear_prequantized_frag(w, xf, sf, y, residual=rd).ok()
+    y_nat = torch.zeros_like(y)
+    assert va.linear_prequantized(w, dev(torch, np.asarray(xq, dtype=np.int8)), dev(torch, np.asarray(xs, dtype=np.float32)),
+                                  y_nat, residual=rd).ok()
+    torch.cuda.synchronize()
+    O.assert_bf16_close(u16(y), y_ref, absterm, rel=REL_TOL)
+    O.assert_bf16_close(u16(y_nat), y_ref, absterm, rel=REL_TOL)
+    if M > 4:   # the natural entry runs the same matrix-core kernel there (2-4 rows: the dot kernel, whose
+        np.testing.assert_array_equal(u16(y), u16(y_nat))   # fp32 sums are added in another order)
+
+
+def test_fused2_frag_equals_two_calls(torch_dev):
+    torch = torch_dev
+    qtype, N, K, M = O.Q4_G64, 1024, 3072, 16
+    ws = []
+    for i in range(2):
+        p, s = O.gen_weights(qtype, N, K, 730 + i, O.SCALE_BF16)
+        ws.append(va.QuantizedWeight(va.QType(qtype), dev(torch, p), dev(torch, s), N, K, 64, va.ScaleEnc.BF16))
+    x = dev(torch, O.gen_act(M, K, 732))
+    rng = np.random.default_rng(733)
+    gamma = dev(torch, bf16(1.0 + 0.1 * rng.standard_normal(K)))
+    xf, sf = _frag_buffers(torch, K, 64)
+    assert va.rmsnorm_quantize_frag(x, gamma, 1e-6, 64, xf, sf).ok()
+    z = lambda: torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    y0, y1, r0, r1 = z(), z(), z(), z()
+    assert va.linear_fused2_prequantized_frag(ws[0], ws[1], xf, sf, y0, y1).ok()
+    assert va.linear_prequantized_frag(ws[0], xf, sf, r0).ok()
+    assert va.linear_prequantized_frag(ws[1], xf, sf, r1).ok()
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(y0), u16(r0))
+    np.testing.assert_array_equal(u16(y1), u16(r1))
+
+
+def test_frag_entry_errors(torch_dev):
+    torch = torch_dev
+    L = va.lib()
+    p, s = O.gen_weights(O.Q4_G64, 64, 512, 740, O.SCALE_FP16)
+    w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, p), dev(torch, s), 64, 512, 64, va.ScaleEnc.FP16)
+    xf, sf = _frag_buffers(torch, 512, 64)
+    y1 = torch.zeros((1, 64), dtype=torch.int16, device="cuda")
+    assert va.linear_prequantized_frag(w, xf, sf, y1).code == va.StatusCode.INVALID_ARGUMENT     # M = 1
+    y = torch.zeros((4, 64), dtype=torch.int16, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    assert L.viper_hip_qlinear_prequantized_frag(4, w.data.data_ptr(), w.scales.data_ptr(), 0, 64, 64, 512,
+                                                 xf.data_ptr() + 8, sf.data_ptr(), 4, y.data_ptr(), None, st) == 2
+    p2, s2 = O.gen_weights(O.Q4_G64, 64, 128, 741, O.SCALE_FP16)   # K = 2 groups: not a multiple of 4
+    w2 = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, p2), dev(torch, s2), 64, 128, 64, va.ScaleEnc.FP16)
+    assert va.linear_prequantized_frag(w2, xf, sf, y).code == va.StatusCode.INVALID_ARGUMENT
+    x = dev(torch, O.gen_act(17, 512, 742))
+    g = dev(torch, bf16(np.ones(512)))
+    assert va.rmsnorm_quantize_frag(x, g, 1e-6, 64, xf, sf).code == va.StatusCode.INVALID_ARGUMENT  # M = 17

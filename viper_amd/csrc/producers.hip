@@ -52,23 +52,37 @@ __device__ __forceinline__ u32x4 pack8(const float* f) {
     return u32x4{f2bf2(f[0], f[1]), f2bf2(f[2], f[3]), f2bf2(f[4], f[5]), f2bf2(f[6], f[7])};
 }
 
-// Quantize the bf16 octet v (octet o of a row of K elements) into xq/xs; all
-// lanes of the wave call this together (the group amax is a DPP reduction).
-template <int G>
-__device__ __forceinline__ void quantize_store(const u32x4& v, bool ok, int o, int8_t* xq, float* xs) {
+// Quantize the bf16 octet v (octet o of row `row`) into xq/xs; all lanes of
+// the wave call this together (the group amax is a DPP reduction).
+// Natural layout (FRAG false): xq/xs point at the row, xq [K] int8 in k order,
+// xs [K/G] fp32.  Fragment layout (FRAG true, at most 16 rows): the matrix-core
+// operand order the fragment quantize writes, xq and xs the whole buffers --
+// group g's quarter qi (16 values; G = 32: its octet qi) sits in k-slot
+// kb = bit-swap(qi) of lane 16 * kb + row, 64-groups as [even k | odd k] per
+// octet, 32-groups in k order; xs [K/G][16].
+template <int G, bool FRAG>
+__device__ __forceinline__ void quantize_store(const u32x4& v, bool ok, int o, int row, int8_t* xq, float* xs) {
     uint32_t d0, d1;
     float s;
-    quantize_octet<G, false>(v, d0, d1, s);
+    quantize_octet<G, FRAG && G == 64>(v, d0, d1, s);
     if (ok) {
-        *(u32x2*)(xq + (size_t)o * 8) = u32x2{d0, d1};
-        if ((o & (G / 8 - 1)) == 0) xs[o / (G / 8)] = s;
+        if constexpr (FRAG) {
+            constexpr int Q = G == 64 ? 16 : 8;  // fragment bytes per lane and group
+            const int k0 = o * 8, g = k0 / G, qi = (k0 % G) / Q;
+            const int kb = ((qi & 1) << 1) | (qi >> 1);
+            *(u32x2*)(xq + ((size_t)(g * 4 + kb) * 16 + row) * Q + k0 % Q) = u32x2{d0, d1};
+            if ((o & (G / 8 - 1)) == 0) xs[g * 16 + row] = s;
+        } else {
+            *(u32x2*)(xq + (size_t)o * 8) = u32x2{d0, d1};
+            if ((o & (G / 8 - 1)) == 0) xs[o / (G / 8)] = s;
+        }
     }
 }
 
 // One workgroup per row; bd = the workgroup size, a multiple of 64 (an
 // argument rather than blockDim.x, which is a hidden argument the wave would
 // wait for before its first load).
-template <int G>
+template <int G, bool FRAG>
 __global__ void __launch_bounds__(1024)
 rmsnorm_quantize_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, float eps,
                         int H, uint16_t* out, int8_t* __restrict__ xq, float* __restrict__ xs, int bd) {
@@ -91,8 +105,8 @@ rmsnorm_quantize_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
     ss = block_sum(ss, red, bd);
     const float inv = __builtin_amdgcn_rsqf(ss / (float)H + eps);
 
-    int8_t* qr = xq + (size_t)row * H;
-    float* sr = xs + (size_t)row * (H / G);
+    int8_t* qr = FRAG ? xq : xq + (size_t)row * H;
+    float* sr = FRAG ? xs : xs + (size_t)row * (H / G);
     for (int it = 0; it < iters; ++it) {
         const int o = (int)threadIdx.x + it * bd;
         const bool ok = o < noct;
@@ -106,13 +120,13 @@ rmsnorm_quantize_kernel(const uint16_t* __restrict__ x, const uint16_t* __restri
             v = pack8(f);
             if (out != nullptr) *(u32x4*)(out + (size_t)row * H + (size_t)o * 8) = v;
         }
-        quantize_store<G>(v, ok, o, qr, sr);
+        quantize_store<G, FRAG>(v, ok, o, row, qr, sr);
     }
 }
 
 // Workgroups tile each row (blockIdx.y = row); in place (out == gate) is
 // allowed: every element is read before the same thread writes it.
-template <int G>
+template <int G, bool FRAG>
 __global__ void __launch_bounds__(PR_NT)
 swiglu_quantize_kernel(const uint16_t* gate, const uint16_t* __restrict__ up, int I, uint16_t* out,
                        int8_t* __restrict__ xq, float* __restrict__ xs) {
@@ -131,7 +145,8 @@ swiglu_quantize_kernel(const uint16_t* gate, const uint16_t* __restrict__ up, in
         v = pack8(g);
         if (out != nullptr) *(u32x4*)(out + base) = v;
     }
-    quantize_store<G>(v, ok, o, xq + (size_t)row * I, xs + (size_t)row * (I / G));
+    if constexpr (FRAG) quantize_store<G, true>(v, ok, o, row, xq, xs);
+    else quantize_store<G, false>(v, ok, o, row, xq + (size_t)row * I, xs + (size_t)row * (I / G));
 }
 
 static int check_producer(int group, int M, int K, const void* a, const void* b, const void* out,
@@ -148,11 +163,13 @@ static int check_producer(int group, int M, int K, const void* a, const void* b,
 
 }  // namespace vq
 
-extern "C" int viper_hip_rmsnorm_quantize(const void* x_bf16, const void* gamma_bf16, float eps, int M,
-                                          int H, int group, void* out_bf16, void* xq, void* xs,
-                                          void* stream) {
-    int rc = vq::check_producer(group, M, H, x_bf16, gamma_bf16, out_bf16, xq, xs);
+namespace vq {
+
+static int rmsnorm_launch(const void* x_bf16, const void* gamma_bf16, float eps, int M, int H, int group,
+                          void* out_bf16, void* xq, void* xs, bool frag, void* stream) {
+    int rc = check_producer(group, M, H, x_bf16, gamma_bf16, out_bf16, xq, xs);
     if (rc != VIPER_OK) return rc;
+    if (frag && (M > 16 || misaligned(xq, 16) || misaligned(xs, 16))) return VIPER_INVALID_ARGUMENT;
     const int noct = H / 8;
     const int bd64 = (noct + 63) / 64 * 64;
     const unsigned bd = (unsigned)(bd64 < 1024 ? bd64 : 1024);
@@ -163,25 +180,54 @@ extern "C" int viper_hip_rmsnorm_quantize(const void* x_bf16, const void* gamma_
     float* a6 = (float*)xs;
     int bdi = (int)bd;
     void* args[] = {&a0, &a1, &eps, &H, &a4, &a5, &a6, &bdi};
-    const void* fn = group == 64 ? (const void*)vq::rmsnorm_quantize_kernel<64>
-                                 : (const void*)vq::rmsnorm_quantize_kernel<32>;
+    const void* fn = group == 64 ? (frag ? (const void*)rmsnorm_quantize_kernel<64, true>
+                                         : (const void*)rmsnorm_quantize_kernel<64, false>)
+                                 : (frag ? (const void*)rmsnorm_quantize_kernel<32, true>
+                                         : (const void*)rmsnorm_quantize_kernel<32, false>);
     (void)hipLaunchKernel(fn, dim3((unsigned)M), dim3(bd), args, 0, (hipStream_t)stream);
-    return vq::status_of(hipGetLastError());
+    return status_of(hipGetLastError());
 }
 
-extern "C" int viper_hip_swiglu_quantize(const void* gate_bf16, const void* up_bf16, int M, int I,
-                                         int group, void* out_bf16, void* xq, void* xs, void* stream) {
-    int rc = vq::check_producer(group, M, I, gate_bf16, up_bf16, out_bf16, xq, xs);
+static int swiglu_launch(const void* gate_bf16, const void* up_bf16, int M, int I, int group, void* out_bf16,
+                         void* xq, void* xs, bool frag, void* stream) {
+    int rc = check_producer(group, M, I, gate_bf16, up_bf16, out_bf16, xq, xs);
     if (rc != VIPER_OK) return rc;
-    const unsigned gx = (unsigned)((I / 8 + vq::PR_NT - 1) / vq::PR_NT);
+    if (frag && (M > 16 || misaligned(xq, 16) || misaligned(xs, 16))) return VIPER_INVALID_ARGUMENT;
+    const unsigned gx = (unsigned)((I / 8 + PR_NT - 1) / PR_NT);
     const uint16_t* a0 = (const uint16_t*)gate_bf16;
     const uint16_t* a1 = (const uint16_t*)up_bf16;
     uint16_t* a3 = (uint16_t*)out_bf16;
     int8_t* a4 = (int8_t*)xq;
     float* a5 = (float*)xs;
     void* args[] = {&a0, &a1, &I, &a3, &a4, &a5};
-    const void* fn = group == 64 ? (const void*)vq::swiglu_quantize_kernel<64>
-                                 : (const void*)vq::swiglu_quantize_kernel<32>;
-    (void)hipLaunchKernel(fn, dim3(gx, (unsigned)M), dim3(vq::PR_NT), args, 0, (hipStream_t)stream);
-    return vq::status_of(hipGetLastError());
+    const void* fn = group == 64 ? (frag ? (const void*)swiglu_quantize_kernel<64, true>
+                                         : (const void*)swiglu_quantize_kernel<64, false>)
+                                 : (frag ? (const void*)swiglu_quantize_kernel<32, true>
+                                         : (const void*)swiglu_quantize_kernel<32, false>);
+    (void)hipLaunchKernel(fn, dim3(gx, (unsigned)M), dim3(PR_NT), args, 0, (hipStream_t)stream);
+    return status_of(hipGetLastError());
+}
+
+}  // namespace vq
+
+extern "C" int viper_hip_rmsnorm_quantize(const void* x_bf16, const void* gamma_bf16, float eps, int M,
+                                          int H, int group, void* out_bf16, void* xq, void* xs,
+                                          void* stream) {
+    return vq::rmsnorm_launch(x_bf16, gamma_bf16, eps, M, H, group, out_bf16, xq, xs, false, stream);
+}
+
+extern "C" int viper_hip_swiglu_quantize(const void* gate_bf16, const void* up_bf16, int M, int I,
+                                         int group, void* out_bf16, void* xq, void* xs, void* stream) {
+    return vq::swiglu_launch(gate_bf16, up_bf16, M, I, group, out_bf16, xq, xs, false, stream);
+}
+
+extern "C" int viper_hip_rmsnorm_quantize_frag(const void* x_bf16, const void* gamma_bf16, float eps, int M,
+                                               int H, int group, void* out_bf16, void* xfrag, void* xsfrag,
+                                               void* stream) {
+    return vq::rmsnorm_launch(x_bf16, gamma_bf16, eps, M, H, group, out_bf16, xfrag, xsfrag, true, stream);
+}
+
+extern "C" int viper_hip_swiglu_quantize_frag(const void* gate_bf16, const void* up_bf16, int M, int I,
+                                              int group, void* out_bf16, void* xfrag, void* xsfrag, void* stream) {
+    return vq::swiglu_launch(gate_bf16, up_bf16, M, I, group, out_bf16, xfrag, xsfrag, true, stream);
 }

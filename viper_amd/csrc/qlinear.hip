@@ -387,6 +387,24 @@ static int prequant_common(int qtype, const void* w, const void* s, int senc, in
     return rc;
 }
 
+// 2..16 int8 rows already in the matrix-core fragment order (a producer's
+// fragment output): one launch of the row-contiguous matrix-core kernel, no
+// workspace (long K runs its segment loop rather than the K split, whose
+// control words a preceding launch would have to reset).
+static int prequant_frag(int qtype, const void* w, const void* s, int senc, int group, int N, int K,
+                         const void* xf, const void* xsf, int M, void* y, const void* res, void* stream,
+                         Second b = Second()) {
+    int rc = validate_weights(qtype, w, s, senc, group, N, K, M);
+    if (rc != VIPER_OK) return rc;
+    if (xf == nullptr || xsf == nullptr || y == nullptr || M < 2 || !rc_ok(qtype, K)) return VIPER_INVALID_ARGUMENT;
+    if (misaligned(xf, 16) || misaligned(xsf, 16) || misaligned(y, 2) || misaligned(res, 2))
+        return VIPER_INVALID_ARGUMENT;
+    rc = validate_second(b, qtype, senc, group, N, K, M, res, nullptr);
+    if (rc != VIPER_OK) return rc;
+    return launch_rc(qtype, w, s, senc, N, K, xf, xsf, RC_FRAG, M, y, res, nullptr, b.w, b.s, b.y,
+                     (hipStream_t)stream);
+}
+
 }  // namespace vq
 
 // ------------------------------------------------------------------- C ABI
@@ -485,6 +503,24 @@ extern "C" int viper_hip_qlinear_fused2_prequantized(int qtype, const void* w0_p
     if (w1_packed == nullptr || w1_scales == nullptr || y1_bf16 == nullptr) return VIPER_INVALID_ARGUMENT;
     return vq::prequant_common(qtype, w0_packed, w0_scales, scale_enc, group, N, K, xq, xs, M, y0_bf16,
                                nullptr, stream, vq::Second{w1_packed, w1_scales, y1_bf16});
+}
+
+extern "C" int viper_hip_qlinear_prequantized_frag(int qtype, const void* w_packed, const void* w_scales,
+                                                   int scale_enc, int group, int N, int K, const void* xfrag,
+                                                   const void* xsfrag, int M, void* y_bf16,
+                                                   const void* residual_bf16, void* stream) {
+    return vq::prequant_frag(qtype, w_packed, w_scales, scale_enc, group, N, K, xfrag, xsfrag, M, y_bf16,
+                             residual_bf16, stream);
+}
+
+extern "C" int viper_hip_qlinear_fused2_prequantized_frag(int qtype, const void* w0_packed,
+                                                          const void* w0_scales, const void* w1_packed,
+                                                          const void* w1_scales, int scale_enc, int group,
+                                                          int N, int K, const void* xfrag, const void* xsfrag,
+                                                          int M, void* y0_bf16, void* y1_bf16, void* stream) {
+    if (w1_packed == nullptr || w1_scales == nullptr || y1_bf16 == nullptr) return VIPER_INVALID_ARGUMENT;
+    return vq::prequant_frag(qtype, w0_packed, w0_scales, scale_enc, group, N, K, xfrag, xsfrag, M, y0_bf16,
+                             nullptr, stream, vq::Second{w1_packed, w1_scales, y1_bf16});
 }
 
 extern "C" int viper_hip_qlinear_m1(int qtype, int scale_enc, int group, int K, int prologue, const void* a,

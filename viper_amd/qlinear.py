@@ -136,6 +136,11 @@ _SYMBOLS = (
     "viper_hip_qlinear_timeline",
     "viper_hip_check_bf16_rounding",
     "viper_hip_clock_stamp",
+    "viper_hip_prefetch",
+    "viper_hip_rmsnorm_quantize_frag",
+    "viper_hip_swiglu_quantize_frag",
+    "viper_hip_qlinear_prequantized_frag",
+    "viper_hip_qlinear_fused2_prequantized_frag",
 )
 
 
@@ -176,6 +181,17 @@ def lib():
     L.viper_hip_stream_read.restype = i32
     L.viper_hip_clock_stamp.argtypes = [vp, vp]
     L.viper_hip_clock_stamp.restype = i32
+    L.viper_hip_prefetch.argtypes = [vp, sz, i32, vp, vp]
+    L.viper_hip_prefetch.restype = i32
+    L.viper_hip_rmsnorm_quantize_frag.argtypes = [vp, vp, C.c_float, i32, i32, i32, vp, vp, vp, vp]
+    L.viper_hip_rmsnorm_quantize_frag.restype = i32
+    L.viper_hip_swiglu_quantize_frag.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, vp]
+    L.viper_hip_swiglu_quantize_frag.restype = i32
+    L.viper_hip_qlinear_prequantized_frag.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp]
+    L.viper_hip_qlinear_prequantized_frag.restype = i32
+    L.viper_hip_qlinear_fused2_prequantized_frag.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, i32,
+                                                             vp, vp, vp]
+    L.viper_hip_qlinear_fused2_prequantized_frag.restype = i32
     L.viper_hip_qlinear_fused2.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     L.viper_hip_qlinear_fused2.restype = i32
     L.viper_hip_qlinear_fused2_prequantized.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, i32,
@@ -362,6 +378,52 @@ def swiglu_quantize(gate, up, group, xq, xs, out=None, stream=None) -> Status:
     rc = lib().viper_hip_swiglu_quantize(ptr(gate, 2), ptr(up, 2), M, I, group, ptr(out, 2), ptr(xq, 1), ptr(xs, 4),
                                          _stream(stream))
     return _status(rc, "viper_hip_swiglu_quantize")
+
+
+def frag_bytes(K: int, group: int):
+    """Bytes of the fragment-order activation buffers for up to 16 rows: (xfrag, xsfrag)."""
+    return K * 16, (K // group) * 16 * 4
+
+
+def rmsnorm_quantize_frag(x, gamma, eps, group, xfrag, xsfrag, out=None, stream=None) -> Status:
+    """rmsnorm_quantize for M <= 16 rows of x [M, H], the int8 rows and scales in fragment order."""
+    H = gamma.numel()
+    M = int(x.numel() // H)
+    rc = lib().viper_hip_rmsnorm_quantize_frag(ptr(x, 2), ptr(gamma, 2), float(eps), M, H, group, ptr(out, 2),
+                                               ptr(xfrag, 1), ptr(xsfrag, 4), _stream(stream))
+    return _status(rc, "viper_hip_rmsnorm_quantize_frag")
+
+
+def swiglu_quantize_frag(gate, up, group, xfrag, xsfrag, out=None, stream=None) -> Status:
+    """swiglu_quantize for M <= 16 rows of [M, I], the int8 rows and scales in fragment order."""
+    I = gate.shape[-1]
+    M = int(gate.numel() // I)
+    rc = lib().viper_hip_swiglu_quantize_frag(ptr(gate, 2), ptr(up, 2), M, I, group, ptr(out, 2), ptr(xfrag, 1),
+                                              ptr(xsfrag, 4), _stream(stream))
+    return _status(rc, "viper_hip_swiglu_quantize_frag")
+
+
+def linear_prequantized_frag(w: QuantizedWeight, xfrag, xsfrag, y, residual=None, stream=None) -> Status:
+    """y [M, N] (M = 2..16) from int8 rows in fragment order (rmsnorm/swiglu_quantize_frag)."""
+    K, N = w.cols, w.rows
+    M = int(y.numel() // N)
+    rc = lib().viper_hip_qlinear_prequantized_frag(int(w.qtype), ptr(w.data, 1), ptr(w.scales, 2), int(w.scale_enc),
+                                                   w.group_size, N, K, ptr(xfrag, 1), ptr(xsfrag, 4), M, ptr(y, 2),
+                                                   ptr(residual, 2), _stream(stream))
+    return _status(rc, "viper_hip_qlinear_prequantized_frag")
+
+
+def linear_fused2_prequantized_frag(w0: QuantizedWeight, w1: QuantizedWeight, xfrag, xsfrag, y0, y1,
+                                    stream=None) -> Status:
+    if not _same_kind(w0, w1):
+        return Status(StatusCode.SHAPE_MISMATCH, "linear_fused2: the two weights differ in kind or shape")
+    K, N = w0.cols, w0.rows
+    M = int(y0.numel() // N)
+    rc = lib().viper_hip_qlinear_fused2_prequantized_frag(int(w0.qtype), ptr(w0.data, 1), ptr(w0.scales, 2),
+                                                          ptr(w1.data, 1), ptr(w1.scales, 2), int(w0.scale_enc),
+                                                          w0.group_size, N, K, ptr(xfrag, 1), ptr(xsfrag, 4), M,
+                                                          ptr(y0, 2), ptr(y1, 2), _stream(stream))
+    return _status(rc, "viper_hip_qlinear_fused2_prequantized_frag")
 
 
 class Prologue(enum.IntEnum):

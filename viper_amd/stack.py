@@ -45,15 +45,24 @@ class Stack:
         self.gen = g
         H, I, nQ, nKV = self.H, self.I, self.nQ, self.nKV
         shapes = [(nQ, H), (nKV, H), (nKV, H), (H, nQ), (I, H), (I, H), (H, I)]
-        self.w = []   # per layer: 7 (packed, scales) pairs
+        self.w = []        # per layer: 7 (packed, scales, N, K), views of the layer's arena
+        self.arenas = []   # per layer: one device buffer, every section at a 256-byte aligned offset
+        sec = lambda nbytes: (nbytes + 255) // 256 * 256
         for _ in range(layers):
-            lw = []
+            arena = torch.empty(sum(sec(n * k // 2) + sec(n * (k // 64) * 2) for n, k in shapes), dtype=torch.uint8,
+                                device="cuda")
+            lw, off = [], 0
             for (n, k) in shapes:
-                packed = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device="cuda", generator=g)
+                packed = arena[off:off + n * k // 2]
+                packed.copy_(torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device="cuda", generator=g))
+                off += sec(n * k // 2)
                 u = torch.rand((n * (k // 64),), device="cuda", generator=g)
-                scales = torch.exp(math.log(1e-3) + u * math.log(10.0)).to(torch.float16)
+                scales = arena[off:off + n * (k // 64) * 2].view(torch.float16)
+                scales.copy_(torch.exp(math.log(1e-3) + u * math.log(10.0)).to(torch.float16))
+                off += sec(n * (k // 64) * 2)
                 lw.append((packed, scales, n, k))
             self.w.append(lw)
+            self.arenas.append(arena)
         bf = torch.bfloat16
         self.ln = [(1.0 + 0.05 * torch.randn((H,), device="cuda", generator=g)).to(bf) for _ in range(2 * layers)]
         self.final_ln = (1.0 + 0.05 * torch.randn((H,), device="cuda", generator=g)).to(bf)
@@ -79,6 +88,9 @@ class Stack:
         # kernels' optional outputs, so a test can check each launch in turn
         self.trace = False
         self.g = torch.empty((1, I), dtype=bf, device="cuda")
+        # MALL warming of the next slot's weights from a second stream (default priority)
+        self.side = None
+        self.sink = torch.zeros((1,), dtype=torch.int32, device="cuda")
         L = _q.lib()
         self.L = L
 
@@ -171,16 +183,40 @@ class Stack:
         else:
             self._ok(L.viper_hip_sampling_greedy(p(self.logits), p(self.token), 1, self.V, st), "greedy")
 
-    def _step(self, fused):
+    def _prefetch(self, layer, workgroups):
+        """Warm `layer`'s weight arena into the memory-side cache on the side stream, after the main
+        stream's work so far has been issued (the event orders nothing on the main stream)."""
+        torch = self.torch
+        main = torch.cuda.current_stream()
+        ev = torch.cuda.Event()
+        ev.record(main)
+        self.side.wait_event(ev)
+        a = self.arenas[layer]
+        self._ok(self.L.viper_hip_prefetch(a.data_ptr(), a.numel(), workgroups, self.sink.data_ptr(),
+                                           self.side.cuda_stream), "prefetch")
+
+    def _step(self, fused, prefetch=0):
+        torch = self.torch
         self.x.copy_(self.x0)
-        for l in range(self.layers * self.passes):
+        slots = self.layers * self.passes
+        if prefetch:
+            if self.side is None:
+                self.side = torch.cuda.Stream()
+            self.side.wait_stream(torch.cuda.current_stream())
+        for l in range(slots):
+            if prefetch and l + 1 < slots:
+                self._prefetch((l + 1) % self.layers, prefetch)
             self.attention_half(l, fused)
             self.mlp_half(l, fused)
+        if prefetch:
+            torch.cuda.current_stream().wait_stream(self.side)
         self.head_step(fused)
 
-    def step_fused(self):
-        """One decode step, 4 launches per slot (producers folded, q/k/v together)."""
-        self._step(True)
+    def step_fused(self, prefetch=0):
+        """One decode step, 4 launches per slot (producers folded, q/k/v together).  prefetch > 0:
+        while slot s runs, a second stream warms slot s + 1's weights into the memory-side cache with
+        that many workgroups (viper_hip_prefetch); the results are the same bit for bit."""
+        self._step(True, prefetch)
 
     def step(self):
         """One decode step of the linear path, reference launch sequence."""
