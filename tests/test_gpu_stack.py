@@ -178,3 +178,30 @@ def test_stack_step_graph_replays_equal_eager(torch_dev, fused):
         torch.cuda.synchronize()
         np.testing.assert_array_equal(u16(s.logits), logits)
     assert int(s.greedy_ws.count_nonzero()) == 0
+
+
+def test_stack_step_prefetch_equals_plain(torch_dev):
+    """The fused step with the next slot's weights warmed from a second stream
+    (viper_hip_prefetch) gives the plain fused step's logits and token bit for
+    bit, eagerly and as graph replays (the warming only reads)."""
+    torch = torch_dev
+    from viper_amd.stack import Stack
+    s = Stack(torch, hidden=512, inter=1024, n_heads=4, n_kv_heads=1, head_dim=128, layers=3, passes=2,
+              vocab=20000, seed=13)
+    s.step_fused()
+    torch.cuda.synchronize()
+    logits, token = u16(s.logits), int(s.token.item())
+    s.step_fused(prefetch=64)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(u16(s.logits), logits)
+    assert int(s.token.item()) == token
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        s.step_fused(prefetch=64)
+    for i in range(2):
+        s.logits.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(u16(s.logits), logits, err_msg=f"replay {i}")
+        assert int(s.token.item()) == token
+    assert int(s.sink.item()) == 0
