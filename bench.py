@@ -365,6 +365,56 @@ def timeline(torch, L, gen, N, K, qt=4):
                       "percentiles_us_p10_p50_p90_max": rows}), flush=True)
 
 
+def timeline_rc(torch, L, gen, N, K, M):
+    """Per-wave timeline of the M-row matrix-core GEMM (Q4_G64, fragment input:
+    viper_hip_qlinear_frag_timeline) at shape (K, N): percentiles of each stamp over all waves of one
+    dispatch (the last of a back-to-back sequence over rotating weights), in us from the first wave's
+    start."""
+    G = 64
+    copy_bytes = N * (K // 2) + N * (K // G) * 2
+    copies = max(2, -(-ROTATE_BYTES // copy_bytes) + 1)
+    W, S = make_weights(torch, copies, N, K, gen)
+    x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
+    xf = torch.empty(16 * K, dtype=torch.int8, device="cuda")
+    xs = torch.empty(16 * (K // G), dtype=torch.float32, device="cuda")
+    ones = torch.ones(K, dtype=torch.bfloat16, device="cuda")
+    st0 = torch.cuda.current_stream().cuda_stream
+    if L.viper_hip_rmsnorm_quantize_frag(x.data_ptr(), ones.data_ptr(), 1e-6, M, K, G, None, xf.data_ptr(),
+                                         xs.data_ptr(), st0) != 0:
+        raise RuntimeError("rmsnorm_quantize_frag failed")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    stamps = torch.zeros(1 << 20, dtype=torch.int64, device="cuda")
+    grid, waves = C.c_int(0), C.c_int(0)
+
+    def launch(i):
+        c = i % copies
+        st = torch.cuda.current_stream().cuda_stream
+        rc = L.viper_hip_qlinear_frag_timeline(4, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K, xf.data_ptr(),
+                                               xs.data_ptr(), M, y.data_ptr(), stamps.data_ptr(), stamps.numel() * 8,
+                                               C.byref(grid), C.byref(waves), st)
+        if rc != 0:
+            raise RuntimeError(f"frag timeline failed: {rc}")
+    for i in range(50):
+        launch(i)
+    g = capture_n(torch, launch, 400)
+    us = time_graph(torch, g, 1) * 1e3 / 400
+    g.replay()
+    torch.cuda.synchronize()
+    nw = grid.value * waves.value
+    t = stamps[: nw * 8].view(nw, 8).cpu().numpy()
+    t = (t - t[:, 0].min()) * 0.01       # 100 MHz ticks -> us
+    names = ["wave start", "activation + scale loads issued", "weight loads issued", "staged scales in LDS",
+             "first group scaled", "last group scaled", "cross-wave barrier passed", "outputs stored"]
+    import numpy as np
+    rows = {}
+    for i, nm in enumerate(names):
+        v = np.sort(t[:, i])
+        rows[nm] = [round(float(np.percentile(v, p)), 3) for p in (10, 50, 90)] + [round(float(v[-1]), 3)]
+    print(json.dumps({"timeline": f"qgemm_rc Q4_G64 M={M} K={K} N={N} (fragment input)", "workgroups": grid.value,
+                      "waves_per_workgroup": waves.value, "us_per_launch_stamped": round(us, 3),
+                      "percentiles_us_p10_p50_p90_max": rows}), flush=True)
+
+
 def time_config3(torch, stk, fused, replays=10, prefetch=0):
     """us per config-3 decode step (one graph of the whole step, replayed), its weight + head GB/s,
     and the launches per step (prefetch > 0: the fused step with the next slot's weights warmed from a
@@ -475,14 +525,17 @@ def main():
     ap.add_argument("--timeline", nargs="?", const="q4", default=None, choices=("q4", "q5", "q6", "w8"),
                     help="only the per-wave timeline of the M=1 GEMV at the north-star shape, Q4_G64 unless a "
                          "format is named (viper_hip_qlinear_timeline)")
+    ap.add_argument("--timeline-rc", type=int, default=0, metavar="M",
+                    help="only the per-wave timeline of the M-row matrix-core GEMM (Q4_G64, fragment input) at "
+                         "the north-star shape (viper_hip_qlinear_frag_timeline)")
     ap.add_argument("--shape", type=int, nargs=2, default=None, metavar=("K", "N"),
-                    help="with --timeline: another shape than the north star's (one with an exact tiling)")
+                    help="with --timeline / --timeline-rc: another shape than the north star's")
     ap.add_argument("--only", default="", metavar="LINE",
                     help="only one line (rocprofv3 runs): config0[_pre], down, verify_mM (K=2560 N=10240) or "
                          "verify_mM_down (K=10240 N=2560), pre_mM[_down] (the same through the prequantized "
                          "entry, x quantized once outside the timed calls), frag_mM[_down] (the same from "
                          "fragment-order rows), q5_m1 / q6_m8 / w8_m1 ... "
-                         "(config 4), FMT_kK_nN_mM (any shape, e.g. q4_k3072_n6144_m1), config1 / "
+                         "(config 4), FMT_kK_nN_mM[_pre|_frag] (any shape, e.g. q4_k3072_n6144_m1), config1 / "
                          "config1_2launch (MLP), config3 (fused step), config3_prefetchW (the fused step with the next slot's "
                          "weights warmed from a second stream by W workgroups) or config3_ref (reference launch "
                          "sequence)")
@@ -538,11 +591,11 @@ def main():
             shape = (2560, 10240) if one.endswith("_down") else (10240, 2560)
             res = time_linear(torch, L, gen, qtype, shape[0], shape[1], Mv, steps=args.steps,
                               prequantized=one.startswith("pre_m"), frag=one.startswith("frag_m"))
-        elif re.fullmatch(r"(q4|q5|q6|w8)_k\d+_n\d+_m\d+", one):
-            fmt, kk, nn, mm = one.split("_")
+        elif re.fullmatch(r"(q4|q5|q6|w8)_k\d+_n\d+_m\d+(_pre|_frag)?", one):
+            fmt, kk, nn, mm = one.split("_")[:4]
             qt = {"q4": 4, "q5": 5, "q6": 6, "w8": 8}[fmt]
             res = time_linear(torch, L, gen, qt, int(nn[1:]), int(kk[1:]), int(mm[1:]), steps=args.steps,
-                              outliers=qt != 4)
+                              outliers=qt != 4, prequantized=one.endswith("_pre"), frag=one.endswith("_frag"))
         elif one[:1] in "qw" and "_m" in one:
             fmt, mpart = one.split("_m")
             qt = {"q5": 5, "q6": 6, "w8": 8}[fmt]
@@ -563,6 +616,10 @@ def main():
         return
     if args.read_sweep:
         read_sweep(torch, L, gen)
+        return
+    if args.timeline_rc:
+        Kt, Nt = (args.shape[0], args.shape[1]) if args.shape else (K, N)
+        timeline_rc(torch, L, gen, Nt, Kt, args.timeline_rc)
         return
     if args.timeline:
         Kt, Nt = (args.shape[0], args.shape[1]) if args.shape else (K, N)

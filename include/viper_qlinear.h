@@ -57,6 +57,8 @@
  *                                   the exact per-group int32 dots for parity tests.
  *   viper_hip_qlinear_timeline      no counterpart: the M = 1 GEMV with per-wave
  *                                   timestamps (measurement).
+ *   viper_hip_qlinear_frag_timeline no counterpart: the M = 2..16 matrix-core GEMM
+ *                                   with per-wave timestamps (measurement).
  *   viper_hip_check_bf16_rounding   no counterpart: device self-check of the
  *                                   bf16 output rounding.
  *   viper_hip_check_quantizer       no counterpart: device self-check of the
@@ -326,6 +328,20 @@ int viper_hip_qlinear_timeline(int qtype, const void* w_packed, const void* w_sc
  * if the folded data equals a fixed word. */
 int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads, const void* side, int side_bytes,
                           void* y_bf16, uint32_t* sink, void* stream);
+
+/* Measurement entry point, no counterpart in the reference: the M = 2..16
+ * matrix-core GEMM of viper_hip_qlinear_prequantized_frag (Q4_G64, K a
+ * multiple of 4 groups and at most 20 quads of 4 groups: one segment) with a
+ * per-wave timeline.  Lane 0 of every wave writes 8 s_memrealtime readings
+ * (uint64, 100 MHz) to stamps[(workgroup * waves + wave) * 8 + i]: wave
+ * start, activation and scale loads issued, weight loads issued, staged
+ * scales in LDS, first group scaled, last group scaled, cross-wave barrier
+ * passed, outputs stored.  *workgroups and *waves_per_workgroup (may be NULL)
+ * receive the grid; stamp_bytes must cover it. */
+int viper_hip_qlinear_frag_timeline(int qtype, const void* w_packed, const void* w_scales, int scale_enc, int group,
+                                    int N, int K, const void* xfrag, const void* xsfrag, int M, void* y_bf16,
+                                    uint64_t* stamps, size_t stamp_bytes, int* workgroups, int* waves_per_workgroup,
+                                    void* stream);
 
 /* Warms `bytes` (a multiple of 16, 16-byte aligned) at buf into the GPU's
  * memory-side cache with plain loads, split over `workgroups` workgroups of

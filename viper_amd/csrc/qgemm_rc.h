@@ -136,7 +136,14 @@ struct RcSeg {
 // A part counts as soon as its slot stores are issued; the last part
 // requests every slot at once, then re-reads any that does not yet carry
 // the current tag.
-template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, int SK = 1, bool PR = true>
+// TLM (measurement, fragment input, one segment, no split): `part` receives
+// per-wave s_memrealtime readings (100 MHz) at RC_TL_STAMPS points --
+// [workgroup][wave][RC_TL_STAMPS] uint64: wave start, activation and scale
+// loads issued, weight loads issued, staged scales in LDS, first group
+// scaled, last group scaled, cross-wave barrier passed, outputs stored.
+constexpr int RC_TL_STAMPS = 8;
+template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, int SK = 1, bool PR = true,
+          bool TLM = false>
 __global__ void __launch_bounds__(64 * W)
 qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
                 unsigned nm, const uint16_t* res, int32_t* __restrict__ part,
@@ -147,6 +154,12 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     constexpr int T = Seg::T;
     constexpr bool XNAT = AM == RC_NAT, XBF = AM == RC_BF16;
     static_assert(SK == 1 || AM == RC_FRAG, "the K split reads fragments");
+    static_assert(!TLM || (ONE && !PART && SK == 1 && AM == RC_FRAG), "timeline: one fragment-input segment");
+    uint64_t tstamp[RC_TL_STAMPS];
+    auto stamp = [&](int i) {
+        if constexpr (TLM) tstamp[i] = __builtin_amdgcn_s_memrealtime();
+    };
+    stamp(0);
     constexpr int G = F == 8 ? 32 : 64;
     extern __shared__ __align__(16) uint8_t smem[];
     // the wave index as a scalar: per-quad conditions are then uniform branches
@@ -274,6 +287,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                 for (int t = 0; t < T; ++t) S.S[j][t] = bload8(srj, ((16 * t + n16) * NG + 4 * Q) * 2);
         }
         issue_fence();
+        if (seg == 0) stamp(1);
 #pragma unroll
         for (int j = 0; j < QW; ++j) {
             const int Q = wave + W * (seg * QW + j);
@@ -412,6 +426,8 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                                              __uint_as_float(S.XS[j][h].z), __uint_as_float(S.XS[j][h].w)};
 #pragma unroll
                         for (int r = 0; r < 4; ++r) acc[t][r] = __builtin_fmaf(wsf * xf[r], (float)C[r], acc[t][r]);
+                        if constexpr (TLM)
+                            if (j == 0 && t == 0 && h == 0) stamp(4);
                         if constexpr (PART) {
                             if (16 * t + n16 < nrows) {
 #pragma unroll
@@ -466,6 +482,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     if constexpr (ONE) {
         Seg S;
         load(S, 0);
+        stamp(2);
         if constexpr (STG) {
             issue_fence();  // the weight requests stay ahead of the staging stores
 #pragma unroll
@@ -489,7 +506,9 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                 }
             }
         }
+        stamp(3);
         compute(S, 0);
+        stamp(5);
     } else {
         Seg S0, S1;
         load(S0, 0);
@@ -510,6 +529,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
 #pragma unroll
         for (int r = 0; r < 4; ++r) red[((wave * T + t) * 4 + r) * 64 + L] = acc[t][r];
     __syncthreads();
+    stamp(6);
     constexpr int MINE = (4 * T + W - 1) / W;
     float mine[MINE] = {};
     const int kpart = SK > 1 ? (int)(blockIdx.x % SK) : 0;
@@ -537,6 +557,14 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                 if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
                 y[o] = f2bf(v);
             }
+        }
+    }
+    if constexpr (TLM) {
+        stamp(7);
+        if (L == 0) {
+            uint64_t* o = (uint64_t*)part + ((size_t)blockIdx.x * W + wave) * RC_TL_STAMPS;
+#pragma unroll
+            for (int i = 0; i < RC_TL_STAMPS; ++i) o[i] = tstamp[i];
         }
     }
     if constexpr (SK > 1) {
@@ -666,6 +694,34 @@ rc_fn rc_pick2(const RcShape& s, int am, bool part, int senc, bool pair) {
         default: return nullptr;
     }
 }
+
+// Timeline kernels (fragment input, one segment; Q4 only, qgemm_rc_q4.hip).
+template <int F, int RB>
+rc_fn rc_pick_tl3(const RcShape& s, int senc) {
+#define VQ_RC_TL(W_, QW_)                                                                              \
+    if (s.w == W_ && s.qw == QW_)                                                                      \
+        return senc ? qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 1, 1, false, true>         \
+                    : qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 0, 1, false, true>;
+    VQ_RC_TL(4, 1)
+    VQ_RC_TL(10, 1)
+    if constexpr (RB <= rc_rb_qw2(F)) VQ_RC_TL(10, 2)
+#undef VQ_RC_TL
+    return nullptr;
+}
+template <int F>
+rc_fn rc_pick_tl(const RcShape& s, int senc) {
+    if (!s.one || s.sk != 1) return nullptr;
+    switch (s.rb) {
+        case 1: return rc_pick_tl3<F, 1>(s, senc);
+        case 2: return rc_pick_tl3<F, 2>(s, senc);
+        case 3: return rc_pick_tl3<F, 3>(s, senc);
+        case 4: return rc_pick_tl3<F, 4>(s, senc);
+        case 5: return rc_pick_tl3<F, 5>(s, senc);
+        case 6: return rc_pick_tl3<F, 6>(s, senc);
+        default: return nullptr;
+    }
+}
+rc_fn rc_pick_tl4(const RcShape& s, int senc);
 
 // Kernels of format F (each defined in its own translation unit).
 template <int F>

@@ -134,4 +134,36 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     return status_of(hipGetLastError());
 }
 
+// The timeline variant of launch_rc (Q4, fragment input, one segment): see
+// viper_hip_qlinear_frag_timeline.
+int launch_rc_timeline(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
+                       const void* xs, int M, void* y, uint64_t* stamps, size_t stamp_bytes, int* workgroups,
+                       int* waves, hipStream_t st) {
+    if (qtype != VIPER_QTYPE_Q4_G64 || !rc_ok(qtype, K) || M < 2 || M > 16 || N >= (1 << 27)) return VIPER_INVALID_ARGUMENT;
+    const RcShape sh = rc_launch_shape(qtype, N, K);
+    const rc_fn fn = rc_pick_tl4(sh, senc);
+    if (fn == nullptr) return VIPER_INVALID_ARGUMENT;
+    const int nb0 = (N + 8 * sh.rb - 1) / (8 * sh.rb);
+    if (stamps == nullptr || stamp_bytes < (size_t)nb0 * sh.w * RC_TL_STAMPS * sizeof(uint64_t)) return VIPER_INVALID_ARGUMENT;
+    if (workgroups != nullptr) *workgroups = nb0;
+    if (waves != nullptr) *waves = sh.w;
+    const size_t lds = rc_launch_lds(qtype, sh, K, RC_FRAG);
+    const int8_t* a0 = (const int8_t*)xq;
+    const float* a1 = (const float*)xs;
+    const uint8_t* a2 = (const uint8_t*)w;
+    const uint16_t* a3 = (const uint16_t*)s;
+    uint16_t* a4 = (uint16_t*)y;
+    const uint16_t* a5 = nullptr;
+    int32_t* part = (int32_t*)stamps;
+    const uint8_t* b0 = nullptr;
+    const uint16_t* b1 = nullptr;
+    uint16_t* b2 = nullptr;
+    uint64_t* sp = nullptr;
+    unsigned* sc = nullptr;
+    unsigned nm = (unsigned)N | ((unsigned)(M - 1) << 27) | (senc ? 1u << 31 : 0u);
+    void* args[] = {&a0, &a1, &a2, &a3, &a4, &K, &nm, &a5, &part, &b0, &b1, &b2, &sp, &sc};
+    launch((const void*)fn, (unsigned)nb0, (unsigned)(64 * sh.w), lds, st, args);
+    return status_of(hipGetLastError());
+}
+
 }  // namespace vq

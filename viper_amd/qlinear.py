@@ -141,6 +141,7 @@ _SYMBOLS = (
     "viper_hip_swiglu_quantize_frag",
     "viper_hip_qlinear_prequantized_frag",
     "viper_hip_qlinear_fused2_prequantized_frag",
+    "viper_hip_qlinear_frag_timeline",
 )
 
 
@@ -192,6 +193,9 @@ def lib():
     L.viper_hip_qlinear_fused2_prequantized_frag.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, i32,
                                                              vp, vp, vp]
     L.viper_hip_qlinear_fused2_prequantized_frag.restype = i32
+    L.viper_hip_qlinear_frag_timeline.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, sz, vp, vp,
+                                                  vp]
+    L.viper_hip_qlinear_frag_timeline.restype = i32
     L.viper_hip_qlinear_fused2.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     L.viper_hip_qlinear_fused2.restype = i32
     L.viper_hip_qlinear_fused2_prequantized.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, i32,
