@@ -18,7 +18,8 @@ dispatch duration (us_per_gemv).  Every other line is timed over one graph of
 (same semantics, seeded inputs), timed on this host with 1 and all threads.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
-       python bench.py --read-sweep | --timeline [q4|q5|q6|w8] | --only LINE   (measurement modes)
+       python bench.py --read-sweep | --dispatch-floor | --clock-period | --timeline [q4|q5|q6|w8]
+                       | --timeline-rc M | --only LINE   (measurement modes)
 """
 import argparse
 import ctypes as C
@@ -67,7 +68,8 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False, prequa
     prequantized: x quantized once (viper_hip_quantize_act) outside the timed calls, each call
     viper_hip_qlinear_prequantized (int8 rows and their fp32 group scales in, bf16 y out);
     frag: the same with the rows in the matrix-core fragment order (viper_hip_rmsnorm_quantize_frag of
-    x with gamma = 1 outside the timed calls, each call viper_hip_qlinear_prequantized_frag)."""
+    x with gamma = 1 outside the timed calls, each call viper_hip_qlinear_prequantized_frag with a
+    workspace of viper_hip_qlinear_frag_workspace_bytes, so long K splits over workgroups)."""
     G = GROUP[qtype]
     rb = ROW_BYTES[qtype](K)
     copy_bytes = N * rb + N * (K // G) * 2
@@ -79,7 +81,8 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False, prequa
         xf[:, ch] *= 20.0
     x = xf.to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    nws = L.viper_hip_qlinear_workspace_bytes(qtype, N, K, M)
+    nws = L.viper_hip_qlinear_frag_workspace_bytes(qtype, N, K, M) if frag else \
+        L.viper_hip_qlinear_workspace_bytes(qtype, N, K, M)
     ws = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda")   # zero before first use
     if prequantized:
         xq = torch.empty(M * K, dtype=torch.int8, device="cuda")
@@ -100,7 +103,8 @@ def time_linear(torch, L, gen, qtype, N, K, M, steps=400, outliers=False, prequa
         st = torch.cuda.current_stream().cuda_stream
         if frag:
             rc = L.viper_hip_qlinear_prequantized_frag(qtype, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K,
-                                                       xq.data_ptr(), xs.data_ptr(), M, y.data_ptr(), None, st)
+                                                       xq.data_ptr(), xs.data_ptr(), M, y.data_ptr(), None,
+                                                       ws.data_ptr() if nws else None, nws, st)
         elif prequantized:
             rc = L.viper_hip_qlinear_prequantized(qtype, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K,
                                                   xq.data_ptr(), xs.data_ptr(), M, y.data_ptr(), None, st)
@@ -281,6 +285,26 @@ def _time_probe(torch, L, pool, nbytes, threads, loads, y=None, launches=200, si
     us = time_graph(torch, g, 1) * 1e3 / n
     del g
     return us
+
+
+def dispatch_floor(torch, L, launches=400):
+    """us per launch of viper_hip_empty_dispatch, back to back in one HIP graph (time_steps): one
+    64-thread workgroup; the north-star GEMV's grid (512 x 320) without stores; the same grid storing one
+    bf16 per 16-lane team (10240 rows, the GEMV's output pattern); and the 16-row GEMM's grid
+    (256 x 640)."""
+    y = torch.zeros(65536, dtype=torch.bfloat16, device="cuda")
+    for nm, wg, nt, store in (("one_workgroup", 1, 64, False), ("gemv_grid", 512, 320, False),
+                              ("gemv_grid_row_stores", 512, 320, True), ("gemm16_grid", 256, 640, False)):
+        def launch(i, wg=wg, nt=nt, store=store):
+            rc = L.viper_hip_empty_dispatch(wg, nt, y.data_ptr() if store else None,
+                                            torch.cuda.current_stream().cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"viper_hip_empty_dispatch failed: {rc}")
+        for i in range(50):
+            launch(i)
+        us = min(time_steps(torch, launch, launches) for _ in range(3))
+        print(json.dumps({"dispatch": nm, "workgroups": wg, "threads": nt, "row_stores": store,
+                          "us_per_launch": round(us, 3)}), flush=True)
 
 
 def read_sweep(torch, L, gen):
@@ -546,6 +570,10 @@ def main():
     ap.add_argument("--trace-summary", default="", metavar="CSV",
                     help="only summarise a rocprofv3 kernel-trace CSV of this bench run with the same --steps "
                          "and --warmup (no GPU needed)")
+    ap.add_argument("--dispatch-floor", action="store_true",
+                    help="only the fixed cost of a dispatch: back-to-back launches of a kernel that reads nothing "
+                         "(viper_hip_empty_dispatch) on one workgroup and on the north-star GEMV's grid, with and "
+                         "without its row stores (JSON lines)")
     ap.add_argument("--verify-only", type=int, default=0, metavar="M",
                     help="only time the M-row verify (K=2560, N=10240) line (rocprofv3 runs)")
     args = ap.parse_args()
@@ -616,6 +644,9 @@ def main():
         return
     if args.read_sweep:
         read_sweep(torch, L, gen)
+        return
+    if args.dispatch_floor:
+        dispatch_floor(torch, L)
         return
     if args.timeline_rc:
         Kt, Nt = (args.shape[0], args.shape[1]) if args.shape else (K, N)

@@ -69,6 +69,8 @@
  *                                   streaming dispatch).
  *   viper_hip_clock_stamp           no counterpart: a device-clock reading between
  *                                   launches (measurement).
+ *   viper_hip_empty_dispatch        no counterpart: a launch that reads nothing
+ *                                   (measurement: the fixed cost of a dispatch).
  *   viper_hip_prefetch              no counterpart: warms a weight range into the
  *                                   memory-side cache from a second stream.
  *
@@ -121,11 +123,14 @@ extern "C" {
 #define VIPER_SCALE_BF16 1
 
 #define VIPER_QLINEAR_MAX_M 16
-/* 6: the M > 1 workspace is zero-filled before its first use and keeps the
- *    K split's control words at offset 0 (5 needed no initialisation);
- *    viper_hip_qlinear_workspace_layout.
+/* 7: the K split keeps its own per-block counters (no launch before it), so
+ *    the fragment-input entry points take an optional workspace;
+ *    viper_hip_qlinear_frag_workspace_bytes; the workspace layout's offsets
+ *    changed (viper_hip_qlinear_workspace_layout).
+ * 6: the M > 1 workspace is zero-filled before its first use and keeps the
+ *    K split's control words at offset 0 (5 needed no initialisation).
  * 5: weight scales must be 16-byte aligned (4 accepted 2-byte aligned scales) */
-#define VIPER_QLINEAR_ABI_VERSION 6
+#define VIPER_QLINEAR_ABI_VERSION 7
 
 int viper_hip_abi_version(void);
 
@@ -133,26 +138,30 @@ int viper_hip_abi_version(void);
 int viper_hip_group_size(int qtype);
 
 /* Bytes of caller workspace viper_hip_qlinear needs for this shape; 0 when
- * the activation quantize is fused into the GEMV (M == 1).  It holds the
- * int8 activations and their scales, and for long K on the matrix cores
- * (K of more than 20 quads of 4 groups) the K split's control words, block
- * counters and fp32 part sums.  A workspace is zero-filled before its first
- * use (hipMemset, torch.zeros); after that it serves any sequence of shapes
- * that fit it with no clearing (each call leaves it valid for the next), as
- * long as nothing else writes it.  Calls that use one workspace
- * concurrently race. */
+ * the activation quantize is fused into the GEMV (M == 1).  It holds the K
+ * split's control words and block counters (the first 4352 bytes, for every
+ * shape), for long K on the matrix cores (K of more than 20 quads of 4
+ * groups) the K split's fp32 part sums, then the int8 activations and their
+ * scales.  A workspace is zero-filled before its
+ * first use (hipMemset, torch.zeros); after that it serves any sequence of
+ * shapes and entry points that fit it with no clearing (each call leaves it
+ * valid for the next), as long as nothing else writes it.  Calls that use
+ * one workspace concurrently race. */
 size_t viper_hip_qlinear_workspace_bytes(int qtype, int N, int K, int M);
 
 /* The workspace's layout for this shape (no counterpart in the reference;
  * tests and debugging).  Returns viper_hip_qlinear_workspace_bytes() and,
- * when offsets is not NULL, writes six byte offsets into the workspace
- * (SIZE_MAX where the shape has no such part):
- *   [0] the K split's generation word (uint32; 0 for every shape),
- *   [1] the count of K-split sums that did not arrive within the kernel's
- *       bounded wait (uint32 at 4 for every shape; such outputs are NaN;
- *       the library never clears it, so a caller can check it stayed 0),
- *   [2] the K split's block counters (from byte 256), [3] xq, [4] xs,
- *       [5] the K split's part sums (64-bit slots). */
+ * when offsets is not NULL, writes six values (SIZE_MAX where the shape has
+ * no such part):
+ *   [0] the count of K-split sums that did not arrive within the kernel's
+ *       bounded wait (uint32 at byte 4 for every shape; such outputs are
+ *       NaN; the library never clears it, so a caller can check it stayed 0),
+ *   [1] the K split's block counters (1024 uint32 from byte 256, for every
+ *       shape: 64 * epoch + parts counted, a multiple of 64 between calls),
+ *   [2] the K split's part sums (from byte 4352 for every shape: one record
+ *       of 8 * 16 * 48 64-bit slots per row block),
+ *   [3] xq, [4] xs,
+ *   [5] the K split's row blocks (a count, not an offset; 0 without it). */
 size_t viper_hip_qlinear_workspace_layout(int qtype, int N, int K, int M, size_t* offsets);
 
 /* y[M][N] = linear(w, x) with x[M][K] bf16 quantized per row and group.
@@ -377,10 +386,19 @@ int viper_hip_swiglu_quantize_frag(const void* gate_bf16, const void* up_bf16, i
 /* linear_q4_dp4a_prequantized{,_residual} (kernels/ops/linear_multim.h:30-41)
  * and dp4a_smem_gemv_fused2 (kernels/ops/dp4a_smem_kernel.cu:141-152) at
  * M = 2..16 over activations in the fragment order above: one launch of the
- * matrix-core kernel, no workspace.  K must be a multiple of 4 groups. */
+ * matrix-core kernel.  K must be a multiple of 4 groups.  workspace (16-byte
+ * aligned, may be NULL): with viper_hip_qlinear_frag_workspace_bytes() bytes
+ * or more, long K is split over workgroups (the reference's hidden static
+ * buffer, kernels/ops/linear_multim.cu:133-146, in the caller's hands); with
+ * NULL, or for shapes that need none, each workgroup loops over all of K.
+ * Same workspace rules as viper_hip_qlinear's (zero-filled before its first
+ * use, then reused by any entry point without clearing; concurrent calls on
+ * one workspace race).  The fused pair takes no workspace. */
+size_t viper_hip_qlinear_frag_workspace_bytes(int qtype, int N, int K, int M);
 int viper_hip_qlinear_prequantized_frag(int qtype, const void* w_packed, const void* w_scales, int scale_enc,
                                         int group, int N, int K, const void* xfrag, const void* xsfrag, int M,
-                                        void* y_bf16, const void* residual_bf16, void* stream);
+                                        void* y_bf16, const void* residual_bf16, void* workspace,
+                                        size_t workspace_bytes, void* stream);
 int viper_hip_qlinear_fused2_prequantized_frag(int qtype, const void* w0_packed, const void* w0_scales,
                                                const void* w1_packed, const void* w1_scales, int scale_enc,
                                                int group, int N, int K, const void* xfrag, const void* xsfrag,
@@ -391,6 +409,14 @@ int viper_hip_qlinear_fused2_prequantized_frag(int qtype, const void* w0_packed,
  * out[0] (uint64, 8-byte aligned).  Two of them around a sequence of
  * launches on one stream time the sequence on the device's clock. */
 int viper_hip_clock_stamp(uint64_t* out, void* stream);
+
+/* Measurement probe, no counterpart in the reference: one launch of
+ * `workgroups` x `threads` (a multiple of 64, at most 1024) that reads
+ * nothing.  With y_bf16 (2-byte aligned, workgroups * threads / 16 entries)
+ * lane 0 of every 16-lane team stores one bf16 to y_bf16[row], the M = 1
+ * GEMV's output pattern; with NULL nothing is stored.  Back-to-back launches
+ * time the fixed cost of a dispatch. */
+int viper_hip_empty_dispatch(int workgroups, int threads, void* y_bf16, void* stream);
 
 #ifdef __cplusplus
 }

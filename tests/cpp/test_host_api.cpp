@@ -81,7 +81,7 @@ int main() {
     Tensor y4(fake, DType::BF16, {4, 64});
     EXPECT(code(w, x4, y4) == StatusCode::INVALID_ARGUMENT);  // no workspace
     EXPECT(ops::linear_workspace_bytes(w, 1) == 0);
-    EXPECT(ops::linear_workspace_bytes(w, 4) == 16 + 16 * 128 + 2 * 16 * 4);  // control words, xq, xs for 16 rows
+    EXPECT(ops::linear_workspace_bytes(w, 4) == 256 + 4 * 1024 + 16 * 128 + 2 * 16 * 4);  // control words and counters, xq, xs for 16 rows
     Tensor misaligned(reinterpret_cast<void*>(0x10008), DType::BF16, {128});
     EXPECT(code(w, misaligned, y) == StatusCode::INVALID_ARGUMENT);
     // lossy dtypes through the Tensor overload: UNIMPLEMENTED, as the

@@ -28,65 +28,79 @@ def test_header_symbols_exported():
     for n in names:
         assert hasattr(L, n), n
     assert set(names) == set(ql._SYMBOLS)
-    assert L.viper_hip_abi_version() == 6
+    assert L.viper_hip_abi_version() == 7
 
 
 def test_group_sizes_and_workspace():
     L = va.lib()
     assert [L.viper_hip_group_size(q) for q in (4, 5, 6, 8, 0, 1, 7)] == [64, 64, 64, 32, 0, 0, 0]
     assert va.workspace_bytes(4, 10240, 2560, 1) == 0
-    # 16 bytes of control words, int8 activations with room for 16 rows, then
-    # fp32 scales for 16 rows per group
-    assert va.workspace_bytes(4, 10240, 2560, 4) == 16 + 16 * 2560 + 40 * 16 * 4
-    assert va.workspace_bytes(8, 10, 2560, 3) == 16 + 16 * 2560 + 80 * 16 * 4
-    assert va.workspace_bytes(6, 10, 2496, 3) == 16 + 16 * 2496 + 39 * 16 * 4
-    # long K (the K split in 4 parts): also one counter per 8 rows (16-byte
-    # aligned, from byte 256: a cache line apart from the control words) and
-    # the part sums [4][M][N] as 64-bit {tag, fp32} slots
-    assert va.workspace_bytes(4, 2560, 10240, 16) == 256 + 1280 + 16 * 10240 + 160 * 16 * 4 + 4 * 16 * 2560 * 8
-    assert va.workspace_bytes(8, 2560, 10240, 3) == 256 + 1280 + 16 * 10240 + 320 * 16 * 4 + 4 * 3 * 2560 * 8
-    assert va.workspace_bytes(4, 2560, 5120, 16) == 16 + 16 * 5120 + 80 * 16 * 4   # one segment: no split
+    # the K split's control words and 1024 block counters (4352 bytes, for
+    # every M > 1 shape), int8 activations with room for 16 rows, then fp32
+    # scales for 16 rows per group
+    CTL = 256 + 4 * 1024
+    assert va.workspace_bytes(4, 10240, 2560, 4) == CTL + 16 * 2560 + 40 * 16 * 4
+    assert va.workspace_bytes(8, 10, 2560, 3) == CTL + 16 * 2560 + 80 * 16 * 4
+    assert va.workspace_bytes(6, 10, 2496, 3) == CTL + 16 * 2496 + 39 * 16 * 4
+    # long K (the K split): one record of 8 parts x 16 rows x 48 64-bit slots
+    # per row block (down shape: 107 blocks of 24 rows), before xq and xs
+    REC = 8 * 16 * 48 * 8
+    assert va.workspace_bytes(4, 2560, 10240, 16) == CTL + 107 * REC + 16 * 10240 + 160 * 16 * 4
+    nb8 = va.workspace_layout(8, 2560, 10240, 3)["split_blocks"]     # W8: 80 quads, 8 parts of 10
+    assert 0 < nb8 <= 107
+    assert va.workspace_bytes(8, 2560, 10240, 3) == CTL + nb8 * REC + 16 * 10240 + 320 * 16 * 4
+    assert va.workspace_bytes(4, 2560, 5120, 16) == CTL + 16 * 5120 + 80 * 16 * 4   # one segment: no split
+    # the fragment-input entry: control words and records only, 0 without a split
+    assert va.frag_workspace_bytes(4, 2560, 10240, 16) == CTL + 107 * REC
+    assert va.frag_workspace_bytes(4, 10240, 2560, 16) == 0
+    assert va.frag_workspace_bytes(4, 2560, 10240, 1) == 0
+    # K = 10752 (42 quads: 6 parts of 7), K = 6144 (24 quads: 3 parts of 8)
+    assert va.workspace_layout(4, 3072, 10752, 16)["split_blocks"] > 0
+    assert va.workspace_layout(4, 3072, 6144, 16)["split_blocks"] > 0
 
 
 def _split_shapes():
     for qtype in (4, 5, 6, 8):
-        for K in (6144, 10240, 12288, 20480):
+        for K in (6144, 10240, 10752, 12288, 20480):
             for M in (5, 6, 9, 12, 16):
-                for N in (64, 640, 1000, 2048, 2560, 10240):
+                for N in (64, 640, 1000, 2048, 2560, 3072, 10240):
                     yield qtype, N, K, M
 
 
-def test_split_control_words_fixed_for_every_shape():
-    # The K split's generation word sits at offset 0 whatever the shape, so
-    # every call on one workspace draws a new generation; no other part of
-    # any shape's layout covers the 16 bytes of control words, and the parts
-    # of one shape do not overlap.
+def test_split_layout_fixed_for_every_shape():
+    # The K split's counters and records of part sums sit at the same offsets
+    # for every shape (a record is written only by its own row block, whose
+    # counter carries the epoch the record's tags are made from), the missed-sum
+    # count at 4; xq and xs follow the records and nothing overlaps.
+    CTL, REC = 256 + 4 * 1024, 8 * 16 * 48 * 8
     seen = 0
     for qtype, N, K, M in _split_shapes():
         lay = va.workspace_layout(qtype, N, K, M)
+        assert lay["missed"] == 4 and lay["counters"] == 256, (qtype, N, K, M)
+        nb = lay["split_blocks"]
         if lay["sums"] is None:
+            assert nb == 0 and lay["xq"] == CTL
             continue
         seen += 1
-        assert lay["generation"] == 0 and lay["missed"] == 4, (qtype, N, K, M)
-        assert lay["counters"] == 256
-        n_blocks = (N + 7) // 8
-        assert lay["counters"] + 4 * n_blocks <= lay["xq"]
-        assert lay["xq"] % 16 == 0 and lay["xs"] % 16 == 0 and lay["sums"] % 16 == 0
+        assert 0 < nb <= 1024 and lay["sums"] == CTL
+        assert nb * 48 >= N and (nb - 1) * 8 < N                 # blocks of 8..48 rows cover N
+        assert lay["xq"] == CTL + nb * REC
+        assert lay["xq"] % 16 == 0 and lay["xs"] % 16 == 0
         assert lay["xq"] + 16 * K <= lay["xs"]
         G = 32 if qtype == 8 else 64
-        assert lay["xs"] + (K // G) * 16 * 4 <= lay["sums"]
-        assert lay["sums"] + 4 * M * N * 8 == lay["total"] == va.workspace_bytes(qtype, N, K, M)
+        assert lay["xs"] + (K // G) * 16 * 4 == lay["total"] == va.workspace_bytes(qtype, N, K, M)
+        assert va.frag_workspace_bytes(qtype, N, K, M) == CTL + nb * REC
     assert seen > 300
-    # shapes without the split keep the control words too (xq at 16)
     lay = va.workspace_layout(4, 10240, 2560, 8)
-    assert lay["xq"] == 16 and lay["sums"] is None and lay["counters"] is None
+    assert lay["sums"] is None and lay["split_blocks"] == 0 and lay["counters"] == 256
     assert va.workspace_layout(4, 10240, 2560, 1)["total"] == 0
 
 
 def test_split_tag_cannot_match_library_words():
     # A slot is accepted when its high word equals the call's tag, whose top
-    # byte is 0x80.  The other words the library stores in a workspace are
-    # int8 activations, fp32 activation scales and counters (at most 4): the
+    # byte is 0x80.  The other words the library stores where slots can lie
+    # are int8 activations and fp32 activation scales (the counters have a
+    # region of their own): the
     # quantizer's bytes never include 0x80 (|q| <= 127, also for groups
     # holding the largest finite bf16 values, and the device quantizer equals
     # the oracle's on every finite bf16 pair, test_device_quantizer_exhaustive)
@@ -154,6 +168,10 @@ def test_other_entry_validation():
     assert L.viper_hip_sampling_greedy_split(FAKE, FAKE, 2, 4096, FAKE + 4, 32, None) == 2    # not 8-byte aligned
     assert L.viper_hip_sampling_greedy_split(FAKE, FAKE, 0, 4096, FAKE, 32, None) == 2
     assert L.viper_hip_sampling_greedy_split(FAKE + 1, FAKE, 2, 4096, FAKE, 32, None) == 2    # logits not bf16-aligned
+    assert L.viper_hip_empty_dispatch(0, 64, None, None) == 2
+    assert L.viper_hip_empty_dispatch(1, 65, None, None) == 2                                 # not whole waves
+    assert L.viper_hip_empty_dispatch(1, 1088, None, None) == 2
+    assert L.viper_hip_empty_dispatch(1, 64, FAKE + 1, None) == 2                             # y not 2-byte aligned
     W = 320 * 5 * 16                                                      # one workgroup's bytes
     assert L.viper_hip_stream_read(None, W, 320, 5, None, 0, None, FAKE, None) == 2
     assert L.viper_hip_stream_read(FAKE, 0, 320, 5, None, 0, None, FAKE, None) == 2

@@ -31,5 +31,5 @@ def test_world_size_above_one_exits_with_a_message():
 def test_help_lists_the_modes():
     r = run_bench("--help")
     assert r.returncode == 0
-    for flag in ("--steps", "--warmup", "--only", "--read-sweep", "--timeline", "--no-cpu", "--no-extras"):
+    for flag in ("--steps", "--warmup", "--only", "--read-sweep", "--dispatch-floor", "--timeline", "--no-cpu", "--no-extras"):
         assert flag in r.stdout

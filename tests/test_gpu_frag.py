@@ -8,7 +8,10 @@ Bar: fragment bytes and scales bit-exact against the natural-layout producer
 (itself pinned against the oracle in test_gpu_producers.py); GEMM outputs
 within 1 bf16 ulp or 1e-5 * sum |group terms| of the oracle, and equal bit for
 bit to the natural-layout prequantized entry where that runs the same
-matrix-core kernel (more than 4 rows).
+matrix-core kernel (more than 4 rows).  With a workspace, long K splits over
+workgroups: then the output equals the bf16 entry's (which quantizes the same
+rows on the device and runs the same split kernel) bit for bit, and the K
+split's block counters are whole epochs (multiples of 64) after every call.
 """
 import numpy as np
 import pytest
@@ -126,9 +129,10 @@ def test_swiglu_quantize_frag_equals_natural(torch_dev, M, I, G):
     _check_frag(xf, sf, want_q, want_s)
 
 
-# The GEMM from fragments: every format, single-segment and long-K (segment
-# loop) shapes, the north-star verify at full size, the reference engine's q
-# and down shapes, residual, ragged N.
+# The GEMM from fragments: every format, single-segment and long-K shapes
+# (segment loop without a workspace, K split with one), the north-star
+# verify at full size, the reference engine's q and down shapes, residual,
+# ragged N.
 @pytest.mark.parametrize("qtype,N,K,M", [
     (O.Q4_G64, 10240, 2560, 16),
     (O.Q4_G64, 2560, 10240, 8),
@@ -157,11 +161,67 @@ def test_prequantized_frag_against_oracle(torch_dev, qtype, N, K, M):
     y_nat = torch.zeros_like(y)
     assert va.linear_prequantized(w, dev(torch, np.asarray(xq, dtype=np.int8)), dev(torch, np.asarray(xs, dtype=np.float32)),
                                   y_nat, residual=rd).ok()
+    nws = va.frag_workspace_bytes(qtype, N, K, M)
+    ys = torch.zeros_like(y)
+    ws = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda")
+    assert va.linear_prequantized_frag(w, xf, sf, ys, residual=rd, workspace=ws).ok()
     torch.cuda.synchronize()
     O.assert_bf16_close(u16(y), y_ref, absterm, rel=REL_TOL)
     O.assert_bf16_close(u16(y_nat), y_ref, absterm, rel=REL_TOL)
+    O.assert_bf16_close(u16(ys), y_ref, absterm, rel=REL_TOL)
     if M > 4:   # the natural entry runs the same matrix-core kernel there (2-4 rows: the dot kernel, whose
         np.testing.assert_array_equal(u16(y), u16(y_nat))   # fp32 sums are added in another order)
+    if nws == 0:  # no split for this shape: the workspace is not used
+        np.testing.assert_array_equal(u16(ys), u16(y))
+    else:
+        assert split_state_ok(ws)
+
+
+def split_state_ok(ws):
+    """After a call: every K-split block counter is a whole epoch (64 * calls) and no sum missed."""
+    w = ws[:4352].cpu().numpy().view(np.uint32)
+    return int(w[1]) == 0 and bool((w[64:64 + 1024] % 64 == 0).all())
+
+
+# The K split of the fragment entry keeps its own counters: one zeroed
+# workspace serves frag calls of different shapes and part counts (K = 10240:
+# 4 parts of 10 quads, K = 10752: 6 of 7, K = 6144: 3 of 8, K = 8960: 5 of 7,
+# K = 11264: 4 of 11 (two quads per wave), W8 K = 6144: 6 of 8), growing and
+# shrinking in rows and row blocks, interleaved with the bf16 entry (its own
+# quantize launch and split) on the same bytes.  Every output against the
+# oracle; the frag output equal to the bf16 entry's bit for bit (same rows,
+# same kernel); counters whole epochs after every call; no sum missed.
+def test_frag_split_shapes_share_one_workspace(torch_dev):
+    torch = torch_dev
+    shapes = [(O.Q4_G64, 2560, 10240, 16), (O.Q4_G64, 3072, 10752, 5), (O.Q4_G64, 640, 10240, 16),
+              (O.Q4_G64, 2560, 10240, 6), (O.W8_G32, 1000, 6144, 9), (O.Q4_G64, 3072, 6144, 16),
+              (O.Q4_G64, 1000, 8960, 7), (O.Q4_G64, 700, 11264, 16), (O.Q5_G64, 2560, 10240, 8),
+              (O.Q4_G64, 2560, 10240, 16), (O.Q4_G64, 3072, 10752, 12)]
+    nws = max(max(va.workspace_bytes(*sh), va.frag_workspace_bytes(*sh)) for sh in shapes)
+    ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
+    for i, (qtype, N, K, M) in enumerate(shapes * 2):
+        print(f"shared workspace call {i}: qtype={qtype} N={N} K={K} M={M}", flush=True)
+        assert va.frag_workspace_bytes(qtype, N, K, M) > 0
+        G = O.group_size(qtype)
+        seed = 760 + 13 * (i % len(shapes))
+        packed, scales = O.gen_weights(qtype, N, K, seed, O.SCALE_FP16)
+        x = O.gen_act(M, K, seed + 1)
+        res = O.gen_act(M, N, seed + 2) if i % 3 == 1 else None
+        y_ref, _, absterm = O.qlinear(qtype, packed, scales, O.SCALE_FP16, N, K, x, residual=res)
+        w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, va.ScaleEnc.FP16)
+        xq, xs = O.quantize_act(x, G)
+        fq, fs = to_frag(np.asarray(xq, dtype=np.int8).reshape(M, K), np.asarray(xs, dtype=np.float32).reshape(M, K // G), G)
+        rd = None if res is None else dev(torch, res)
+        yf = torch.zeros((M, N), dtype=torch.int16, device="cuda")
+        yb = torch.full((M, N), 7, dtype=torch.int16, device="cuda")
+        assert va.linear_prequantized_frag(w, dev(torch, fq), dev(torch, fs), yf, residual=rd, workspace=ws).ok()
+        torch.cuda.synchronize()
+        assert split_state_ok(ws)
+        assert va.linear(w, dev(torch, x), yb, residual=rd, workspace=ws).ok()
+        torch.cuda.synchronize()
+        assert split_state_ok(ws)
+        O.assert_bf16_close(u16(yf), y_ref, absterm, rel=REL_TOL)
+        np.testing.assert_array_equal(u16(yb), u16(yf))
 
 
 def test_fused2_frag_equals_two_calls(torch_dev):
@@ -197,7 +257,18 @@ def test_frag_entry_errors(torch_dev):
     y = torch.zeros((4, 64), dtype=torch.int16, device="cuda")
     st = torch.cuda.current_stream().cuda_stream
     assert L.viper_hip_qlinear_prequantized_frag(4, w.data.data_ptr(), w.scales.data_ptr(), 0, 64, 64, 512,
-                                                 xf.data_ptr() + 8, sf.data_ptr(), 4, y.data_ptr(), None, st) == 2
+                                                 xf.data_ptr() + 8, sf.data_ptr(), 4, y.data_ptr(), None, None, 0,
+                                                 st) == 2
+    # a long-K shape with a workspace that is too small or misaligned
+    p3, s3 = O.gen_weights(O.Q4_G64, 64, 10240, 743, O.SCALE_FP16)
+    xf3, sf3 = _frag_buffers(torch, 10240, 64)
+    need = va.frag_workspace_bytes(O.Q4_G64, 64, 10240, 4)
+    assert need > 0
+    ws3 = torch.zeros(need + 16, dtype=torch.uint8, device="cuda")
+    args3 = (4, dev(torch, p3).data_ptr(), dev(torch, s3).data_ptr(), 0, 64, 64, 10240, xf3.data_ptr(),
+             sf3.data_ptr(), 4, y.data_ptr(), None)
+    assert L.viper_hip_qlinear_prequantized_frag(*args3, ws3.data_ptr(), need - 1, st) == 2
+    assert L.viper_hip_qlinear_prequantized_frag(*args3, ws3.data_ptr() + 8, need, st) == 2
     p2, s2 = O.gen_weights(O.Q4_G64, 64, 128, 741, O.SCALE_FP16)   # K = 2 groups: not a multiple of 4
     w2 = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, p2), dev(torch, s2), 64, 128, 64, va.ScaleEnc.FP16)
     assert va.linear_prequantized_frag(w2, xf, sf, y).code == va.StatusCode.INVALID_ARGUMENT

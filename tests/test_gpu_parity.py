@@ -163,9 +163,9 @@ def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
     run_case(torch_dev, qtype, N, K, M, seed=3000 + N + M, scale_enc=senc, residual=(M % 2 == 1))
 
 
-# Long K on the matrix cores (K of 24..80 quads of 4 groups, a multiple of 4
-# quads) splits K in 4 parts, one workgroup each; the last part of a row block
-# to finish adds the parts' sums in part order.  The workspace starts zeroed
+# Long K on the matrix cores (more than 20 quads of 4 groups) splits K in
+# 2..8 parts, one workgroup each; the last part of a row block to finish adds
+# the parts' sums in part order.  The workspace starts zeroed
 # (the contract) and serves a second call with another row count; a repeated
 # call must give the same bits.
 @pytest.mark.parametrize("qtype", FORMATS)
@@ -173,7 +173,10 @@ def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
     (2560, 10240, 16, 4, O.SCALE_FP16),   # down shape
     (50, 10240, 7, 3, O.SCALE_BF16),      # ragged last row block
     (1000, 6144, 12, 2, O.SCALE_FP16),    # 6 quads per part; M2 = 2 on the dot path
-    (333, 12288, 9, 16, O.SCALE_BF16),    # 12 quads per part (W8: 24, the segment loop)
+    (333, 12288, 9, 16, O.SCALE_BF16),    # 6 parts of 8 quads (W8: 8 parts of 12, two quads per wave)
+    (777, 8960, 9, 5, O.SCALE_FP16),      # 5 parts of 7 quads (W8: 70 quads, 7 parts of 10)
+    (500, 11264, 16, 6, O.SCALE_BF16),    # 4 parts of 11 quads: two quads per wave
+    (3072, 10752, 12, 16, O.SCALE_FP16),  # the reference engine's down shape: 6 parts of 7
 ])
 def test_k_split(torch_dev, qtype, N, K, M, M2, senc):
     torch = torch_dev
@@ -200,16 +203,16 @@ def test_k_split(torch_dev, qtype, N, K, M, M2, senc):
     assert missed_sums(ws) == 0
 
 
-# Seeded random shapes on the K split: K of 24..80 quads (every multiple of
-# 4 quads the split takes: one or two quads per wave and part), ragged N,
-# rows past the multi-row bound, both scale encodings, residual on odd M.
+# Seeded random shapes on the K split: K of 24..80 quads (2..8 parts of one
+# or two quads per wave), ragged N, rows past the multi-row bound, both scale
+# encodings, residual on odd M.
 def _k_split_shapes(n=12, seed=0x5EED5):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(n):
         qtype = FORMATS[i % len(FORMATS)]
         G = O.group_size(qtype)
-        nq = int(rng.choice([24, 28, 32, 36, 40, 48, 56, 64, 72, 80]))
+        nq = int(rng.choice([24, 28, 30, 32, 35, 36, 40, 42, 45, 48, 56, 64, 72, 80]))
         K = nq * 4 * G
         M = int(rng.integers(max(4, 32768 // K + 1), 17))
         N = int(rng.integers(1, 3000))
@@ -276,12 +279,13 @@ def _run_split_case(torch, c, ws, i):
     O.assert_bf16_close(host(yd, np.uint16), c["y_ref"], c["absterm"], rel=REL_TOL)
 
 
-# Split shapes of different sizes alternating on one zeroed workspace: the
-# generation word sits at offset 0 for every shape, so every call draws a new
-# one; with a shape-dependent generation word these two shapes would reuse
-# generation 5 from the 5th call on (the small call's word is a counter of
-# the large call's) and could accept the other call's sums.  Every call is
-# checked against the oracle (group dots bit-exact), and no sum may miss.
+# Split shapes of different sizes alternating on one zeroed workspace: each
+# row block's record of slots and its counter (whose epoch tags the slots)
+# sit at the same offsets for every shape, so a slot can only hold an earlier
+# epoch of its own block; the two shapes' blocks cover different rows and
+# different slot ranges of the same records.  Every call is checked against
+# the oracle (group dots bit-exact); counters are whole epochs after every
+# call and no sum may miss.
 def test_k_split_shapes_alternate_on_one_workspace(torch_dev):
     torch = torch_dev
     cases = [_split_case(torch, O.Q4_G64, 2048, 10240, 5, 0x5A10),
@@ -290,6 +294,8 @@ def test_k_split_shapes_alternate_on_one_workspace(torch_dev):
     ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
     for i in range(10):
         _run_split_case(torch, cases[i % 2], ws, i)
+        counters = ws[256:256 + 4096].cpu().numpy().view(np.uint32)
+        assert (counters % 64 == 0).all()
     assert missed_sums(ws) == 0
 
 
@@ -843,6 +849,30 @@ def test_clock_stamp_probe(torch_dev):
     assert 0 < t1 - t0 < 100_000_000
     assert L.viper_hip_clock_stamp(None, st) == 2
     assert L.viper_hip_clock_stamp(t.data_ptr() + 4, st) == 2
+
+
+def test_empty_dispatch_probe(torch_dev):
+    # the dispatch-cost probe: with y, lane 0 of every 16-lane team stores its row index (as a
+    # 16-bit word) and nothing else is written; without y nothing is written; bad launch shapes and a
+    # misaligned y are rejected before any launch
+    torch = torch_dev
+    L = va.lib()
+    st = torch.cuda.current_stream().cuda_stream
+    wg, nt = 512, 320
+    rows = wg * nt // 16
+    y = torch.full((rows + 8,), -1, dtype=torch.int16, device="cuda")
+    assert L.viper_hip_empty_dispatch(wg, nt, None, st) == 0
+    torch.cuda.synchronize()
+    assert bool((y == -1).all())
+    assert L.viper_hip_empty_dispatch(wg, nt, y.data_ptr(), st) == 0
+    torch.cuda.synchronize()
+    got = y.cpu().numpy().view(np.uint16)
+    np.testing.assert_array_equal(got[:rows], (np.arange(rows) & 0xFFFF).astype(np.uint16))
+    assert (got[rows:] == 0xFFFF).all()
+    assert L.viper_hip_empty_dispatch(0, nt, None, st) == 2
+    assert L.viper_hip_empty_dispatch(wg, 100, None, st) == 2
+    assert L.viper_hip_empty_dispatch(wg, 2048, None, st) == 2
+    assert L.viper_hip_empty_dispatch(wg, nt, y.data_ptr() + 1, st) == 2
 
 
 def test_stream_read_probe(torch_dev):

@@ -59,11 +59,10 @@ def _call_pair(torch, L, qtype, N, K, M, seed, residual):
 
 
 # (qtype, N, K, M) sequences: shrinking (the K split (long K) with its
-# control words and sums, the fragment quantize + matrix-core path, the
+# counters and records of sums, the fragment quantize + matrix-core path, the
 # multi-row path, and M = 1 with no workspace at all), growing (each call's
-# K-split sums cover more of the array than the last) and two K-split shapes
-# alternating (with a shape-dependent generation word they would share
-# generation 5 from the 5th call on).
+# K-split sums cover more of the array than the last), two K-split shapes
+# alternating, and K splits in 4 and 3 parts (K = 10240, 10752) alternating.
 SEQUENCES = [
     [(O.Q4_G64, 2560, 10240, 16), (O.Q4_G64, 1000, 10240, 5)],
     [(O.W8_G32, 2048, 10240, 12), (O.W8_G32, 777, 6144, 4)],
@@ -72,6 +71,7 @@ SEQUENCES = [
     [(O.Q4_G64, 2560, 10240, 5), (O.Q4_G64, 2560, 10240, 6), (O.Q4_G64, 2560, 10240, 16),
      (O.Q4_G64, 1000, 10240, 16), (O.Q4_G64, 2560, 10240, 16)],
     [(O.Q4_G64, 2048, 10240, 5), (O.Q4_G64, 640, 10240, 16)] * 5,
+    [(O.Q4_G64, 3072, 10752, 16), (O.Q4_G64, 2560, 10240, 9)] * 3,
 ]
 
 
@@ -85,8 +85,9 @@ def test_static_equals_workspace_entry(torch_dev, seq):
 def test_static_rejects_past_the_array():
     L = va.lib()
     cap = 8 << 20
-    N, K, M = 65536, 10240, 16          # K-split sums alone: 4 * 16 * 65536 * 8 bytes
-    assert L.viper_hip_qlinear_workspace_bytes(O.Q4_G64, N, K, M) > cap
-    fake = C.c_void_p(0x10000)          # never dereferenced: the size check comes first
-    rc = L.viper_hip_qlinear_static(O.Q4_G64, fake, fake, 0, 64, N, K, fake, M, fake, None, None)
-    assert rc == 2
+    for N, K, M in ((64, 1 << 20, 16),        # int8 activations alone: 16 * 2^20 bytes
+                    (8192, 10240, 16)):       # K-split records: 171 blocks of 48 rows x 49152 bytes
+        assert L.viper_hip_qlinear_workspace_bytes(O.Q4_G64, N, K, M) > cap
+        fake = C.c_void_p(0x10000)          # never dereferenced: the size check comes first
+        rc = L.viper_hip_qlinear_static(O.Q4_G64, fake, fake, 0, 64, N, K, fake, M, fake, None, None)
+        assert rc == 2

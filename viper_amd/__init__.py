@@ -8,4 +8,4 @@ from .qlinear import (GROUP, MAX_M, Prologue, QType, QuantizedWeight, ScaleEnc, 
                       linear_m1_swiglu, linear_partials, linear_prequantized, packed_bytes, qtype_name, quantize_act,
                       linear_bf16, rmsnorm_quantize, sampling_greedy, greedy_workspace_bytes, swiglu_quantize,
                       workspace_bytes, workspace_layout, frag_bytes, rmsnorm_quantize_frag, swiglu_quantize_frag,
-                      linear_prequantized_frag, linear_fused2_prequantized_frag)
+                      linear_prequantized_frag, linear_fused2_prequantized_frag, frag_workspace_bytes)

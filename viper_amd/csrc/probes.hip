@@ -73,6 +73,18 @@ __global__ void __launch_bounds__(64) clock_stamp_kernel(uint64_t* out) {
     if (threadIdx.x == 0) out[0] = t;
 }
 
+// A dispatch that reads nothing: with y, lane 0 of every 16-lane team stores
+// one bf16 (its row index) to y[row], the M = 1 GEMV's output pattern;
+// without it nothing is stored.  Back-to-back launches time the fixed cost
+// of a dispatch of the given grid, with and without the GEMV's row stores.
+__global__ void __launch_bounds__(1024) empty_probe_kernel(uint16_t* y) {
+    const int tid = (int)threadIdx.x;
+    if (y != nullptr && (tid & 15) == 0) {
+        const int row = ((int)blockIdx.x * (int)blockDim.x + tid) >> 4;
+        y[row] = (uint16_t)row;
+    }
+}
+
 // Warms a byte range into the memory-side cache (MALL): workgroup b reads
 // chunk b of the range with plain (allocating) 16-byte loads, PF_LOADS per
 // thread in flight per round, and folds the words so the loads stay live
@@ -109,6 +121,17 @@ extern "C" int viper_hip_prefetch(const void* buf, size_t bytes, int workgroups,
     chunk = (chunk + 15) / 16 * 16;
     void* args[] = {&a0, &a1, &chunk, &sink};
     vq::launch((const void*)vq::prefetch_kernel, (unsigned)workgroups, vq::PF_NT, 0, (hipStream_t)stream, args);
+    return vq::status_of(hipGetLastError());
+}
+
+extern "C" int viper_hip_empty_dispatch(int workgroups, int threads, void* y_bf16, void* stream) {
+    if (workgroups <= 0 || workgroups > 65536 || threads <= 0 || threads > 1024 || threads % 64 != 0)
+        return VIPER_INVALID_ARGUMENT;
+    if (vq::misaligned(y_bf16, 2)) return VIPER_INVALID_ARGUMENT;
+    uint16_t* a0 = (uint16_t*)y_bf16;
+    void* args[] = {&a0};
+    vq::launch((const void*)vq::empty_probe_kernel, (unsigned)workgroups, (unsigned)threads, 0, (hipStream_t)stream,
+               args);
     return vq::status_of(hipGetLastError());
 }
 

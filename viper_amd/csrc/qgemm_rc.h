@@ -44,10 +44,13 @@
 // a later argument is a scalar load from the argument buffer that the wave
 // waits for (the weight-scale encoding read after the weight loads cost
 // 0.17 us of the M = 16 verify, the residual pointer waited for before the
-// first load 0.3 us).  So everything the common path reads fits 14 dwords:
-// N, M - 1 and the encoding share one word (nm: N in bits 0..26, M - 1 in
-// 27..30, the encoding in bit 31) and the first matrix's workgroup count is
-// derived from N (both matrices of a pair have N rows).
+// first load 0.3 us).  So everything the common path reads before its loads
+// fits 14 dwords: N, M - 1 and the encoding share one word (nm: N in bits
+// 0..26, M - 1 in 27..30, the encoding in bit 31), K and the K split's part
+// count share another (kk), the first matrix's workgroup count is derived
+// from N (both matrices of a pair have N rows), and the K split's control
+// words (sc, whose block counter is the split's first load) come before the
+// residual, which is read only when the outputs are formed.
 //
 // Activation modes (AM): RC_FRAG reads the fragments and [group][16] scales
 // the fragment quantize wrote; RC_NAT gathers them from the natural layout
@@ -104,57 +107,61 @@ struct RcSeg {
 // ONE: the quads of every wave fit one load segment.  SE: the weight-scale
 // encoding, fp16 (0) or bf16 (1) as a constant for the production variants
 // (a run-time choice cost 0.1 us of the M = 16 verify), or read from nm (2)
-// for the partials and natural-layout variants.  SK > 1 (fragment input
-// only): K split into SK equal parts, one workgroup per (row block, part),
-// blockIdx = SK * block + part; each part stores its fp32 sums to sp
-// [SK][M][N], and the last part of a block to arrive (counter
-// sc[RC_CTL_CNT + block], zeroed by the fragment quantize launch) adds the SK
-// sums in part order, so the result does not depend on which part finishes
-// last.  Partials (PART) are written by each part for its own groups.  PR:
-// the launch may carry a fused pair (without it the matrix select is not
-// compiled).
+// for the partials and natural-layout variants.  KS (fragment input only):
+// K split into sk equal parts (sk = K's argument word >> 27, 2..RC_SK_MAX),
+// one workgroup per (row block, part), blockIdx = sk * block + part; each
+// part stores its fp32 sums to its block's record of slots, and the last
+// part of a block to count adds the sk sums in part order, so the result
+// does not depend on which part finishes last.  Partials (PART) are written
+// by each part for its own groups.  PR: the launch may carry a fused pair
+// (without it the matrix select is not compiled).
 //
-// The exchange between the parts of a block.  Each sum travels in a 64-bit
-// slot {tag, fp32 bits}, written and read as agent-scope relaxed atomics.
-// sc points at the workspace's control words, at offset 0 for every shape:
-// sc[RC_CTL_GEN] is the generation, which the fragment quantize launch
-// increments once per call, so every call on one workspace, whatever its
-// shape, draws a new one; the tag is rc_tag(generation): top byte 0x80, the
-// generation's low 24 bits below it.  No other word the library stores in a
+// The exchange between the parts of a block needs no launch before it and
+// leaves the workspace ready for the next call of any shape.  Each sum
+// travels in a 64-bit slot {tag, fp32 bits}, written and read as agent-scope
+// relaxed atomics, at a place that depends only on (block, part, row m, row
+// of the block): record `block` of RC_REC_SLOTS slots, so only that block
+// ever writes it, whatever the shape.  The block's counter sc[RC_CTL_CNT +
+// block] holds 64 * epoch + (parts of the running call that have counted):
+// every part reads it when it starts (its first load: at most sk - 1 parts
+// have counted by then, so every part sees the same epoch), tags its slots
+// rc_tag(epoch) and counts once its slot stores are issued; the part that
+// counts sk - 1 is the last and adds 64 - sk, which moves the counter to
+// the next epoch for the next call.  No other word the library stores in a
 // workspace can equal a tag: int8 activations are in [-127, 127] (never the
-// byte 0x80), fp32 activation scales are positive, counters are at most SK.
-// So in a workspace zero-filled before its first use, a slot that carries
-// this call's tag was written by this call (a slot written 2^24 calls
-// earlier and not rewritten since is the only exception).  The last part
-// accepts a slot only when it carries the current tag and re-reads it
-// otherwise (bounded by RC_SPIN; then the output is NaN and
-// sc[RC_CTL_MISS] is incremented, a count the library never clears).  So
+// byte 0x80) and fp32 activation scales are positive; counters live in their
+// own region.  So in a workspace zero-filled before its first use, a slot
+// that carries the block's current tag was written by this call (a slot
+// written 2^24 epochs earlier and not rewritten since is the only
+// exception).  The last part accepts a slot only when it carries the current
+// tag and re-reads it otherwise (bounded by RC_SPIN; then the output is NaN
+// and sc[RC_CTL_MISS] is incremented, a count the library never clears).  So
 // the result depends only on the coherence of the atomic accesses to each
 // slot, not on any ordering between the slots and the counter.  (An
 // agent-scope release/acquire pair would order them but costs a write-back
 // and an invalidate of the XCD's L2 per workgroup: 70 us on the down shape.)
-// A part counts as soon as its slot stores are issued; the last part
-// requests every slot at once, then re-reads any that does not yet carry
-// the current tag.
+// The last part requests every slot at once, then re-reads any that does not
+// yet carry the current tag.
 // TLM (measurement, fragment input, one segment, no split): `part` receives
 // per-wave s_memrealtime readings (100 MHz) at RC_TL_STAMPS points --
 // [workgroup][wave][RC_TL_STAMPS] uint64: wave start, activation and scale
 // loads issued, weight loads issued, staged scales in LDS, first group
 // scaled, last group scaled, cross-wave barrier passed, outputs stored.
 constexpr int RC_TL_STAMPS = 8;
-template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, int SK = 1, bool PR = true,
+template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, bool KS = false, bool PR = true,
           bool TLM = false>
 __global__ void __launch_bounds__(64 * W)
-qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, int K,
-                unsigned nm, const uint16_t* res, int32_t* __restrict__ part,
-                const uint8_t* w1, const uint16_t* ws1, uint16_t* y1, uint64_t* __restrict__ sp,
-                unsigned* __restrict__ sc) {
+qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint16_t* ws, uint16_t* y, unsigned kk,
+                unsigned nm, unsigned* __restrict__ sc, const uint16_t* res, int32_t* __restrict__ part,
+                const uint8_t* w1, const uint16_t* ws1, uint16_t* y1) {
     using FM = RcFmt<F>;
     using Seg = RcSeg<F, RB, QW>;
     constexpr int T = Seg::T;
     constexpr bool XNAT = AM == RC_NAT, XBF = AM == RC_BF16;
-    static_assert(SK == 1 || AM == RC_FRAG, "the K split reads fragments");
-    static_assert(!TLM || (ONE && !PART && SK == 1 && AM == RC_FRAG), "timeline: one fragment-input segment");
+    static_assert(!KS || AM == RC_FRAG, "the K split reads fragments");
+    static_assert(!TLM || (ONE && !PART && !KS && AM == RC_FRAG), "timeline: one fragment-input segment");
+    // K in bits 0..26, the K split's part count in 27..31
+    const int K = (int)(kk & 0x07FFFFFFu), SK = KS ? (int)(kk >> 27) : 1;
     uint64_t tstamp[RC_TL_STAMPS];
     auto stamp = [&](int i) {
         if constexpr (TLM) tstamp[i] = __builtin_amdgcn_s_memrealtime();
@@ -172,9 +179,17 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     const int nb0 = (N + 8 * RB - 1) / (8 * RB);
     int bid = (int)blockIdx.x;
     int q0 = 0;  // first quad of the part
-    if constexpr (SK > 1) {
+    uint32_t cnt0 = 0;
+    if constexpr (KS) {
         q0 = (int)(blockIdx.x % SK) * NQ;
         bid = (int)(blockIdx.x / SK);
+        // the block's counter, for its epoch: the first vector load of the
+        // kernel, so it returns ahead of the weights (loads retire in issue
+        // order) and no wait for an earlier load or LDS access waits for it
+        // (a scalar load made the first LDS barrier wait for it: down shape
+        // 0.25-0.45 us slower)
+        cnt0 = bload4(buf(sc + RC_CTL_CNT + bid, 4u), 0);
+        issue_fence();
     }
     // the second matrix of a fused pair and the residual are the rare paths:
     // marked unlikely, the common path is laid out and scheduled straight
@@ -206,7 +221,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     // RC_BF16: the LDS fragments and scales (after the transpose buffers and
     // the cross-wave sums)
     int8_t* lxq = (int8_t*)(smem + rc_lds_bytes(FM::HSTR, RB, W));
-    float* lxs = (float*)(lxq + (size_t)NG * 64 * FM::QB);
+    float* lxs = (float*)(lxq + (size_t)NQ * 4 * 64 * FM::QB);
     constexpr int NTT = 64 * W;
     const int KO = K / 8, noct = M * KO;  // RC_BF16: octets of all rows
     u32x4 xv[XBF ? RC_XR : 1];
@@ -532,12 +547,10 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     stamp(6);
     constexpr int MINE = (4 * T + W - 1) / W;
     float mine[MINE] = {};
-    const int kpart = SK > 1 ? (int)(blockIdx.x % SK) : 0;
-    // K split: this call's tag (from the generation the preceding quantize
-    // launch wrote), read once the sums are formed: issued earlier as a
-    // vector load among the weights it cost 2 us of the down-shape launch
-    unsigned tag = 0;
-    if constexpr (SK > 1) tag = rc_tag(sc[RC_CTL_GEN]);
+    const int kpart = KS ? (int)(blockIdx.x % SK) : 0;
+    // K split: the block's record of slots and this call's tag
+    uint64_t* rec = KS ? (uint64_t*)((uint8_t*)sc + RC_CTL_BYTES) + (size_t)bid * RC_REC_SLOTS : nullptr;
+    const unsigned tag = rc_tag((unsigned)__builtin_amdgcn_readfirstlane((int)cnt0) >> 6);
 #pragma unroll
     for (int i = 0; i < MINE; ++i) {
         const int sl = wave + i * W;
@@ -550,8 +563,8 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         const int m = 4 * kb + r, nl = 16 * t + n16;
         if (m < M && nl < nrows) {
             const size_t o = (size_t)m * N + row0 + nl;
-            if constexpr (SK > 1) {
-                __hip_atomic_store(sp + (size_t)kpart * M * N + o, ((uint64_t)tag << 32) | __float_as_uint(v),
+            if constexpr (KS) {
+                __hip_atomic_store(rec + (kpart * 16 + m) * RC_REC_ROWS + nl, ((uint64_t)tag << 32) | __float_as_uint(v),
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             } else {
                 if (__builtin_expect(res != nullptr, 0)) v += bf16f(res[o]);
@@ -567,32 +580,39 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
             for (int i = 0; i < RC_TL_STAMPS; ++i) o[i] = tstamp[i];
         }
     }
-    if constexpr (SK > 1) {
+    if constexpr (KS) {
         // count once every wave's slot stores are issued; a slot whose store
         // is still in flight when the last part reads it is re-read (waiting
-        // for the stores to complete before counting measured 0.4 us slower)
+        // for the stores to complete before counting measured 0.4 us slower).
+        // The last part moves the counter to the next epoch (64 * (epoch + 1)).
         lds_barrier();
         int* last = (int*)red;
-        if (tid == 0) last[0] = atomicAdd(sc + RC_CTL_CNT + bid, 1u) == (unsigned)(SK - 1);
+        if (tid == 0) {
+            unsigned* cnt = sc + RC_CTL_CNT + bid;
+            const unsigned old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int is_last = (int)(old & 63u) == SK - 1;
+            if (is_last) __hip_atomic_fetch_add(cnt, (unsigned)(64 - SK), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            last[0] = is_last;
+        }
         lds_barrier();
         if (!last[0]) return;
         // every slot of the other parts is requested at once (a load that
         // waited for the previous one's tag would serialise the round trips:
         // 0.4 us of the down-shape launch), then the tags are checked and a
         // slot that does not carry this call's tag yet is re-read
-        uint64_t u[MINE][SK];
+        uint64_t u[MINE][RC_SK_MAX];
 #pragma unroll
         for (int i = 0; i < MINE; ++i) {
             const int sl = wave + i * W;
             const int t = sl >> 2, r = sl & 3;
             const int m = 4 * kb + r, nl = 16 * t + n16;
             const bool ok = sl < 4 * T && m < M && nl < nrows;
-            const size_t o = (size_t)m * N + row0 + nl;
 #pragma unroll
-            for (int p = 0; p < SK; ++p) {
+            for (int p = 0; p < RC_SK_MAX; ++p) {
                 u[i][p] = ((uint64_t)tag << 32) | __float_as_uint(mine[i]);
-                if (ok && p != kpart)
-                    u[i][p] = __hip_atomic_load(sp + (size_t)p * M * N + o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (ok && p < SK && p != kpart)
+                    u[i][p] = __hip_atomic_load(rec + (p * 16 + m) * RC_REC_ROWS + nl, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
             }
         }
         unsigned missed = 0;  // sums that never arrived (NaN in y), counted in the workspace
@@ -606,10 +626,11 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                 const size_t o = (size_t)m * N + row0 + nl;
                 float v = 0.0f;
 #pragma unroll
-                for (int p = 0; p < SK; ++p) {
+                for (int p = 0; p < RC_SK_MAX; ++p) {
+                    if (p >= SK) break;
                     uint64_t w = u[i][p];
                     if (__builtin_expect((unsigned)(w >> 32) != tag, 0)) {
-                        uint64_t* a = sp + (size_t)p * M * N + o;
+                        uint64_t* a = rec + (p * 16 + m) * RC_REC_ROWS + nl;
                         for (int it = 0; (unsigned)(w >> 32) != tag && it < RC_SPIN; ++it)
                             w = __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
@@ -628,15 +649,15 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
 
 // ------------------------------------------------------------------ host side
 
-typedef void (*rc_fn)(const int8_t*, const float*, const uint8_t*, const uint16_t*, uint16_t*, int, unsigned,
-                      const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*, uint64_t*, unsigned*);
+typedef void (*rc_fn)(const int8_t*, const float*, const uint8_t*, const uint16_t*, uint16_t*, unsigned, unsigned,
+                      unsigned*, const uint16_t*, int32_t*, const uint8_t*, const uint16_t*, uint16_t*);
 
 // Launch shape: rows per workgroup (8 * rb), waves, quads per wave per
 // segment, single segment or double-buffered loop.
 struct RcShape {
     int rb, w, qw;
     bool one;
-    int sk = 1;  // parts of K (1: no split, else RC_SK)
+    int sk = 1;  // parts of K (1: no split, else 2..RC_SK_MAX)
 };
 // Most 8-row blocks per workgroup that two quads per wave, or the
 // double-buffered segment loop, hold in registers without spilling.
@@ -645,8 +666,8 @@ constexpr int RC_RB_LOOP = 2;
 
 template <int F, int RB, int W, int QW, bool ONE, int AM, int SE>
 rc_fn rc_pick5(bool pair) {
-    return pair ? qgemm_rc_kernel<F, RB, W, QW, ONE, AM, false, SE, 1, true>
-                : qgemm_rc_kernel<F, RB, W, QW, ONE, AM, false, SE, 1, false>;
+    return pair ? qgemm_rc_kernel<F, RB, W, QW, ONE, AM, false, SE, false, true>
+                : qgemm_rc_kernel<F, RB, W, QW, ONE, AM, false, SE, false, false>;
 }
 template <int F, int RB, int W, int QW, bool ONE>
 rc_fn rc_pick4(int am, bool part, int senc, bool pair) {
@@ -661,14 +682,14 @@ rc_fn rc_pick4(int am, bool part, int senc, bool pair) {
 }
 template <int F, int RB, int QW>
 rc_fn rc_pick_split(int senc, bool part) {
-    if (part) return qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, true, 2, RC_SK, false>;
-    return senc ? qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 1, RC_SK, false>
-                : qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 0, RC_SK, false>;
+    if (part) return qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, true, 2, true, false>;
+    return senc ? qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 1, true, false>
+                : qgemm_rc_kernel<F, RB, 10, QW, true, RC_FRAG, false, 0, true, false>;
 }
 template <int F, int RB>
 rc_fn rc_pick3(const RcShape& s, int am, bool part, int senc, bool pair) {
     if (s.sk != 1) {  // K split: fragment input, one segment of 10 waves
-        if (s.sk != RC_SK || am != RC_FRAG || !s.one || s.w != 10) return nullptr;
+        if (s.sk < 2 || s.sk > RC_SK_MAX || am != RC_FRAG || !s.one || s.w != 10 || pair) return nullptr;
         if (s.qw == 1) return rc_pick_split<F, RB, 1>(senc, part);
         if constexpr (RB <= rc_rb_qw2(F))
             if (s.qw == 2) return rc_pick_split<F, RB, 2>(senc, part);
@@ -700,8 +721,8 @@ template <int F, int RB>
 rc_fn rc_pick_tl3(const RcShape& s, int senc) {
 #define VQ_RC_TL(W_, QW_)                                                                              \
     if (s.w == W_ && s.qw == QW_)                                                                      \
-        return senc ? qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 1, 1, false, true>         \
-                    : qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 0, 1, false, true>;
+        return senc ? qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 1, false, false, true>     \
+                    : qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 0, false, false, true>;
     VQ_RC_TL(4, 1)
     VQ_RC_TL(10, 1)
     if constexpr (RB <= rc_rb_qw2(F)) VQ_RC_TL(10, 2)

@@ -2,6 +2,10 @@
 // shape and dispatch.  The kernel template is in qgemm_rc.h.
 #include "qgemm_rc.h"
 
+#include <map>
+#include <mutex>
+#include <utility>
+
 namespace vq {
 
 // Waves per workgroup and quads per wave of the single-segment shapes, in
@@ -33,31 +37,80 @@ static RcShape rc_shape(int F, int rows_total, int NQ, int cus) {
 }
 
 // K split (fragment input): K whose unsplit shape is the segment loop, in
-// RC_SK parts that each fit one segment of 10 waves (one or two quads per
-// wave); rows per workgroup spread the RC_SK * N (row, part) pairs over two
-// workgroups per CU.  Down shape K = 10240, N = 2560: 107 blocks of 24 rows x
-// 4 parts instead of 160 blocks of 16 rows that each read all of K's
-// activation (M = 4 / 8 / 16: 9.47 / 9.45 / 9.87 us; 40 rows, one workgroup
-// per CU: 9.9 / 9.8 / 10.0 us; 16 rows 11.3 / 11.6 / 11.9 us).
-static bool rc_split_fits(int NQ) { return NQ > 20 && NQ % RC_SK == 0 && NQ / RC_SK <= 20; }
+// sk parts that each fit one segment of 10 waves: the fewest parts of at most
+// 10 quads (one per wave; K = 10240: 4 parts, K = 6144: 3 parts of 8 quads,
+// 6.7 us at M = 16 and N = 3072 against 7.3 us for 4 parts of 6), else of at
+// most 20 (two per wave).  Rows per workgroup spread the sk * N (row, part)
+// pairs over two workgroups per CU where the kernel fits two (down shape
+// K = 10240, N = 2560: 107 blocks of 24 rows x 4 parts instead of 160 blocks
+// of 16 rows that each read all of K's activation, M = 4 / 8 / 16: 9.47 /
+// 9.45 / 9.87 us; 40 rows, one workgroup per CU: 9.9 / 9.8 / 10.0 us; 16 rows
+// 11.3 / 11.6 / 11.9 us), and never leave workgroups for a second round: a
+// launch with more workgroups than fit the CUs at once took twice as long
+// (K = 10752, N = 3072, 40-row blocks whose registers fit one workgroup per
+// CU: 13.7 us).
+static int rc_split_parts(int NQ) {
+    if (NQ <= 20) return 0;
+    for (int lim : {10, 20})
+        for (int sk = 2; sk <= RC_SK_MAX; ++sk)
+            if (NQ % sk == 0 && NQ / sk <= lim) return sk;
+    return 0;
+}
 
-static bool rc_split_shape(int F, int N, int NQ, int cus, RcShape& s) {
-    if (!rc_split_fits(NQ)) return false;
+// Workgroups of a launch one CU holds at once (2 where the device cannot be
+// asked: the shapes' design point), cached per kernel and LDS size.
+static int rc_occupancy(rc_fn fn, int threads, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void*, size_t>, int> cache;
+    const std::pair<const void*, size_t> key((const void*)fn, lds);
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void*)fn, threads, lds) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        return 2;
+    }
+    cache[key] = n;
+    return n;
+}
+
+static size_t rc_launch_lds(int qtype, const RcShape& sh, int K, int am);
+
+static bool rc_split_shape(int qtype, int rows, int K, int cus, RcShape& s) {
+    const int F = qtype == VIPER_QTYPE_W8_G32 ? 8 : qtype, NQ = K / group_of(qtype) / 4;
+    const int sk = rc_split_parts(NQ);
+    if (sk == 0) return false;
     s.w = 10;
     s.one = true;
-    s.qw = NQ / RC_SK <= 10 ? 1 : 2;
-    s.sk = RC_SK;
-    const int rb = (RC_SK * N + 16 * cus - 1) / (16 * cus), rbmax = s.qw == 2 ? rc_rb_qw2(F) : 6;
-    s.rb = rb < 1 ? 1 : (rb > rbmax ? rbmax : rb);
-    return true;
+    s.qw = NQ / sk <= 10 ? 1 : 2;
+    s.sk = sk;
+    const int rbmax = s.qw == 2 ? rc_rb_qw2(F) : 6;
+    int rb = (sk * rows + 16 * cus - 1) / (16 * cus);
+    rb = rb < 1 ? 1 : (rb > rbmax ? rbmax : rb);
+    for (s.rb = rb;; ++s.rb) {
+        const long wgs = (long)(rows + 8 * s.rb - 1) / (8 * s.rb) * sk;
+        rc_fn fn;
+        switch (F) {
+            case 4: fn = rc_pick<4>(s, RC_FRAG, false, 0, false); break;
+            case 5: fn = rc_pick<5>(s, RC_FRAG, false, 0, false); break;
+            case 6: fn = rc_pick<6>(s, RC_FRAG, false, 0, false); break;
+            default: fn = rc_pick<8>(s, RC_FRAG, false, 0, false); break;
+        }
+        if (s.rb == rbmax || fn == nullptr ||
+            wgs <= (long)rc_occupancy(fn, 64 * s.w, rc_launch_lds(qtype, s, K, RC_FRAG)) * cus)
+            break;
+    }
+    return (rows + 8 * s.rb - 1) / (8 * s.rb) <= RC_CNT_MAX;
 }
 
-bool rc_split_ok(int qtype, int K) {
+int rc_split_blocks(int qtype, int N, int K) {
     const int G = group_of(qtype);
-    return G != 0 && K % (4 * G) == 0 && rc_split_fits(K / G / 4);
+    if (G == 0 || K % (4 * G) != 0 || K >= (1 << 27)) return 0;
+    RcShape s{0, 0, 0, true};
+    if (!rc_split_shape(qtype, N, K, device_cus(), s)) return 0;
+    return (N + 8 * s.rb - 1) / (8 * s.rb);
 }
-
-size_t rc_split_bytes(int N, int M) { return align16((size_t)RC_SK * M * N * 8); }
 
 bool rc_ok(int qtype, int K) {
     const int G = group_of(qtype);
@@ -76,8 +129,9 @@ static int rc_hstr(int qtype) {
 static size_t rc_launch_lds(int qtype, const RcShape& sh, int K, int am) {
     const int qb = qtype == VIPER_QTYPE_W8_G32 ? RcFmt<8>::QB : RcFmt<4>::QB;
     const bool staged = sh.one && am == RC_FRAG && rc_hstr(qtype) == 0;  // the kernel's staged scales
-    return rc_lds_bytes(rc_hstr(qtype), sh.rb, sh.w) + (am == RC_BF16 ? rc_act_lds_bytes(qb, K / group_of(qtype)) : 0) +
-           (staged ? rc_stage_bytes(sh.rb, K / group_of(qtype) / 4 / sh.sk) : 0);
+    const int ngp = K / group_of(qtype) / sh.sk;  // groups of the workgroup's part
+    return rc_lds_bytes(rc_hstr(qtype), sh.rb, sh.w) + (am == RC_BF16 ? rc_act_lds_bytes(qb, ngp) : 0) +
+           (staged ? rc_stage_bytes(sh.rb, ngp / 4) : 0);
 }
 
 static RcShape rc_launch_shape(int qtype, int rows_total, int K) {
@@ -102,9 +156,8 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     if (am == RC_BF16 && !rc_bf16_ok(qtype, N, K, M, w1 != nullptr)) return VIPER_INTERNAL;
     RcShape sh = rc_launch_shape(qtype, w1 != nullptr ? 2 * N : N, K);
     if (sp != nullptr) {
-        const int F = qtype == VIPER_QTYPE_W8_G32 ? 8 : qtype;
-        if (am != RC_FRAG || w1 != nullptr || sc == nullptr ||
-            !rc_split_shape(F, N, K / group_of(qtype) / 4, device_cus(), sh))
+        if (am != RC_FRAG || w1 != nullptr || sc == nullptr || K >= (1 << 27) ||
+            !rc_split_shape(qtype, N, K, device_cus(), sh))
             return VIPER_INTERNAL;
     }
     rc_fn fn;
@@ -117,7 +170,7 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     if (fn == nullptr) return VIPER_INTERNAL;
     int nb0 = (N + 8 * sh.rb - 1) / (8 * sh.rb);
     const unsigned grid = (unsigned)(w1 != nullptr ? 2 * nb0 : nb0 * sh.sk);
-    if (sh.sk > 1 && nb0 > rc_split_counters(N)) return VIPER_INTERNAL;
+    if (sh.sk > 1 && nb0 > RC_CNT_MAX) return VIPER_INTERNAL;
     const size_t lds = rc_launch_lds(qtype, sh, K, am);
     const int8_t* a0 = (const int8_t*)xq;
     const float* a1 = (const float*)xs;
@@ -129,7 +182,8 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     const uint16_t* b1 = (const uint16_t*)s1;
     uint16_t* b2 = (uint16_t*)y1;
     unsigned nm = (unsigned)N | ((unsigned)(M - 1) << 27) | (senc ? 1u << 31 : 0u);  // see the kernel's arguments note
-    void* args[] = {&a0, &a1, &a2, &a3, &a4, &K, &nm, &a5, &part, &b0, &b1, &b2, &sp, &sc};
+    unsigned kk = (unsigned)K | (sh.sk > 1 ? (unsigned)sh.sk << 27 : 0u);
+    void* args[] = {&a0, &a1, &a2, &a3, &a4, &kk, &nm, &sc, &a5, &part, &b0, &b1, &b2};
     launch((const void*)fn, grid, (unsigned)(64 * sh.w), lds, st, args);
     return status_of(hipGetLastError());
 }
@@ -161,7 +215,8 @@ int launch_rc_timeline(int qtype, const void* w, const void* s, int senc, int N,
     uint64_t* sp = nullptr;
     unsigned* sc = nullptr;
     unsigned nm = (unsigned)N | ((unsigned)(M - 1) << 27) | (senc ? 1u << 31 : 0u);
-    void* args[] = {&a0, &a1, &a2, &a3, &a4, &K, &nm, &a5, &part, &b0, &b1, &b2, &sp, &sc};
+    unsigned kk = (unsigned)K;
+    void* args[] = {&a0, &a1, &a2, &a3, &a4, &kk, &nm, &sc, &a5, &part, &b0, &b1, &b2};
     launch((const void*)fn, (unsigned)nb0, (unsigned)(64 * sh.w), lds, st, args);
     return status_of(hipGetLastError());
 }

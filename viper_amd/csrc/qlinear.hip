@@ -65,30 +65,14 @@ static int scratch_address(void** out) {
 
 // ------------------------------------------------ standalone activation quantize
 
-// The K split's control words (ctl, offset 0 of the workspace): the quantize
-// launch that precedes the split launch on the stream clears the ncnt block
-// counters and increments the generation once per call (one thread), so the
-// split launch sees both.  Written through.
-__device__ __forceinline__ void reset_split_control(unsigned* ctl, int ncnt, int i0, int stride) {
-    const auto cw = buf(ctl + RC_CTL_CNT, (uint32_t)ncnt * 4u);
-    for (int i = i0; i < ncnt; i += stride) bstore4<AUX_SC1>(cw, i * 4, 0u);
-    if (ncnt > 0 && i0 == 0) {
-        const unsigned v = __hip_atomic_load(ctl + RC_CTL_GEN, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(ctl + RC_CTL_GEN, v + 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
 // MF: the fragment order the matrix-core kernels read (xs transposed to
 // [K/G][16]; 64-groups use quantize_frag64_kernel); else xq [M][K] in k order
 // and xs [M][K/G].
-// Both fragment-order quantizers also reset the control words of a K-split
-// matrix-core launch that follows (ncnt > 0).
 template <int G, bool MF>
 __global__ void __launch_bounds__(NT)
 quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
-                    float* __restrict__ xs, int oct_total, int K, unsigned* __restrict__ ctl, int ncnt) {
+                    float* __restrict__ xs, int oct_total, int K) {
     const int o = (int)blockIdx.x * NT + (int)threadIdx.x;
-    if constexpr (MF) reset_split_control(ctl, ncnt, o, (oct_total + NT - 1) / NT * NT);
     const bool ok = o < oct_total;
     u32x4 v = {0u, 0u, 0u, 0u};
     if (ok) v = *(const u32x4*)(x + (size_t)o * 8);
@@ -124,10 +108,8 @@ quantize_act_kernel(const uint16_t* x, int8_t* __restrict__ xq,
 // group amax is the max over the 4 lanes of row m (lanes m, m + 16, m + 32,
 // m + 48).  Rows m >= M are neither read nor written.
 __global__ void __launch_bounds__(64)
-quantize_frag64_kernel(const uint16_t* x, int M, int K, int8_t* __restrict__ xq, float* __restrict__ xs,
-                       unsigned* __restrict__ ctl, int ncnt) {
+quantize_frag64_kernel(const uint16_t* x, int M, int K, int8_t* __restrict__ xq, float* __restrict__ xs) {
     const int L = (int)threadIdx.x, g = (int)blockIdx.x;
-    reset_split_control(ctl, ncnt, g * 64 + L, K);  // K threads in the grid
     const int m = L & 15, kb = L >> 4, qi = ((kb & 1) << 1) | (kb >> 1);
     const bool ok = m < M;
     const auto xr = buf(x, (uint32_t)M * (uint32_t)K * 2u);
@@ -205,20 +187,18 @@ __global__ void __launch_bounds__(NT) check_quantizer_kernel(int ab0, int32_t* _
     if (threadIdx.x == 0) counts[blockIdx.x] = red[0];
 }
 
-static int launch_quantize(int group, const void* x, int M, int K, void* xq, void* xs, bool mf,
-                           hipStream_t st, unsigned* ctl = nullptr, int ncnt = 0) {
+static int launch_quantize(int group, const void* x, int M, int K, void* xq, void* xs, bool mf, hipStream_t st) {
     const int oct_total = M * K / 8;
     const unsigned grid = (unsigned)((oct_total + NT - 1) / NT);
     const uint16_t* a0 = (const uint16_t*)x;
     int8_t* a1 = (int8_t*)xq;
     float* a2 = (float*)xs;
-    if (ncnt > 0 && !mf) return VIPER_INTERNAL;
     if (mf && group == 64) {
-        void* fargs[] = {&a0, &M, &K, &a1, &a2, &ctl, &ncnt};
+        void* fargs[] = {&a0, &M, &K, &a1, &a2};
         launch((const void*)quantize_frag64_kernel, (unsigned)(K / 64), 64, 0, st, fargs);
         return status_of(hipGetLastError());
     }
-    void* args[] = {&a0, &a1, &a2, (void*)&oct_total, &K, &ctl, &ncnt};
+    void* args[] = {&a0, &a1, &a2, (void*)&oct_total, &K};
     const void* fn;
     if (group == 64) fn = (const void*)quantize_act_kernel<64, false>;
     else fn = mf ? (const void*)quantize_act_kernel<32, true> : (const void*)quantize_act_kernel<32, false>;
@@ -233,31 +213,41 @@ static bool fused_ok(int qtype, int M, int K) {
 }
 
 // Workspace of a call with M > 1 (zero-filled before its first use): the
-// K split's control words at offset 0 for every shape (generation, missed
-// sums; 16 bytes, room up to byte 256 for the split), its block counters from
-// byte 256, then xq ([M][K], or fragment order with room for 16 rows), xs
-// ([M][K/G], or [K/G][16]) fp32 and (long K on the matrix cores) the K
-// split's part sums.  Offsets in bytes.
+// K split's control words and block counters at offset 0 for every shape
+// (RC_CTL_BYTES: the missed-sum count, then RC_CNT_MAX counters from byte
+// 256), then (long K on the matrix cores) the K split's records of part sums,
+// one per row block at the same offset for every shape, then xq ([M][K], or
+// fragment order with room for 16 rows) and xs ([M][K/G], or [K/G][16])
+// fp32.  Offsets in bytes.
 struct WsLayout {
-    size_t cnt, xq, xs, sp, total;
-    bool split;
+    size_t cnt, sp, xq, xs, total;
+    int blocks;  // row blocks of the K split (0: no split)
 };
-constexpr size_t WS_CTL_BYTES = 16;
 static size_t workspace_xq(int K) { return align16((size_t)16 * K); }
 static size_t workspace_xs(int qtype, int K) { return align16((size_t)(K / group_of(qtype)) * 16 * 4); }
+static size_t split_record_bytes(int blocks) { return (size_t)blocks * RC_REC_SLOTS * 8; }
 
 static WsLayout workspace_layout(int qtype, int N, int K, int M) {
-    WsLayout l{0, 0, 0, 0, 0, false};
+    WsLayout l{0, 0, 0, 0, 0, 0};
     const int G = group_of(qtype);
     if (G == 0 || M <= 0 || K <= 0 || N <= 0 || K % G != 0) return l;
     if (fused_ok(qtype, M, K)) return l;
-    l.split = M >= 2 && M <= 16 && rc_split_ok(qtype, K);
+    l.blocks = M >= 2 && M <= 16 ? rc_split_blocks(qtype, N, K) : 0;
     l.cnt = (size_t)RC_CTL_CNT * 4;
-    l.xq = l.split ? l.cnt + align16((size_t)rc_split_counters(N) * 4) : WS_CTL_BYTES;
+    l.sp = RC_CTL_BYTES;
+    l.xq = l.sp + split_record_bytes(l.blocks);
     l.xs = l.xq + workspace_xq(K);
-    l.sp = l.xs + workspace_xs(qtype, K);
-    l.total = l.sp + (l.split ? rc_split_bytes(N, M) : 0);
+    l.total = l.xs + workspace_xs(qtype, K);
     return l;
+}
+
+// Workspace of the fragment-input entry points: the control words and, for
+// long K, the K split's records (0: the launch needs none).
+static size_t frag_workspace_need(int qtype, int N, int K, int M) {
+    const int G = group_of(qtype);
+    if (G == 0 || M < 2 || M > 16 || N <= 0 || K <= 0 || K % G != 0) return 0;
+    const int blocks = rc_split_blocks(qtype, N, K);
+    return blocks > 0 ? RC_CTL_BYTES + split_record_bytes(blocks) : 0;
 }
 
 static size_t workspace_need(int qtype, int N, int K, int M) { return workspace_layout(qtype, N, K, M).total; }
@@ -307,9 +297,12 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
         const M1Out outs[1] = {{w, s, y, N}};
         return launch_m1(qtype, senc, K, PRO_BF16, x, nullptr, 0.0f, nullptr, outs, 1, res, part, st, M);
     }
-    // (long K splits over workgroups in the two-launch path instead: down
-    // shape K = 10240, 4 rows 9.5 us against 10.3 us)
-    const bool split_ok = mf && b.w == nullptr && rc_split_ok(qtype, K);
+    // Long K splits over workgroups in the two-launch path (down shape
+    // K = 10240, 4 rows 9.5 us against 10.3 us without the split).  (Every
+    // workgroup quantizing the bf16 rows of its own part of K, in one launch,
+    // measured slower at every row count: down shape 3 / 8 / 16 rows 10.4 /
+    // 12.6 / 15.9 us against 8.4 / 9.4 / 9.8 us.)
+    const bool split_ok = mf && b.w == nullptr && rc_split_blocks(qtype, N, K) > 0;
     // Q5/Q6/W8 (K = 2560, N = 10240, 5% outlier channels): 3 or 4 rows of one
     // matrix run faster on the multi-row dot kernel below (Q5 4 rows 7.86
     // against 8.10 us; W8 3 / 4 rows 7.47 / 7.77 against 8.9 / 9.17 us); 5-8
@@ -341,15 +334,15 @@ static int qlinear_common(int qtype, const void* w, const void* s, int senc, int
     const bool staged = mf && mfma_staged(qtype, N, K);
     if (!mf && lds_pre(qtype, M, K) > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
     const WsLayout lay = workspace_layout(qtype, N, K, M);
-    if (split_ok && !lay.split) return VIPER_INTERNAL;
+    if (split_ok && lay.blocks == 0) return VIPER_INTERNAL;
     uint8_t* xq = (uint8_t*)wsp + lay.xq;
     float* xs = (float*)((uint8_t*)wsp + lay.xs);
-    // long K on the matrix cores: the K split (control words at the
-    // workspace's start, part sums after xs)
+    // long K on the matrix cores: the K split (control words and counters at
+    // the workspace's start, then the records of part sums)
     const bool split = split_ok;
     uint64_t* sp = split ? (uint64_t*)((uint8_t*)wsp + lay.sp) : nullptr;
     unsigned* sc = split ? (unsigned*)wsp : nullptr;
-    rc = launch_quantize(group, x, M, K, xq, xs, staged, st, sc, split ? rc_split_counters(N) : 0);
+    rc = launch_quantize(group, x, M, K, xq, xs, staged, st);
     if (rc != VIPER_OK) return rc;
     if (mf)
         return launch_mfma(qtype, w, s, senc, N, K, xq, xs, !staged, M, y, res, part, b.w, b.s, b.y,
@@ -388,12 +381,13 @@ static int prequant_common(int qtype, const void* w, const void* s, int senc, in
 }
 
 // 2..16 int8 rows already in the matrix-core fragment order (a producer's
-// fragment output): one launch of the row-contiguous matrix-core kernel, no
-// workspace (long K runs its segment loop rather than the K split, whose
-// control words a preceding launch would have to reset).
+// fragment output): one launch of the row-contiguous matrix-core kernel.  Long
+// K splits over workgroups when a workspace of frag_workspace_need bytes is
+// given (no launch before it: the split keeps its own counters), else runs
+// the segment loop.
 static int prequant_frag(int qtype, const void* w, const void* s, int senc, int group, int N, int K,
-                         const void* xf, const void* xsf, int M, void* y, const void* res, void* stream,
-                         Second b = Second()) {
+                         const void* xf, const void* xsf, int M, void* y, const void* res, void* wsp,
+                         size_t wsp_bytes, void* stream, Second b = Second()) {
     int rc = validate_weights(qtype, w, s, senc, group, N, K, M);
     if (rc != VIPER_OK) return rc;
     if (xf == nullptr || xsf == nullptr || y == nullptr || M < 2 || !rc_ok(qtype, K)) return VIPER_INVALID_ARGUMENT;
@@ -401,8 +395,14 @@ static int prequant_frag(int qtype, const void* w, const void* s, int senc, int 
         return VIPER_INVALID_ARGUMENT;
     rc = validate_second(b, qtype, senc, group, N, K, M, res, nullptr);
     if (rc != VIPER_OK) return rc;
+    if (wsp != nullptr && misaligned(wsp, 16)) return VIPER_INVALID_ARGUMENT;
+    const size_t need = b.w == nullptr ? frag_workspace_need(qtype, N, K, M) : 0;
+    if (wsp != nullptr && need > 0 && wsp_bytes < need) return VIPER_INVALID_ARGUMENT;
+    const bool split = wsp != nullptr && need > 0;
+    uint64_t* sp = split ? (uint64_t*)((uint8_t*)wsp + RC_CTL_BYTES) : nullptr;
+    unsigned* sc = split ? (unsigned*)wsp : nullptr;
     return launch_rc(qtype, w, s, senc, N, K, xf, xsf, RC_FRAG, M, y, res, nullptr, b.w, b.s, b.y,
-                     (hipStream_t)stream);
+                     (hipStream_t)stream, sp, sc);
 }
 
 }  // namespace vq
@@ -420,14 +420,18 @@ extern "C" size_t viper_hip_qlinear_workspace_bytes(int qtype, int N, int K, int
 extern "C" size_t viper_hip_qlinear_workspace_layout(int qtype, int N, int K, int M, size_t* offsets) {
     const vq::WsLayout l = vq::workspace_layout(qtype, N, K, M);
     if (offsets != nullptr) {
-        offsets[0] = (size_t)vq::RC_CTL_GEN * 4;
-        offsets[1] = (size_t)vq::RC_CTL_MISS * 4;
-        offsets[2] = l.split ? l.cnt : SIZE_MAX;
+        offsets[0] = l.total ? (size_t)vq::RC_CTL_MISS * 4 : SIZE_MAX;
+        offsets[1] = l.total ? l.cnt : SIZE_MAX;
+        offsets[2] = l.blocks ? l.sp : SIZE_MAX;
         offsets[3] = l.total ? l.xq : SIZE_MAX;
         offsets[4] = l.total ? l.xs : SIZE_MAX;
-        offsets[5] = l.split ? l.sp : SIZE_MAX;
+        offsets[5] = (size_t)l.blocks;
     }
     return l.total;
+}
+
+extern "C" size_t viper_hip_qlinear_frag_workspace_bytes(int qtype, int N, int K, int M) {
+    return vq::frag_workspace_need(qtype, N, K, M);
 }
 
 extern "C" int viper_hip_qlinear(int qtype, const void* w_packed, const void* w_scales,
@@ -508,9 +512,10 @@ extern "C" int viper_hip_qlinear_fused2_prequantized(int qtype, const void* w0_p
 extern "C" int viper_hip_qlinear_prequantized_frag(int qtype, const void* w_packed, const void* w_scales,
                                                    int scale_enc, int group, int N, int K, const void* xfrag,
                                                    const void* xsfrag, int M, void* y_bf16,
-                                                   const void* residual_bf16, void* stream) {
+                                                   const void* residual_bf16, void* workspace, size_t workspace_bytes,
+                                                   void* stream) {
     return vq::prequant_frag(qtype, w_packed, w_scales, scale_enc, group, N, K, xfrag, xsfrag, M, y_bf16,
-                             residual_bf16, stream);
+                             residual_bf16, workspace, workspace_bytes, stream);
 }
 
 extern "C" int viper_hip_qlinear_fused2_prequantized_frag(int qtype, const void* w0_packed,
@@ -520,7 +525,7 @@ extern "C" int viper_hip_qlinear_fused2_prequantized_frag(int qtype, const void*
                                                           int M, void* y0_bf16, void* y1_bf16, void* stream) {
     if (w1_packed == nullptr || w1_scales == nullptr || y1_bf16 == nullptr) return VIPER_INVALID_ARGUMENT;
     return vq::prequant_frag(qtype, w0_packed, w0_scales, scale_enc, group, N, K, xfrag, xsfrag, M, y0_bf16,
-                             nullptr, stream, vq::Second{w1_packed, w1_scales, y1_bf16});
+                             nullptr, nullptr, 0, stream, vq::Second{w1_packed, w1_scales, y1_bf16});
 }
 
 extern "C" int viper_hip_qlinear_frag_timeline(int qtype, const void* w_packed, const void* w_scales, int scale_enc,

@@ -127,26 +127,34 @@ bool mfma_ok(int qtype, int K, int M, const void* s);
 enum { RC_FRAG = 0, RC_NAT = 1, RC_BF16 = 2 };
 bool rc_ok(int qtype, int K);
 bool rc_bf16_ok(int qtype, int N, int K, int M, bool pair);
-// K split of the fragment-input launch (long K): sp = the parts' sums
-// [4][M][N] as 64-bit {tag, fp32} slots; sc = the workspace's control words
-// (at offset 0 of every workspace): sc[RC_CTL_GEN] the generation (one per
-// call), sc[RC_CTL_MISS] the count of sums that never arrived (outputs NaN;
-// never cleared by the library), then from sc[RC_CTL_CNT] one counter per row
-// block (rc_split_counters(N) of them, zero when the launch starts).  The
-// fragment quantize launch clears the counters and increments the
-// generation.  rc_split_bytes(N, M): the sums' bytes.
-constexpr int RC_SK = 4;  // parts of the K split
-// The counters start a cache line of their own (byte 256): with them in the
-// generation word's line, every part's counter update made the other parts'
-// generation reads miss (down shape, 8 rows: 8.94 -> 9.8 us).
-constexpr int RC_CTL_GEN = 0, RC_CTL_MISS = 1, RC_CTL_CNT = 64;
+// K split of the fragment-input launch (long K): K in sk parts (2..RC_SK_MAX),
+// one workgroup per (row block, part).  sc = the workspace's control words
+// (offset 0 of every M > 1 workspace): sc[RC_CTL_MISS] counts sums that never
+// arrived (their outputs are NaN; the library never clears it), and from
+// sc[RC_CTL_CNT] one counter per row block (RC_CNT_MAX of them, reserved in
+// every M > 1 layout so no other data lands there).  A counter holds
+// 64 * epoch + the parts of the running call that have counted; the last part
+// of a call (it counts sk - 1) adds 64 - sk, so every call starts on a
+// multiple of 64 and the block's epoch (counter >> 6) grows by one per call.
+// sp = the parts' sums as 64-bit {tag, fp32} slots in one record per row
+// block (RC_REC_SLOTS slots at sp + block * RC_REC_SLOTS, the same place for
+// every shape): a slot position is only ever written by its block, with the
+// tag of that block's epoch.
+constexpr int RC_SK_MAX = 8;      // parts of the K split
+constexpr int RC_REC_ROWS = 48;   // rows of a row block (8 * rb, rb <= 6)
+constexpr int RC_REC_SLOTS = RC_SK_MAX * VIPER_QLINEAR_MAX_M * RC_REC_ROWS;
+constexpr int RC_CNT_MAX = 1024;  // row blocks a split launch may have
+// Control words: the counters start a cache line of their own (byte 256).
+constexpr int RC_CTL_MISS = 1, RC_CTL_CNT = 64;
+constexpr size_t RC_CTL_BYTES = (size_t)RC_CTL_CNT * 4 + (size_t)RC_CNT_MAX * 4;
 // The tag a call's slots carry: top byte 0x80 (no int8 activation byte, fp32
 // activation scale or counter the workspace holds can have it), then the
-// generation's low 24 bits.
-__host__ __device__ constexpr unsigned rc_tag(unsigned gen) { return 0x80000000u | (gen & 0x00FFFFFFu); }
-bool rc_split_ok(int qtype, int K);
-inline int rc_split_counters(int N) { return (N + 7) / 8; }
-size_t rc_split_bytes(int N, int M);
+// block's epoch, low 24 bits.
+__host__ __device__ constexpr unsigned rc_tag(unsigned epoch) { return 0x80000000u | (epoch & 0x00FFFFFFu); }
+// Split shape of a fragment-input launch (rows of both matrices, K): its row
+// blocks (0 when K does not split); the sums' record bytes are
+// blocks * RC_REC_SLOTS * 8.
+int rc_split_blocks(int qtype, int N, int K);
 int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq, const void* xs,
               int am, int M, void* y, const void* res, int32_t* part, const void* w1, const void* s1, void* y1,
               hipStream_t st, uint64_t* sp = nullptr, unsigned* sc = nullptr);

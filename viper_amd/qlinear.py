@@ -136,10 +136,12 @@ _SYMBOLS = (
     "viper_hip_qlinear_timeline",
     "viper_hip_check_bf16_rounding",
     "viper_hip_clock_stamp",
+    "viper_hip_empty_dispatch",
     "viper_hip_prefetch",
     "viper_hip_rmsnorm_quantize_frag",
     "viper_hip_swiglu_quantize_frag",
     "viper_hip_qlinear_prequantized_frag",
+    "viper_hip_qlinear_frag_workspace_bytes",
     "viper_hip_qlinear_fused2_prequantized_frag",
     "viper_hip_qlinear_frag_timeline",
 )
@@ -182,14 +184,19 @@ def lib():
     L.viper_hip_stream_read.restype = i32
     L.viper_hip_clock_stamp.argtypes = [vp, vp]
     L.viper_hip_clock_stamp.restype = i32
+    L.viper_hip_empty_dispatch.argtypes = [i32, i32, vp, vp]
+    L.viper_hip_empty_dispatch.restype = i32
     L.viper_hip_prefetch.argtypes = [vp, sz, i32, vp, vp]
     L.viper_hip_prefetch.restype = i32
     L.viper_hip_rmsnorm_quantize_frag.argtypes = [vp, vp, C.c_float, i32, i32, i32, vp, vp, vp, vp]
     L.viper_hip_rmsnorm_quantize_frag.restype = i32
     L.viper_hip_swiglu_quantize_frag.argtypes = [vp, vp, i32, i32, i32, vp, vp, vp, vp]
     L.viper_hip_swiglu_quantize_frag.restype = i32
-    L.viper_hip_qlinear_prequantized_frag.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp]
+    L.viper_hip_qlinear_prequantized_frag.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, vp, sz,
+                                                      vp]
     L.viper_hip_qlinear_prequantized_frag.restype = i32
+    L.viper_hip_qlinear_frag_workspace_bytes.argtypes = [i32, i32, i32, i32]
+    L.viper_hip_qlinear_frag_workspace_bytes.restype = sz
     L.viper_hip_qlinear_fused2_prequantized_frag.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, vp, i32,
                                                              vp, vp, vp]
     L.viper_hip_qlinear_fused2_prequantized_frag.restype = i32
@@ -263,19 +270,25 @@ def workspace_bytes(qtype, N, K, M) -> int:
     return int(lib().viper_hip_qlinear_workspace_bytes(int(qtype), N, K, M))
 
 
-WS_PARTS = ("generation", "missed", "counters", "xq", "xs", "sums")
+WS_PARTS = ("missed", "counters", "sums", "xq", "xs", "split_blocks")
 
 
 def workspace_layout(qtype, N, K, M) -> dict:
     """Byte offsets of the workspace's parts for this shape (None where the shape has none) and its
-    total size: the K split's generation word and missed-sum count (offsets 0 and 4 for every shape),
-    its block counters, xq, xs and the K split's part sums."""
+    total size: the K split's missed-sum count (offset 4) and block counters (from 256) for every M > 1
+    shape, the K split's records of part sums (from 4352), xq and xs; split_blocks is the K split's
+    count of row blocks (0 without it)."""
     off = (C.c_size_t * 6)()
     total = int(lib().viper_hip_qlinear_workspace_layout(int(qtype), N, K, M, C.cast(off, C.c_void_p)))
     none = (1 << (8 * C.sizeof(C.c_size_t))) - 1
     out = {k: (None if int(v) == none else int(v)) for k, v in zip(WS_PARTS, off)}
     out["total"] = total
     return out
+
+
+def frag_workspace_bytes(qtype, N, K, M) -> int:
+    """Bytes of workspace the fragment-input entry splits long K with (0: the shape needs none)."""
+    return int(lib().viper_hip_qlinear_frag_workspace_bytes(int(qtype), N, K, M))
 
 
 def qlinear_raw(qtype, w, s, scale_enc, group, N, K, x, M, y, residual=None, workspace=None,
@@ -407,13 +420,16 @@ def swiglu_quantize_frag(gate, up, group, xfrag, xsfrag, out=None, stream=None) 
     return _status(rc, "viper_hip_swiglu_quantize_frag")
 
 
-def linear_prequantized_frag(w: QuantizedWeight, xfrag, xsfrag, y, residual=None, stream=None) -> Status:
-    """y [M, N] (M = 2..16) from int8 rows in fragment order (rmsnorm/swiglu_quantize_frag)."""
+def linear_prequantized_frag(w: QuantizedWeight, xfrag, xsfrag, y, residual=None, workspace=None,
+                             stream=None) -> Status:
+    """y [M, N] (M = 2..16) from int8 rows in fragment order (rmsnorm/swiglu_quantize_frag); with a
+    workspace of frag_workspace_bytes (zero-filled before its first use) long K splits over workgroups."""
     K, N = w.cols, w.rows
     M = int(y.numel() // N)
+    nws = 0 if workspace is None else int(workspace.numel() * workspace.element_size())
     rc = lib().viper_hip_qlinear_prequantized_frag(int(w.qtype), ptr(w.data, 1), ptr(w.scales, 2), int(w.scale_enc),
                                                    w.group_size, N, K, ptr(xfrag, 1), ptr(xsfrag, 4), M, ptr(y, 2),
-                                                   ptr(residual, 2), _stream(stream))
+                                                   ptr(residual, 2), ptr(workspace, 1), nws, _stream(stream))
     return _status(rc, "viper_hip_qlinear_prequantized_frag")
 
 
