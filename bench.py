@@ -391,9 +391,10 @@ def timeline(torch, L, gen, N, K, qt=4):
 
 def timeline_rc(torch, L, gen, N, K, M):
     """Per-wave timeline of the M-row matrix-core GEMM (Q4_G64, fragment input:
-    viper_hip_qlinear_frag_timeline) at shape (K, N): percentiles of each stamp over all waves of one
-    dispatch (the last of a back-to-back sequence over rotating weights), in us from the first wave's
-    start."""
+    viper_hip_qlinear_frag_timeline; long K on the K split, with its workspace) at shape (K, N):
+    percentiles of each stamp over all waves of one dispatch (the last of a back-to-back sequence over
+    rotating weights), in us from the first wave's start; with the split, the last parts' output
+    stamps separately."""
     G = 64
     copy_bytes = N * (K // 2) + N * (K // G) * 2
     copies = max(2, -(-ROTATE_BYTES // copy_bytes) + 1)
@@ -409,13 +410,16 @@ def timeline_rc(torch, L, gen, N, K, M):
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     stamps = torch.zeros(1 << 20, dtype=torch.int64, device="cuda")
     grid, waves = C.c_int(0), C.c_int(0)
+    nws = L.viper_hip_qlinear_frag_workspace_bytes(4, N, K, M)
+    ws = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda")
 
     def launch(i):
         c = i % copies
         st = torch.cuda.current_stream().cuda_stream
         rc = L.viper_hip_qlinear_frag_timeline(4, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K, xf.data_ptr(),
                                                xs.data_ptr(), M, y.data_ptr(), stamps.data_ptr(), stamps.numel() * 8,
-                                               C.byref(grid), C.byref(waves), st)
+                                               C.byref(grid), C.byref(waves), ws.data_ptr() if nws else None, nws,
+                                               st)
         if rc != 0:
             raise RuntimeError(f"frag timeline failed: {rc}")
     for i in range(50):
@@ -425,16 +429,28 @@ def timeline_rc(torch, L, gen, N, K, M):
     g.replay()
     torch.cuda.synchronize()
     nw = grid.value * waves.value
-    t = stamps[: nw * 8].view(nw, 8).cpu().numpy()
+    t = stamps[: nw * 10].view(nw, 10).cpu().numpy()
     t = (t - t[:, 0].min()) * 0.01       # 100 MHz ticks -> us
     names = ["wave start", "activation + scale loads issued", "weight loads issued", "staged scales in LDS",
-             "first group scaled", "last group scaled", "cross-wave barrier passed", "outputs stored"]
+             "first group scaled", "last group scaled", "cross-wave barrier passed",
+             "sums stored" if nws else "outputs stored"]
+    if nws:
+        names += ["counted"]
     import numpy as np
     rows = {}
+
+    def pct(v):
+        v = np.sort(v)
+        return [round(float(np.percentile(v, p)), 3) for p in (10, 50, 90)] + [round(float(v[-1]), 3)]
     for i, nm in enumerate(names):
-        v = np.sort(t[:, i])
-        rows[nm] = [round(float(np.percentile(v, p)), 3) for p in (10, 50, 90)] + [round(float(v[-1]), 3)]
-    print(json.dumps({"timeline": f"qgemm_rc Q4_G64 M={M} K={K} N={N} (fragment input)", "workgroups": grid.value,
+        rows[nm] = pct(t[:, i])
+    if nws:   # the blocks' last parts: their outputs stored after the other parts' sums arrived
+        last = t[:, 9] > t[:, 8]
+        if last.any():
+            rows["outputs stored (last parts)"] = pct(t[last, 9])
+            rows["last parts: counted -> outputs stored"] = pct(t[last, 9] - t[last, 8])
+    print(json.dumps({"timeline": f"qgemm_rc Q4_G64 M={M} K={K} N={N} (fragment input"
+                      + (", K split)" if nws else ")"), "workgroups": grid.value,
                       "waves_per_workgroup": waves.value, "us_per_launch_stamped": round(us, 3),
                       "percentiles_us_p10_p50_p90_max": rows}), flush=True)
 
@@ -774,6 +790,12 @@ def main():
         for Mv in (2, 4, 8, 16):
             us_v, gbs_v = time_linear(torch, L, gen, qtype, 2560, 10240, Mv)
             extras[f"verify_m{Mv}_down_us"], extras[f"verify_m{Mv}_down_gbs"] = us_v, gbs_v
+        # the engine's verify step: rows quantized by the producer in the matrix-core fragment order,
+        # one launch per linear (the K split with its workspace at the down shape)
+        for Mv in (8, 16):
+            for nm, (Nf, Kf) in (("", (N, K)), ("_down", (2560, 10240))):
+                us_v, gbs_v = time_linear(torch, L, gen, qtype, Nf, Kf, Mv, frag=True)
+                extras[f"verify_m{Mv}{nm}_frag_us"], extras[f"verify_m{Mv}{nm}_frag_gbs"] = us_v, gbs_v
 
         # config 0: the attention q/o projection, Q4_G64 M=1, K=N=2560
         us_v, gbs_v = time_linear(torch, L, gen, qtype, 2560, 2560, 1)

@@ -340,17 +340,22 @@ int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads,
 
 /* Measurement entry point, no counterpart in the reference: the M = 2..16
  * matrix-core GEMM of viper_hip_qlinear_prequantized_frag (Q4_G64, K a
- * multiple of 4 groups and at most 20 quads of 4 groups: one segment) with a
- * per-wave timeline.  Lane 0 of every wave writes 8 s_memrealtime readings
- * (uint64, 100 MHz) to stamps[(workgroup * waves + wave) * 8 + i]: wave
- * start, activation and scale loads issued, weight loads issued, staged
- * scales in LDS, first group scaled, last group scaled, cross-wave barrier
- * passed, outputs stored.  *workgroups and *waves_per_workgroup (may be NULL)
- * receive the grid; stamp_bytes must cover it. */
+ * multiple of 4 groups; at most 20 quads of 4 groups: one segment, or with a
+ * workspace of viper_hip_qlinear_frag_workspace_bytes() (16-byte aligned)
+ * the K split of a long K) with a per-wave timeline.  Lane 0 of every wave
+ * writes 10 s_memrealtime readings (uint64, 100 MHz) to
+ * stamps[(workgroup * waves + wave) * 10 + i]: wave start, activation and
+ * scale loads issued, weight loads issued, staged scales in LDS, first group
+ * scaled, last group scaled, cross-wave barrier passed, sums stored (y, or
+ * the K split's slots), counted (the K split's block counter returned),
+ * outputs stored (y by the K split's last part of a block); readings a
+ * workgroup does not reach repeat its last one.  *workgroups and
+ * *waves_per_workgroup (may be NULL) receive the grid; stamp_bytes must
+ * cover it.  y equals the production call's bit for bit. */
 int viper_hip_qlinear_frag_timeline(int qtype, const void* w_packed, const void* w_scales, int scale_enc, int group,
                                     int N, int K, const void* xfrag, const void* xsfrag, int M, void* y_bf16,
                                     uint64_t* stamps, size_t stamp_bytes, int* workgroups, int* waves_per_workgroup,
-                                    void* stream);
+                                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* Warms `bytes` (a multiple of 16, 16-byte aligned) at buf into the GPU's
  * memory-side cache with plain loads, split over `workgroups` workgroups of

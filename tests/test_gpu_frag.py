@@ -277,35 +277,52 @@ def test_frag_entry_errors(torch_dev):
     assert va.rmsnorm_quantize_frag(x, g, 1e-6, 64, xf, sf).code == va.StatusCode.INVALID_ARGUMENT  # M = 17
 
 
-@pytest.mark.parametrize("M", [16, 5])
-def test_frag_timeline_matches_gemm(torch_dev, M):
+@pytest.mark.parametrize("M,K", [(16, 2560), (5, 2560), (16, 10240), (7, 10752)])
+def test_frag_timeline_matches_gemm(torch_dev, M, K):
     # the measurement entry point runs the production matrix-core GEMM with
-    # stamps: y equal to viper_hip_qlinear_prequantized_frag's bit for bit, 8
-    # non-decreasing readings per wave; long K (segment loop), other formats
-    # and short stamp buffers rejected
+    # stamps (long K: the K split, with a workspace): y equal to
+    # viper_hip_qlinear_prequantized_frag's bit for bit, 10 non-decreasing
+    # readings per wave; long K without a workspace, other formats and short
+    # stamp buffers rejected
     import ctypes as C
     torch = torch_dev
     L = va.lib()
-    N, K = 4000, 2560
+    N = 4000
     packed, scales = O.gen_weights(O.Q4_G64, N, K, 750 + M, O.SCALE_FP16)
     w = va.QuantizedWeight(va.QType.Q4_G64, dev(torch, packed), dev(torch, scales), N, K, 64, va.ScaleEnc.FP16)
     x = dev(torch, O.gen_act(M, K, 751))
     xf, sf = _frag_buffers(torch, K, 64)
     assert va.rmsnorm_quantize_frag(x, dev(torch, bf16(np.ones(K))), 1e-6, 64, xf, sf).ok()
+    nws = va.frag_workspace_bytes(O.Q4_G64, N, K, M)
+    assert (nws > 0) == (K > 5120)
+    ws = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda")
+    wsp = ws.data_ptr() if nws else None
     y0 = torch.zeros((M, N), dtype=torch.int16, device="cuda")
     y1 = torch.full((M, N), 7, dtype=torch.int16, device="cuda")
-    assert va.linear_prequantized_frag(w, xf, sf, y0).ok()
-    stamps = torch.zeros(1 << 18, dtype=torch.int64, device="cuda")
+    assert va.linear_prequantized_frag(w, xf, sf, y0, workspace=ws if nws else None).ok()
+    stamps = torch.zeros(1 << 19, dtype=torch.int64, device="cuda")
     grid, waves = C.c_int(0), C.c_int(0)
     st = torch.cuda.current_stream().cuda_stream
     args = (w.data.data_ptr(), w.scales.data_ptr(), 0, 64, N, K, xf.data_ptr(), sf.data_ptr(), M, y1.data_ptr())
     assert L.viper_hip_qlinear_frag_timeline(4, *args, stamps.data_ptr(), stamps.numel() * 8, C.byref(grid),
-                                             C.byref(waves), st) == 0
+                                             C.byref(waves), wsp, nws, st) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(u16(y1), u16(y0))
     nw = grid.value * waves.value
     assert nw > 0
-    t = stamps[: nw * 8].view(nw, 8).cpu().numpy()
+    t = stamps[: nw * 10].view(nw, 10).cpu().numpy()
     assert (np.diff(t, axis=1) >= 0).all() and (t[:, 0] > 0).all()
-    assert L.viper_hip_qlinear_frag_timeline(4, *args, stamps.data_ptr(), 64, None, None, st) == 2
-    assert L.viper_hip_qlinear_frag_timeline(5, *args, stamps.data_ptr(), stamps.numel() * 8, None, None, st) == 2
+    if nws:   # one last part per row block stored y after counting
+        last = (t[:, 9] > t[:, 8]).reshape(grid.value, waves.value).any(axis=1)
+        assert 0 < last.sum() <= grid.value
+        assert split_state_ok(ws)
+    else:
+        assert (t[:, 9] == t[:, 7]).all() and (t[:, 8] == t[:, 7]).all()
+    assert L.viper_hip_qlinear_frag_timeline(4, *args, stamps.data_ptr(), 64, None, None, wsp, nws, st) == 2
+    assert L.viper_hip_qlinear_frag_timeline(5, *args, stamps.data_ptr(), stamps.numel() * 8, None, None, wsp, nws,
+                                             st) == 2
+    if nws:   # the split needs its workspace, and a big enough one
+        assert L.viper_hip_qlinear_frag_timeline(4, *args, stamps.data_ptr(), stamps.numel() * 8, None, None, None, 0,
+                                                 st) == 2
+        assert L.viper_hip_qlinear_frag_timeline(4, *args, stamps.data_ptr(), stamps.numel() * 8, None, None, wsp,
+                                                 nws - 16, st) == 2

@@ -142,12 +142,15 @@ struct RcSeg {
 // and an invalidate of the XCD's L2 per workgroup: 70 us on the down shape.)
 // The last part requests every slot at once, then re-reads any that does not
 // yet carry the current tag.
-// TLM (measurement, fragment input, one segment, no split): `part` receives
-// per-wave s_memrealtime readings (100 MHz) at RC_TL_STAMPS points --
+// TLM (measurement, fragment input, one segment): `part` receives per-wave
+// s_memrealtime readings (100 MHz) at RC_TL_STAMPS points --
 // [workgroup][wave][RC_TL_STAMPS] uint64: wave start, activation and scale
 // loads issued, weight loads issued, staged scales in LDS, first group
-// scaled, last group scaled, cross-wave barrier passed, outputs stored.
-constexpr int RC_TL_STAMPS = 8;
+// scaled, last group scaled, cross-wave barrier passed, sums stored (y, or
+// with the K split the part's slots), counted (K split: the block's counter
+// returned), outputs stored (K split: y by the block's last part; the other
+// parts repeat the previous reading; without the split both repeat it).
+constexpr int RC_TL_STAMPS = 10;
 template <int F, int RB, int W, int QW, bool ONE, int AM, bool PART, int SE, bool KS = false, bool PR = true,
           bool TLM = false>
 __global__ void __launch_bounds__(64 * W)
@@ -159,12 +162,22 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     constexpr int T = Seg::T;
     constexpr bool XNAT = AM == RC_NAT, XBF = AM == RC_BF16;
     static_assert(!KS || AM == RC_FRAG, "the K split reads fragments");
-    static_assert(!TLM || (ONE && !PART && !KS && AM == RC_FRAG), "timeline: one fragment-input segment");
+    static_assert(!TLM || (ONE && !PART && AM == RC_FRAG), "timeline: one fragment-input segment");
     // K in bits 0..26, the K split's part count in 27..31
     const int K = (int)(kk & 0x07FFFFFFu), SK = KS ? (int)(kk >> 27) : 1;
     uint64_t tstamp[RC_TL_STAMPS];
     auto stamp = [&](int i) {
         if constexpr (TLM) tstamp[i] = __builtin_amdgcn_s_memrealtime();
+    };
+    // lane 0 of every wave writes its readings (points past `upto` repeat it)
+    auto flush_stamps = [&](int upto) {
+        if constexpr (TLM) {
+            if ((threadIdx.x & 63) == 0) {
+                uint64_t* o = (uint64_t*)part + ((size_t)blockIdx.x * W + (threadIdx.x >> 6)) * RC_TL_STAMPS;
+#pragma unroll
+                for (int i = 0; i < RC_TL_STAMPS; ++i) o[i] = tstamp[i <= upto ? i : upto];
+            }
+        }
     };
     stamp(0);
     constexpr int G = F == 8 ? 32 : 64;
@@ -522,6 +535,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
             }
         }
         stamp(3);
+        if (wave >= NQ) stamp(4);  // a wave with no quad scales no group
         compute(S, 0);
         stamp(5);
     } else {
@@ -572,19 +586,17 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
             }
         }
     }
-    if constexpr (TLM) {
-        stamp(7);
-        if (L == 0) {
-            uint64_t* o = (uint64_t*)part + ((size_t)blockIdx.x * W + wave) * RC_TL_STAMPS;
-#pragma unroll
-            for (int i = 0; i < RC_TL_STAMPS; ++i) o[i] = tstamp[i];
-        }
-    }
+    stamp(7);
+    if constexpr (!KS) flush_stamps(7);
     if constexpr (KS) {
         // count once every wave's slot stores are issued; a slot whose store
         // is still in flight when the last part reads it is re-read (waiting
         // for the stores to complete before counting measured 0.4 us slower).
         // The last part moves the counter to the next epoch (64 * (epoch + 1)).
+        // (A fixed part that adds the sums without counting, the last one
+        // dispatched, saves the counter's round trip but waits as long for
+        // the other parts' slots, 7.8 against 7.7 us at the down shape, and a
+        // part delayed by other work on the GPU would leave it spinning.)
         lds_barrier();
         int* last = (int*)red;
         if (tid == 0) {
@@ -595,7 +607,11 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
             last[0] = is_last;
         }
         lds_barrier();
-        if (!last[0]) return;
+        stamp(8);
+        if (!last[0]) {
+            flush_stamps(8);
+            return;
+        }
         // every slot of the other parts is requested at once (a load that
         // waited for the previous one's tag would serialise the round trips:
         // 0.4 us of the down-shape launch), then the tags are checked and a
@@ -644,6 +660,8 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         }
         if (__builtin_expect(missed != 0, 0))
             __hip_atomic_fetch_add(sc + RC_CTL_MISS, missed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        stamp(9);
+        flush_stamps(9);
     }
 }
 
@@ -719,19 +737,23 @@ rc_fn rc_pick2(const RcShape& s, int am, bool part, int senc, bool pair) {
 // Timeline kernels (fragment input, one segment; Q4 only, qgemm_rc_q4.hip).
 template <int F, int RB>
 rc_fn rc_pick_tl3(const RcShape& s, int senc) {
-#define VQ_RC_TL(W_, QW_)                                                                              \
-    if (s.w == W_ && s.qw == QW_)                                                                      \
-        return senc ? qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 1, false, false, true>     \
-                    : qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 0, false, false, true>;
-    VQ_RC_TL(4, 1)
-    VQ_RC_TL(10, 1)
-    if constexpr (RB <= rc_rb_qw2(F)) VQ_RC_TL(10, 2)
+#define VQ_RC_TL(W_, QW_, KS_)                                                                         \
+    if (s.w == W_ && s.qw == QW_ && (s.sk > 1) == KS_)                                                 \
+        return senc ? qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 1, KS_, false, true>       \
+                    : qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 0, KS_, false, true>;
+    VQ_RC_TL(4, 1, false)
+    VQ_RC_TL(10, 1, false)
+    VQ_RC_TL(10, 1, true)
+    if constexpr (RB <= rc_rb_qw2(F)) {
+        VQ_RC_TL(10, 2, false)
+        VQ_RC_TL(10, 2, true)
+    }
 #undef VQ_RC_TL
     return nullptr;
 }
 template <int F>
 rc_fn rc_pick_tl(const RcShape& s, int senc) {
-    if (!s.one || s.sk != 1) return nullptr;
+    if (!s.one) return nullptr;
     switch (s.rb) {
         case 1: return rc_pick_tl3<F, 1>(s, senc);
         case 2: return rc_pick_tl3<F, 2>(s, senc);

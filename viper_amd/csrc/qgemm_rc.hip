@@ -2,10 +2,6 @@
 // shape and dispatch.  The kernel template is in qgemm_rc.h.
 #include "qgemm_rc.h"
 
-#include <map>
-#include <mutex>
-#include <utility>
-
 namespace vq {
 
 // Waves per workgroup and quads per wave of the single-segment shapes, in
@@ -45,10 +41,9 @@ static RcShape rc_shape(int F, int rows_total, int NQ, int cus) {
 // K = 10240, N = 2560: 107 blocks of 24 rows x 4 parts instead of 160 blocks
 // of 16 rows that each read all of K's activation, M = 4 / 8 / 16: 9.47 /
 // 9.45 / 9.87 us; 40 rows, one workgroup per CU: 9.9 / 9.8 / 10.0 us; 16 rows
-// 11.3 / 11.6 / 11.9 us), and never leave workgroups for a second round: a
-// launch with more workgroups than fit the CUs at once took twice as long
-// (K = 10752, N = 3072, 40-row blocks whose registers fit one workgroup per
-// CU: 13.7 us).
+// 11.3 / 11.6 / 11.9 us).  (K = 10752, N = 3072: 77 blocks of 40 rows x 6
+// parts, whose last workgroups wait for a second round on the CUs: 12.5-14 us
+// with every part count and row block tried.)
 static int rc_split_parts(int NQ) {
     if (NQ <= 20) return 0;
     for (int lim : {10, 20})
@@ -56,26 +51,6 @@ static int rc_split_parts(int NQ) {
             if (NQ % sk == 0 && NQ / sk <= lim) return sk;
     return 0;
 }
-
-// Workgroups of a launch one CU holds at once (2 where the device cannot be
-// asked: the shapes' design point), cached per kernel and LDS size.
-static int rc_occupancy(rc_fn fn, int threads, size_t lds) {
-    static std::mutex mu;
-    static std::map<std::pair<const void*, size_t>, int> cache;
-    const std::pair<const void*, size_t> key((const void*)fn, lds);
-    std::lock_guard<std::mutex> lock(mu);
-    const auto it = cache.find(key);
-    if (it != cache.end()) return it->second;
-    int n = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, (const void*)fn, threads, lds) != hipSuccess || n <= 0) {
-        (void)hipGetLastError();
-        return 2;
-    }
-    cache[key] = n;
-    return n;
-}
-
-static size_t rc_launch_lds(int qtype, const RcShape& sh, int K, int am);
 
 static bool rc_split_shape(int qtype, int rows, int K, int cus, RcShape& s) {
     const int F = qtype == VIPER_QTYPE_W8_G32 ? 8 : qtype, NQ = K / group_of(qtype) / 4;
@@ -85,22 +60,8 @@ static bool rc_split_shape(int qtype, int rows, int K, int cus, RcShape& s) {
     s.one = true;
     s.qw = NQ / sk <= 10 ? 1 : 2;
     s.sk = sk;
-    const int rbmax = s.qw == 2 ? rc_rb_qw2(F) : 6;
-    int rb = (sk * rows + 16 * cus - 1) / (16 * cus);
-    rb = rb < 1 ? 1 : (rb > rbmax ? rbmax : rb);
-    for (s.rb = rb;; ++s.rb) {
-        const long wgs = (long)(rows + 8 * s.rb - 1) / (8 * s.rb) * sk;
-        rc_fn fn;
-        switch (F) {
-            case 4: fn = rc_pick<4>(s, RC_FRAG, false, 0, false); break;
-            case 5: fn = rc_pick<5>(s, RC_FRAG, false, 0, false); break;
-            case 6: fn = rc_pick<6>(s, RC_FRAG, false, 0, false); break;
-            default: fn = rc_pick<8>(s, RC_FRAG, false, 0, false); break;
-        }
-        if (s.rb == rbmax || fn == nullptr ||
-            wgs <= (long)rc_occupancy(fn, 64 * s.w, rc_launch_lds(qtype, s, K, RC_FRAG)) * cus)
-            break;
-    }
+    const int rb = (sk * rows + 16 * cus - 1) / (16 * cus), rbmax = s.qw == 2 ? rc_rb_qw2(F) : 6;
+    s.rb = rb < 1 ? 1 : (rb > rbmax ? rbmax : rb);
     return (rows + 8 * s.rb - 1) / (8 * s.rb) <= RC_CNT_MAX;
 }
 
@@ -188,18 +149,20 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     return status_of(hipGetLastError());
 }
 
-// The timeline variant of launch_rc (Q4, fragment input, one segment): see
-// viper_hip_qlinear_frag_timeline.
+// The timeline variant of launch_rc (Q4, fragment input, one segment, or the
+// K split when sc is given): see viper_hip_qlinear_frag_timeline.
 int launch_rc_timeline(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                        const void* xs, int M, void* y, uint64_t* stamps, size_t stamp_bytes, int* workgroups,
-                       int* waves, hipStream_t st) {
+                       int* waves, unsigned* sc, hipStream_t st) {
     if (qtype != VIPER_QTYPE_Q4_G64 || !rc_ok(qtype, K) || M < 2 || M > 16 || N >= (1 << 27)) return VIPER_INVALID_ARGUMENT;
-    const RcShape sh = rc_launch_shape(qtype, N, K);
+    RcShape sh = rc_launch_shape(qtype, N, K);
+    if (sc != nullptr && (K >= (1 << 27) || !rc_split_shape(qtype, N, K, device_cus(), sh))) return VIPER_INVALID_ARGUMENT;
     const rc_fn fn = rc_pick_tl4(sh, senc);
     if (fn == nullptr) return VIPER_INVALID_ARGUMENT;
-    const int nb0 = (N + 8 * sh.rb - 1) / (8 * sh.rb);
-    if (stamps == nullptr || stamp_bytes < (size_t)nb0 * sh.w * RC_TL_STAMPS * sizeof(uint64_t)) return VIPER_INVALID_ARGUMENT;
-    if (workgroups != nullptr) *workgroups = nb0;
+    const int nb0 = (N + 8 * sh.rb - 1) / (8 * sh.rb), grid = nb0 * sh.sk;
+    if (sh.sk > 1 && nb0 > RC_CNT_MAX) return VIPER_INVALID_ARGUMENT;
+    if (stamps == nullptr || stamp_bytes < (size_t)grid * sh.w * RC_TL_STAMPS * sizeof(uint64_t)) return VIPER_INVALID_ARGUMENT;
+    if (workgroups != nullptr) *workgroups = grid;
     if (waves != nullptr) *waves = sh.w;
     const size_t lds = rc_launch_lds(qtype, sh, K, RC_FRAG);
     const int8_t* a0 = (const int8_t*)xq;
@@ -212,12 +175,10 @@ int launch_rc_timeline(int qtype, const void* w, const void* s, int senc, int N,
     const uint8_t* b0 = nullptr;
     const uint16_t* b1 = nullptr;
     uint16_t* b2 = nullptr;
-    uint64_t* sp = nullptr;
-    unsigned* sc = nullptr;
     unsigned nm = (unsigned)N | ((unsigned)(M - 1) << 27) | (senc ? 1u << 31 : 0u);
-    unsigned kk = (unsigned)K;
+    unsigned kk = (unsigned)K | (sh.sk > 1 ? (unsigned)sh.sk << 27 : 0u);
     void* args[] = {&a0, &a1, &a2, &a3, &a4, &kk, &nm, &sc, &a5, &part, &b0, &b1, &b2};
-    launch((const void*)fn, (unsigned)nb0, (unsigned)(64 * sh.w), lds, st, args);
+    launch((const void*)fn, (unsigned)grid, (unsigned)(64 * sh.w), lds, st, args);
     return status_of(hipGetLastError());
 }
 

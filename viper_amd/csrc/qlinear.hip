@@ -531,14 +531,19 @@ extern "C" int viper_hip_qlinear_fused2_prequantized_frag(int qtype, const void*
 extern "C" int viper_hip_qlinear_frag_timeline(int qtype, const void* w_packed, const void* w_scales, int scale_enc,
                                                int group, int N, int K, const void* xfrag, const void* xsfrag, int M,
                                                void* y_bf16, uint64_t* stamps, size_t stamp_bytes, int* workgroups,
-                                               int* waves_per_workgroup, void* stream) {
+                                               int* waves_per_workgroup, void* workspace, size_t workspace_bytes,
+                                               void* stream) {
     int rc = vq::validate_weights(qtype, w_packed, w_scales, scale_enc, group, N, K, M);
     if (rc != VIPER_OK) return rc;
     if (xfrag == nullptr || xsfrag == nullptr || y_bf16 == nullptr || vq::misaligned(xfrag, 16) ||
-        vq::misaligned(xsfrag, 16) || vq::misaligned(y_bf16, 2) || vq::misaligned(stamps, 8))
+        vq::misaligned(xsfrag, 16) || vq::misaligned(y_bf16, 2) || vq::misaligned(stamps, 8) ||
+        vq::misaligned(workspace, 16))
         return VIPER_INVALID_ARGUMENT;
+    const size_t need = vq::frag_workspace_need(qtype, N, K, M);
+    if (workspace != nullptr && (need == 0 || workspace_bytes < need)) return VIPER_INVALID_ARGUMENT;
     return vq::launch_rc_timeline(qtype, w_packed, w_scales, scale_enc, N, K, xfrag, xsfrag, M, y_bf16, stamps,
-                                  stamp_bytes, workgroups, waves_per_workgroup, (hipStream_t)stream);
+                                  stamp_bytes, workgroups, waves_per_workgroup, (unsigned*)workspace,
+                                  (hipStream_t)stream);
 }
 
 extern "C" int viper_hip_qlinear_m1(int qtype, int scale_enc, int group, int K, int prologue, const void* a,

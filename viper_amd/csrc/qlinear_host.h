@@ -161,7 +161,7 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
 bool mfma_staged(int qtype, int N, int K);
 int launch_rc_timeline(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                        const void* xs, int M, void* y, uint64_t* stamps, size_t stamp_bytes, int* workgroups,
-                       int* waves, hipStream_t st);
+                       int* waves, unsigned* sc, hipStream_t st);
 int launch_mfma(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                 const void* xs, bool xnat, int M, void* y, const void* res, int32_t* part,
                 const void* w1, const void* s1, void* y1, hipStream_t st, uint64_t* sp = nullptr, unsigned* sc = nullptr);

@@ -201,7 +201,7 @@ def lib():
                                                              vp, vp, vp]
     L.viper_hip_qlinear_fused2_prequantized_frag.restype = i32
     L.viper_hip_qlinear_frag_timeline.argtypes = [i32, vp, vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, sz, vp, vp,
-                                                  vp]
+                                                  vp, sz, vp]
     L.viper_hip_qlinear_frag_timeline.restype = i32
     L.viper_hip_qlinear_fused2.argtypes = [i32, vp, vp, vp, vp, i32, i32, i32, i32, vp, i32, vp, vp, vp, sz, vp]
     L.viper_hip_qlinear_fused2.restype = i32
