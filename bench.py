@@ -389,16 +389,17 @@ def timeline(torch, L, gen, N, K, qt=4):
                       "percentiles_us_p10_p50_p90_max": rows}), flush=True)
 
 
-def timeline_rc(torch, L, gen, N, K, M):
-    """Per-wave timeline of the M-row matrix-core GEMM (Q4_G64, fragment input:
+def timeline_rc(torch, L, gen, N, K, M, qt=4):
+    """Per-wave timeline of the M-row matrix-core GEMM (Q4_G64 or W8_G32 by qt, fragment input:
     viper_hip_qlinear_frag_timeline; long K on the K split, with its workspace) at shape (K, N):
     percentiles of each stamp over all waves of one dispatch (the last of a back-to-back sequence over
     rotating weights), in us from the first wave's start; with the split, the last parts' output
     stamps separately."""
-    G = 64
-    copy_bytes = N * (K // 2) + N * (K // G) * 2
+    G = GROUP[qt]
+    rb = ROW_BYTES[qt](K)
+    copy_bytes = N * rb + N * (K // G) * 2
     copies = max(2, -(-ROTATE_BYTES // copy_bytes) + 1)
-    W, S = make_weights(torch, copies, N, K, gen)
+    W, S = make_weights(torch, copies, N, K, gen, row_bytes=rb, G=G)
     x = torch.randn((M, K), device="cuda", generator=gen).to(torch.bfloat16)
     xf = torch.empty(16 * K, dtype=torch.int8, device="cuda")
     xs = torch.empty(16 * (K // G), dtype=torch.float32, device="cuda")
@@ -410,13 +411,13 @@ def timeline_rc(torch, L, gen, N, K, M):
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     stamps = torch.zeros(1 << 20, dtype=torch.int64, device="cuda")
     grid, waves = C.c_int(0), C.c_int(0)
-    nws = L.viper_hip_qlinear_frag_workspace_bytes(4, N, K, M)
+    nws = L.viper_hip_qlinear_frag_workspace_bytes(qt, N, K, M)
     ws = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda")
 
     def launch(i):
         c = i % copies
         st = torch.cuda.current_stream().cuda_stream
-        rc = L.viper_hip_qlinear_frag_timeline(4, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K, xf.data_ptr(),
+        rc = L.viper_hip_qlinear_frag_timeline(qt, W[c].data_ptr(), S[c].data_ptr(), 0, G, N, K, xf.data_ptr(),
                                                xs.data_ptr(), M, y.data_ptr(), stamps.data_ptr(), stamps.numel() * 8,
                                                C.byref(grid), C.byref(waves), ws.data_ptr() if nws else None, nws,
                                                st)
@@ -449,7 +450,7 @@ def timeline_rc(torch, L, gen, N, K, M):
         if last.any():
             rows["outputs stored (last parts)"] = pct(t[last, 9])
             rows["last parts: counted -> outputs stored"] = pct(t[last, 9] - t[last, 8])
-    print(json.dumps({"timeline": f"qgemm_rc Q4_G64 M={M} K={K} N={N} (fragment input"
+    print(json.dumps({"timeline": f"qgemm_rc {'W8_G32' if qt == 8 else 'Q4_G64'} M={M} K={K} N={N} (fragment input"
                       + (", K split)" if nws else ")"), "workgroups": grid.value,
                       "waves_per_workgroup": waves.value, "us_per_launch_stamped": round(us, 3),
                       "percentiles_us_p10_p50_p90_max": rows}), flush=True)
@@ -566,8 +567,8 @@ def main():
                     help="only the per-wave timeline of the M=1 GEMV at the north-star shape, Q4_G64 unless a "
                          "format is named (viper_hip_qlinear_timeline)")
     ap.add_argument("--timeline-rc", type=int, default=0, metavar="M",
-                    help="only the per-wave timeline of the M-row matrix-core GEMM (Q4_G64, fragment input) at "
-                         "the north-star shape (viper_hip_qlinear_frag_timeline)")
+                    help="only the per-wave timeline of the M-row matrix-core GEMM (Q4_G64, or W8_G32 with "
+                         "--timeline w8; fragment input) at the north-star shape (viper_hip_qlinear_frag_timeline)")
     ap.add_argument("--shape", type=int, nargs=2, default=None, metavar=("K", "N"),
                     help="with --timeline / --timeline-rc: another shape than the north star's")
     ap.add_argument("--only", default="", metavar="LINE",
@@ -666,7 +667,7 @@ def main():
         return
     if args.timeline_rc:
         Kt, Nt = (args.shape[0], args.shape[1]) if args.shape else (K, N)
-        timeline_rc(torch, L, gen, Nt, Kt, args.timeline_rc)
+        timeline_rc(torch, L, gen, Nt, Kt, args.timeline_rc, 8 if args.timeline == "w8" else 4)
         return
     if args.timeline:
         Kt, Nt = (args.shape[0], args.shape[1]) if args.shape else (K, N)

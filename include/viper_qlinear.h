@@ -339,8 +339,8 @@ int viper_hip_stream_read(const void* buf, size_t bytes, int threads, int loads,
                           void* y_bf16, uint32_t* sink, void* stream);
 
 /* Measurement entry point, no counterpart in the reference: the M = 2..16
- * matrix-core GEMM of viper_hip_qlinear_prequantized_frag (Q4_G64, K a
- * multiple of 4 groups; at most 20 quads of 4 groups: one segment, or with a
+ * matrix-core GEMM of viper_hip_qlinear_prequantized_frag (Q4_G64 or W8_G32,
+ * K a multiple of 4 groups; at most 20 quads of 4 groups: one segment, or with a
  * workspace of viper_hip_qlinear_frag_workspace_bytes() (16-byte aligned)
  * the K split of a long K) with a per-wave timeline.  Lane 0 of every wave
  * writes 10 s_memrealtime readings (uint64, 100 MHz) to

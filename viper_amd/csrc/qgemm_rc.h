@@ -765,6 +765,7 @@ rc_fn rc_pick_tl(const RcShape& s, int senc) {
     }
 }
 rc_fn rc_pick_tl4(const RcShape& s, int senc);
+rc_fn rc_pick_tl8(const RcShape& s, int senc);
 
 // Kernels of format F (each defined in its own translation unit).
 template <int F>

@@ -149,15 +149,17 @@ int launch_rc(int qtype, const void* w, const void* s, int senc, int N, int K, c
     return status_of(hipGetLastError());
 }
 
-// The timeline variant of launch_rc (Q4, fragment input, one segment, or the
+// The timeline variant of launch_rc (Q4 or W8, fragment input, one segment, or the
 // K split when sc is given): see viper_hip_qlinear_frag_timeline.
 int launch_rc_timeline(int qtype, const void* w, const void* s, int senc, int N, int K, const void* xq,
                        const void* xs, int M, void* y, uint64_t* stamps, size_t stamp_bytes, int* workgroups,
                        int* waves, unsigned* sc, hipStream_t st) {
-    if (qtype != VIPER_QTYPE_Q4_G64 || !rc_ok(qtype, K) || M < 2 || M > 16 || N >= (1 << 27)) return VIPER_INVALID_ARGUMENT;
+    if ((qtype != VIPER_QTYPE_Q4_G64 && qtype != VIPER_QTYPE_W8_G32) || !rc_ok(qtype, K) || M < 2 || M > 16 ||
+        N >= (1 << 27))
+        return VIPER_INVALID_ARGUMENT;
     RcShape sh = rc_launch_shape(qtype, N, K);
     if (sc != nullptr && (K >= (1 << 27) || !rc_split_shape(qtype, N, K, device_cus(), sh))) return VIPER_INVALID_ARGUMENT;
-    const rc_fn fn = rc_pick_tl4(sh, senc);
+    const rc_fn fn = qtype == VIPER_QTYPE_W8_G32 ? rc_pick_tl8(sh, senc) : rc_pick_tl4(sh, senc);
     if (fn == nullptr) return VIPER_INVALID_ARGUMENT;
     const int nb0 = (N + 8 * sh.rb - 1) / (8 * sh.rb), grid = nb0 * sh.sk;
     if (sh.sk > 1 && nb0 > RC_CNT_MAX) return VIPER_INVALID_ARGUMENT;

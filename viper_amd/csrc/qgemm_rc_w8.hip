@@ -4,5 +4,6 @@
 namespace vq {
 
 VQ_RC_PICK(8)
+rc_fn rc_pick_tl8(const RcShape& s, int senc) { return rc_pick_tl<8>(s, senc); }
 
 }  // namespace vq
