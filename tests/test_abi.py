@@ -54,9 +54,8 @@ def test_group_sizes_and_workspace():
     assert va.frag_workspace_bytes(4, 2560, 10240, 16) == CTL + 107 * REC
     assert va.frag_workspace_bytes(4, 10240, 2560, 16) == 0
     assert va.frag_workspace_bytes(4, 2560, 10240, 1) == 0
-    # K = 10752 (42 quads: 6 parts of 7), K = 6144 (24 quads: 3 parts of 8)
-    assert va.workspace_layout(4, 3072, 10752, 16)["split_blocks"] > 0
-    assert va.workspace_layout(4, 3072, 6144, 16)["split_blocks"] > 0
+    # K = 6144 (24 quads: 3 parts of 8, 128 blocks of 24 rows)
+    assert va.workspace_layout(4, 3072, 6144, 16)["split_blocks"] == 128
 
 
 def _split_shapes():

@@ -164,8 +164,9 @@ def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
 
 
 # Long K on the matrix cores (more than 20 quads of 4 groups) splits K in
-# 2..8 parts, one workgroup each; the last part of a row block to finish adds
-# the parts' sums in part order.  The workspace starts zeroed
+# 2..8 parts, one workgroup each, where the split kernel leaves room for two
+# workgroups per CU (else it loops over K); the last part of a row block to
+# finish adds the parts' sums in part order.  The workspace starts zeroed
 # (the contract) and serves a second call with another row count; a repeated
 # call must give the same bits.
 @pytest.mark.parametrize("qtype", FORMATS)
@@ -175,8 +176,8 @@ def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
     (1000, 6144, 12, 2, O.SCALE_FP16),    # 6 quads per part; M2 = 2 on the dot path
     (333, 12288, 9, 16, O.SCALE_BF16),    # 6 parts of 8 quads (W8: 8 parts of 12, two quads per wave)
     (777, 8960, 9, 5, O.SCALE_FP16),      # 5 parts of 7 quads (W8: 70 quads, 7 parts of 10)
-    (500, 11264, 16, 6, O.SCALE_BF16),    # 4 parts of 11 quads: two quads per wave
-    (3072, 10752, 12, 16, O.SCALE_FP16),  # the reference engine's down shape: 6 parts of 7
+    (500, 11264, 16, 6, O.SCALE_BF16),    # W8: 8 parts of 11 quads, two quads per wave (Q4/Q5/Q6: the loop)
+    (3072, 10752, 12, 16, O.SCALE_FP16),  # the reference engine's down shape (Q4: the loop; W8: 6 parts of 14)
 ])
 def test_k_split(torch_dev, qtype, N, K, M, M2, senc):
     torch = torch_dev
@@ -306,7 +307,7 @@ def test_k_split_growing_sequence_one_workspace(torch_dev):
     torch = torch_dev
     shapes = [(O.Q4_G64, 2560, 10240, 5), (O.Q4_G64, 2560, 10240, 6), (O.Q4_G64, 2560, 10240, 16),
               (O.Q4_G64, 1000, 10240, 16), (O.Q4_G64, 2560, 10240, 16), (O.W8_G32, 2048, 6144, 9),
-              (O.Q5_G64, 2560, 12288, 12), (O.Q4_G64, 1000, 10240, 5)]
+              (O.Q5_G64, 1000, 12288, 12), (O.Q4_G64, 1000, 10240, 5)]
     nws = max(va.workspace_bytes(*s) for s in shapes)
     ws = torch.zeros(nws, dtype=torch.uint8, device="cuda")
     for i, (qtype, N, K, M) in enumerate(shapes):

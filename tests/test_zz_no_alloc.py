@@ -86,7 +86,7 @@ def test_static_rejects_past_the_array():
     L = va.lib()
     cap = 8 << 20
     for N, K, M in ((64, 1 << 20, 16),        # int8 activations alone: 16 * 2^20 bytes
-                    (8192, 10240, 16)):       # K-split records: 171 blocks of 48 rows x 49152 bytes
+                    (4096, 1 << 19, 9)):      # 8 MiB of int8 activations plus their scales
         assert L.viper_hip_qlinear_workspace_bytes(O.Q4_G64, N, K, M) > cap
         fake = C.c_void_p(0x10000)          # never dereferenced: the size check comes first
         rc = L.viper_hip_qlinear_static(O.Q4_G64, fake, fake, 0, 64, N, K, fake, M, fake, None, None)

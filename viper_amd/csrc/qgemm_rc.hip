@@ -2,6 +2,9 @@
 // shape and dispatch.  The kernel template is in qgemm_rc.h.
 #include "qgemm_rc.h"
 
+#include <map>
+#include <mutex>
+
 namespace vq {
 
 // Waves per workgroup and quads per wave of the single-segment shapes, in
@@ -41,9 +44,7 @@ static RcShape rc_shape(int F, int rows_total, int NQ, int cus) {
 // K = 10240, N = 2560: 107 blocks of 24 rows x 4 parts instead of 160 blocks
 // of 16 rows that each read all of K's activation, M = 4 / 8 / 16: 9.47 /
 // 9.45 / 9.87 us; 40 rows, one workgroup per CU: 9.9 / 9.8 / 10.0 us; 16 rows
-// 11.3 / 11.6 / 11.9 us).  (K = 10752, N = 3072: 77 blocks of 40 rows x 6
-// parts, whose last workgroups wait for a second round on the CUs: 12.5-14 us
-// with every part count and row block tried.)
+// 11.3 / 11.6 / 11.9 us).
 static int rc_split_parts(int NQ) {
     if (NQ <= 20) return 0;
     for (int lim : {10, 20})
@@ -51,6 +52,33 @@ static int rc_split_parts(int NQ) {
             if (NQ % sk == 0 && NQ / sk <= lim) return sk;
     return 0;
 }
+
+// Registers a kernel takes per lane (0 where the device cannot be asked),
+// cached per kernel.
+static int rc_regs(rc_fn fn) {
+    static std::mutex mu;
+    static std::map<const void*, int> cache;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto it = cache.find((const void*)fn);
+    if (it != cache.end()) return it->second;
+    hipFuncAttributes a{};
+    if (hipFuncGetAttributes(&a, (const void*)fn) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    cache[(const void*)fn] = a.numRegs;
+    return a.numRegs;
+}
+
+// A split pays only where two workgroups of ten waves sit on a CU with room
+// to spare: at most 80 registers, six waves per SIMD (forced shapes, M = 16,
+// fragment input, one box: Q4 24-row blocks, 72 registers: K = 10240 7.6
+// against 8.5 us on the segment loop, K = 6144 6.7 against 7.4; W8 40-row
+// blocks, 68: K = 10240 11.1 against 13.6; Q4 32- and 40-row blocks, 84 and
+// 96 registers: K = 8960 10.6 against 7.9, K = 12288 11.9 against 10.3,
+// K = 10752 13.5 against 10.1; Q5 24-row blocks, 84: K = 10240 11.7 against
+// 10.1).  Without a device to ask, the split is assumed to fit.
+constexpr int RC_SPLIT_MAX_REGS = 80;
 
 static bool rc_split_shape(int qtype, int rows, int K, int cus, RcShape& s) {
     const int F = qtype == VIPER_QTYPE_W8_G32 ? 8 : qtype, NQ = K / group_of(qtype) / 4;
@@ -62,7 +90,15 @@ static bool rc_split_shape(int qtype, int rows, int K, int cus, RcShape& s) {
     s.sk = sk;
     const int rb = (sk * rows + 16 * cus - 1) / (16 * cus), rbmax = s.qw == 2 ? rc_rb_qw2(F) : 6;
     s.rb = rb < 1 ? 1 : (rb > rbmax ? rbmax : rb);
-    return (rows + 8 * s.rb - 1) / (8 * s.rb) <= RC_CNT_MAX;
+    if ((rows + 8 * s.rb - 1) / (8 * s.rb) > RC_CNT_MAX) return false;
+    rc_fn fn;
+    switch (F) {
+        case 4: fn = rc_pick<4>(s, RC_FRAG, false, 0, false); break;
+        case 5: fn = rc_pick<5>(s, RC_FRAG, false, 0, false); break;
+        case 6: fn = rc_pick<6>(s, RC_FRAG, false, 0, false); break;
+        default: fn = rc_pick<8>(s, RC_FRAG, false, 0, false); break;
+    }
+    return fn != nullptr && rc_regs(fn) <= RC_SPLIT_MAX_REGS;
 }
 
 int rc_split_blocks(int qtype, int N, int K) {
