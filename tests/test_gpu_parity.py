@@ -158,6 +158,9 @@ def test_multi_row_long_k(torch_dev, qtype, M, K):
     (29, 192, 4, O.SCALE_FP16),
     (300, 384, 9, O.SCALE_BF16),     # 6 groups (W8: 12): the pair-wise matrix-core kernel
     (70, 640, 12, O.SCALE_FP16),     # 10 groups (W8: 20)
+    (1000, 3072, 16, O.SCALE_BF16),  # 12 quads: one per wave of 12 (W8: 24 quads, 3 parts of 8)
+    (3000, 2816, 9, O.SCALE_FP16),   # 11 quads on 12 waves, the last one idle; 3000 rows: 48-row blocks
+    (10752, 3072, 5, O.SCALE_FP16),  # the reference engine's gate shape on 12 waves (W8: the K split)
 ])
 def test_mfma_shapes(torch_dev, qtype, N, K, M, senc):
     run_case(torch_dev, qtype, N, K, M, seed=3000 + N + M, scale_enc=senc, residual=(M % 2 == 1))

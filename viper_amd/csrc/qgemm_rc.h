@@ -715,6 +715,7 @@ rc_fn rc_pick3(const RcShape& s, int am, bool part, int senc, bool pair) {
     }
     if (s.one && s.w == 4 && s.qw == 1) return rc_pick4<F, RB, 4, 1, true>(am, part, senc, pair);
     if (s.one && s.w == 10 && s.qw == 1) return rc_pick4<F, RB, 10, 1, true>(am, part, senc, pair);
+    if (s.one && s.w == 12 && s.qw == 1) return rc_pick4<F, RB, 12, 1, true>(am, part, senc, pair);
     if constexpr (RB <= rc_rb_qw2(F))
         if (s.one && s.w == 10 && s.qw == 2) return rc_pick4<F, RB, 10, 2, true>(am, part, senc, pair);
     if constexpr (RB <= RC_RB_LOOP)
@@ -743,6 +744,7 @@ rc_fn rc_pick_tl3(const RcShape& s, int senc) {
                     : qgemm_rc_kernel<F, RB, W_, QW_, true, RC_FRAG, false, 0, KS_, false, true>;
     VQ_RC_TL(4, 1, false)
     VQ_RC_TL(10, 1, false)
+    VQ_RC_TL(12, 1, false)
     VQ_RC_TL(10, 1, true)
     if constexpr (RB <= rc_rb_qw2(F)) {
         VQ_RC_TL(10, 2, false)

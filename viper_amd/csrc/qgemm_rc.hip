@@ -9,7 +9,10 @@ namespace vq {
 
 // Waves per workgroup and quads per wave of the single-segment shapes, in
 // order of preference; longer K loops over segments of one quad per wave.
-constexpr int RC_WQ[][2] = {{4, 1}, {10, 1}, {10, 2}};
+// (12 waves of one quad: the reference engine's K = 3072, whose 12 quads on
+// 10 waves of two left two waves with twice the work and, at N = 10752, the
+// two-quad kernel's registers one workgroup per CU for 336 workgroups.)
+constexpr int RC_WQ[][2] = {{4, 1}, {10, 1}, {12, 1}, {10, 2}};
 
 // Rows per workgroup: the multiple of 8 that spreads all rows (both matrices
 // of a fused pair) over one workgroup per CU, at most 48 (fewer with two
