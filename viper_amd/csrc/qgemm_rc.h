@@ -198,9 +198,9 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
         bid = (int)(blockIdx.x / SK);
         // the block's counter, for its epoch: the first vector load of the
         // kernel, so it returns ahead of the weights (loads retire in issue
-        // order) and no wait for an earlier load or LDS access waits for it
-        // (a scalar load made the first LDS barrier wait for it: down shape
-        // 0.25-0.45 us slower)
+        // order), with sc among the preloaded arguments (a scalar load of the
+        // counter through an sc read from the argument buffer measured
+        // 0.25-0.45 us slower at the down shape)
         cnt0 = bload4(buf(sc + RC_CTL_CNT + bid, 4u), 0);
         issue_fence();
     }
