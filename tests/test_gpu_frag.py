@@ -177,6 +177,59 @@ def test_prequantized_frag_against_oracle(torch_dev, qtype, N, K, M):
         assert split_state_ok(ws)
 
 
+# Seeded random shapes on the fragment entry: every format, K of 1..72 quads
+# of 4 groups (one segment, the segment loop without a workspace, the K split
+# of 2..8 parts with one), ragged N, 2..16 rows, both scale encodings,
+# residual on odd M.  Each output against the oracle, with and without a
+# workspace; above 4 rows equal bit for bit to the natural-layout entry,
+# which runs the same kernel.
+def _frag_random_shapes(n=12, seed=0xF7A6):
+    rng = np.random.default_rng(seed)
+    out = []
+    formats = [O.Q4_G64, O.Q5_G64, O.Q6_G64, O.W8_G32]
+    for i in range(n):
+        qtype = formats[i % 4]
+        G = O.group_size(qtype)
+        nq = int(rng.choice([1, 2, 3, 5, 8, 10, 12, 16, 20, 24, 30, 35, 40, 48, 60, 72]))
+        K = nq * 4 * G
+        N = int(rng.integers(1, 2200))
+        M = int(rng.integers(2, 17))
+        out.append((qtype, N, K, M, int(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("qtype,N,K,M,senc", _frag_random_shapes())
+def test_prequantized_frag_random_shapes(torch_dev, qtype, N, K, M, senc):
+    torch = torch_dev
+    print(f"frag random qtype={qtype} N={N} K={K} M={M} senc={senc}", flush=True)
+    G = O.group_size(qtype)
+    packed, scales = O.gen_weights(qtype, N, K, 7300 + N, senc)
+    x = O.gen_act(M, K, 7301 + M, outlier_frac=0.05)
+    xq, xs = O.quantize_act(x, G)
+    res = O.gen_act(M, N, 7302) if M % 2 == 1 else None
+    y_ref, _, absterm = O.qlinear_prequant(qtype, packed, scales, senc, N, K, xq, xs, residual=res)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, va.ScaleEnc(senc))
+    fq, fs = to_frag(np.asarray(xq, dtype=np.int8).reshape(M, K), np.asarray(xs, dtype=np.float32).reshape(M, K // G), G)
+    xf, sf = dev(torch, fq), dev(torch, fs)
+    rd = None if res is None else dev(torch, res)
+    nws = va.frag_workspace_bytes(qtype, N, K, M)
+    ws = torch.zeros(max(nws, 16), dtype=torch.uint8, device="cuda")
+    y, ys, y_nat = (torch.zeros((M, N), dtype=torch.int16, device="cuda") for _ in range(3))
+    assert va.linear_prequantized_frag(w, xf, sf, y, residual=rd).ok()
+    assert va.linear_prequantized_frag(w, xf, sf, ys, residual=rd, workspace=ws).ok()
+    assert va.linear_prequantized(w, dev(torch, np.asarray(xq, dtype=np.int8)), dev(torch, np.asarray(xs, dtype=np.float32)),
+                                  y_nat, residual=rd).ok()
+    torch.cuda.synchronize()
+    O.assert_bf16_close(u16(y), y_ref, absterm, rel=REL_TOL)
+    O.assert_bf16_close(u16(ys), y_ref, absterm, rel=REL_TOL)
+    if M > 4:
+        np.testing.assert_array_equal(u16(y), u16(y_nat))
+    if nws == 0:
+        np.testing.assert_array_equal(u16(ys), u16(y))
+    else:
+        assert split_state_ok(ws)
+
+
 def split_state_ok(ws):
     """After a call: every K-split block counter is a whole epoch (64 * calls) and no sum missed."""
     w = ws[:4352].cpu().numpy().view(np.uint32)
