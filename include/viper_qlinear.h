@@ -123,6 +123,10 @@ extern "C" {
 #define VIPER_SCALE_BF16 1
 
 #define VIPER_QLINEAR_MAX_M 16
+/* Longest K of the quantized entry points (a workgroup's block of weight
+ * rows is addressed with 32-bit sizes and offsets); longer K is
+ * INVALID_ARGUMENT. */
+#define VIPER_QLINEAR_MAX_K (1 << 24)
 /* 7: the K split keeps its own per-block counters (no launch before it), so
  *    the fragment-input entry points take an optional workspace;
  *    viper_hip_qlinear_frag_workspace_bytes; the workspace layout's offsets

@@ -136,6 +136,7 @@ FAKE = 0x10000  # never dereferenced: every call below fails validation first
     (dict(M=0), 2),
     (dict(N=0), 2),
     (dict(K=96), 2),                # K % 64 != 0 (dp4a_smem_kernel.cu:82)
+    (dict(K=(1 << 24) + 64), 2),    # K past VIPER_QLINEAR_MAX_K (32-bit block addressing)
     (dict(group=32), 2),            # group does not match the format
     (dict(senc=2), 2),
     (dict(w=FAKE + 8), 2),          # weights not 16-byte aligned

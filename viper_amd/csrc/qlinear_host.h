@@ -45,7 +45,7 @@ inline int validate_weights(int qtype, const void* w, const void* s, int senc, i
     if (w == nullptr || s == nullptr) return VIPER_INVALID_ARGUMENT;
     if (senc != VIPER_SCALE_FP16 && senc != VIPER_SCALE_BF16) return VIPER_INVALID_ARGUMENT;
     if (group != G) return VIPER_INVALID_ARGUMENT;
-    if (N <= 0 || K <= 0 || M <= 0 || M > VIPER_QLINEAR_MAX_M) return VIPER_INVALID_ARGUMENT;
+    if (N <= 0 || K <= 0 || M <= 0 || M > VIPER_QLINEAR_MAX_M || K > VIPER_QLINEAR_MAX_K) return VIPER_INVALID_ARGUMENT;
     if (K % G != 0) return VIPER_INVALID_ARGUMENT;
     if ((int64_t)M * K > INT32_MAX / 2) return VIPER_INVALID_ARGUMENT;
     // the kernels read scales in 8- and 16-byte loads (a workgroup's scale block at once)
