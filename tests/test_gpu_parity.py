@@ -230,6 +230,33 @@ def test_k_split_random_shapes(torch_dev, qtype, N, K, M, senc):
     run_case(torch_dev, qtype, N, K, M, seed=5500 + N, scale_enc=senc, residual=(M % 2 == 1))
 
 
+# Seeded random shapes through the bf16 entry, every dispatch path: 1..16
+# rows, K of 1..200 groups (odd group counts on the dot kernel, even ones on
+# the pair-swap matrix-core kernel, multiples of 4 on the row-contiguous one,
+# long K split or looped; M = 1 on exact, masked or general tilings), ragged
+# N, both scale encodings, residual at random.  Group dots bit-exact through
+# the partials entry; the production entry's output equal to the partials
+# entry's bit for bit (the same arithmetic) and within the bar of the oracle.
+def _random_shapes(n=24, seed=0x5EED7):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(n):
+        qtype = FORMATS[i % len(FORMATS)]
+        G = O.group_size(qtype)
+        ng = int(rng.choice([1, 2, 3, 4, 7, 8, 12, 16, 20, 33, 40, 48, 64, 80, 96, 100, 120, 160, 168, 200]))
+        M = 1 if rng.random() < 0.3 else int(rng.integers(2, 17))
+        out.append((qtype, int(rng.integers(1, 3000)), ng * G, M, int(rng.integers(0, 2)), bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("qtype,N,K,M,senc,residual", _random_shapes())
+def test_random_shapes_every_path(torch_dev, qtype, N, K, M, senc, residual):
+    seed = 9100 + N + K + M
+    y_part = run_case(torch_dev, qtype, N, K, M, seed=seed, scale_enc=senc, residual=residual)
+    y_prod = run_case(torch_dev, qtype, N, K, M, seed=seed, scale_enc=senc, residual=residual, check_partials=False)
+    np.testing.assert_array_equal(y_prod, y_part)
+
+
 # Two different activations at the same row count alternating on one
 # workspace: each result must be the oracle's for its own x (a part that
 # consumed the previous call's sums would give the other x's output).
