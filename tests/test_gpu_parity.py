@@ -703,6 +703,37 @@ def test_fused2(torch_dev, qtype, N, K, M, prequantized):
         O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
 
 
+# The same random shapes through the prequantized entry and both fused-pair
+# entries (bf16 rows and prequantized), each output against the oracle.
+@pytest.mark.parametrize("qtype,N,K,M,senc,residual", _random_shapes(n=16, seed=0x5EED8))
+def test_random_shapes_prequantized_and_fused2(torch_dev, qtype, N, K, M, senc, residual):
+    torch = torch_dev
+    G = O.group_size(qtype)
+    note(f"random pre/fused2 qtype={qtype} N={N} K={K} M={M} senc={senc} res={residual}")
+    p0, s0 = O.gen_weights(qtype, N, K, 9300 + N, senc)
+    p1, s1 = O.gen_weights(qtype, N, K, 9301 + N, senc)
+    x = O.gen_act(M, K, 9302 + M, outlier_frac=0.05)
+    xq, xs = O.quantize_act(x, G)
+    res = O.gen_act(M, N, 9303) if residual else None
+    ref_res = O.qlinear_prequant(qtype, p0, s0, senc, N, K, xq, xs, residual=res)
+    refs = [O.qlinear_prequant(qtype, p, sc, senc, N, K, xq, xs) for p, sc in ((p0, s0), (p1, s1))]
+    w0 = va.QuantizedWeight(va.QType(qtype), dev(torch, p0), dev(torch, s0), N, K, G, va.ScaleEnc(senc))
+    w1 = va.QuantizedWeight(va.QType(qtype), dev(torch, p1), dev(torch, s1), N, K, G, va.ScaleEnc(senc))
+    xqd, xsd = dev(torch, np.asarray(xq, dtype=np.int8)), dev(torch, np.asarray(xs, dtype=np.float32))
+    z = lambda: torch.zeros((M, N), dtype=torch.int16, device="cuda")
+    yp, a0, a1, b0, b1 = z(), z(), z(), z(), z()
+    assert va.linear_prequantized(w0, xqd, xsd, yp, residual=None if res is None else dev(torch, res)).ok()
+    nws = va.workspace_bytes(qtype, N, K, M)
+    ws = torch.zeros(max(16, nws), dtype=torch.uint8, device="cuda") if nws else None
+    assert va.linear_fused2(w0, w1, dev(torch, x), a0, a1, workspace=ws).ok()
+    assert va.linear_fused2_prequantized(w0, w1, xqd, xsd, b0, b1).ok()
+    torch.cuda.synchronize()
+    O.assert_bf16_close(host(yp, np.uint16), ref_res[0], ref_res[2], rel=REL_TOL)
+    for pair in ((a0, a1), (b0, b1)):
+        for yd, (y_ref, _, absterm) in zip(pair, refs):
+            O.assert_bf16_close(host(yd, np.uint16), y_ref, absterm, rel=REL_TOL)
+
+
 def test_fused2_matches_two_calls(torch_dev):
     # bit-identical to two single-matrix calls
     torch = torch_dev
