@@ -501,6 +501,39 @@ def test_engine_shapes_full_size(torch_dev, N, K, M):
     run_case(torch_dev, O.Q4_G64, N, K, M, seed=0xE0000 + K + M, residual=(N == 3072))
 
 
+# One Q4 / Q5 matrix at K = 3072 takes the 44-row workgroup where its grid
+# covers the CUs (N = 10752, 11000, ragged); N = 9000 and Q6 keep the shape
+# the picker takes by per-CU rows.  Group dots bit-exact, the output against the oracle, the production
+# entry equal to the partials entry bit for bit, and the timeline entry's
+# output equal to the production call's.
+@pytest.mark.parametrize("qtype,N", [(O.Q4_G64, 10752), (O.Q5_G64, 10752), (O.Q4_G64, 11000), (O.Q4_G64, 9000),
+                                     (O.Q6_G64, 10752)])
+def test_k3072_workgroup_choice(torch_dev, qtype, N):
+    import ctypes as C
+    torch = torch_dev
+    seed = 0xE3000 + N + qtype
+    y_part = run_case(torch, qtype, N, 3072, 1, seed=seed, residual=False)
+    y_prod = run_case(torch, qtype, N, 3072, 1, seed=seed, residual=False, check_partials=False)
+    np.testing.assert_array_equal(y_prod, y_part)
+    G = O.group_size(qtype)
+    packed, scales = O.gen_weights(qtype, N, 3072, seed, O.SCALE_FP16)
+    x = O.gen_act(1, 3072, seed + 1)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, 3072, G, va.ScaleEnc.FP16)
+    yt = torch.zeros((1, N), dtype=torch.int16, device="cuda")
+    stamps = torch.zeros(1 << 18, dtype=torch.int64, device="cuda")
+    grid, waves = C.c_int(0), C.c_int(0)
+    assert va.lib().viper_hip_qlinear_timeline(qtype, w.data.data_ptr(), w.scales.data_ptr(), 0, G, N, 3072,
+                                               dev(torch, x).data_ptr(), yt.data_ptr(), stamps.data_ptr(),
+                                               stamps.numel() * 8, C.byref(grid), C.byref(waves),
+                                               torch.cuda.current_stream().cuda_stream) == 0
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(host(yt, np.uint16), y_prod)
+    if qtype != O.Q6_G64 and N != 9000:
+        assert (grid.value, waves.value) == ((N + 43) // 44, 11)
+    else:
+        assert waves.value != 11
+
+
 # Every format at the engine's K (ragged N, both scale encodings, outliers):
 # Q4 / Q5 / Q6 on the 6-slot and masked tilings, W8 on its own (K = 3072:
 # 32 lanes x 6, 6144: 64 x 6; 10752 on the general path).
@@ -653,12 +686,13 @@ def test_prequantized_entry(torch_dev, N, K, M):
 
 @pytest.mark.parametrize("qtype", FORMATS)
 @pytest.mark.parametrize("N,K", [(2560, 2560), (61, 10240), (10240, 2560), (10010, 2560), (3072, 10752),
-                                 (6144, 3072), (3001, 6144)])
+                                 (6144, 3072), (3001, 6144), (10752, 3072), (11000, 3072)])
 def test_prequantized_m1(torch_dev, qtype, N, K):
     # M = 1 from int8 activations: the M = 1 kernel's prequantized prologue
     # (one octet per thread on 256 threads; Q4's two octets per thread on 320
     # and 640, a ragged last workgroup at N = 10010; the reference engine's K
-    # on the 6-slot tilings and the masked K = 10752 one)
+    # on the 6-slot tilings and the masked K = 10752 one; Q4 / Q5 at K = 3072
+    # and N = 10752 / 11000 on the 44-row workgroup, ragged at 11000)
     torch = torch_dev
     G = O.group_size(qtype)
     packed, scales = O.gen_weights(qtype, N, K, 50 + qtype, O.SCALE_FP16)

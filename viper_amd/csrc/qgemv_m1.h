@@ -728,6 +728,10 @@ constexpr int M1_SHAPES[][3] = {{8, 128, 10}, {8, 192, 10}, {8, 320, 10}, {16, 2
 // keep K constant and the staged scale block, and mask the last slots.  336
 // chunks: the engine's K = 10752 (Q4/Q5/Q6), 64 lanes x 6 slots; 384 and 768
 // threads put the engine's N = 3072 on 512 / 256 workgroups (6 / 12 rows).
+// One Q4 / Q5 matrix of 96 chunks per row (K = 3072) whose 384-thread
+// workgroups leave the CUs unevenly loaded: an 11-wave workgroup of 44 rows
+// (m1_wide96 says when).
+constexpr int M1_WIDE96[3] = {16, 704, 6};
 constexpr int M1_MASKED[][4] = {{64, 320, 6, 336}, {64, 384, 6, 336}, {64, 640, 6, 336}, {64, 768, 6, 336}};
 
 // Shapes of 5 or 6 chunk slots per lane are only ever exact tilings (m1_shape
@@ -745,6 +749,10 @@ m1_fn m1_kernel_v(int ts, int ntt, int cpl, int kc) {
     VQ_M1(32, 320, 10) VQ_M1(32, 640, 10) VQ_M1(64, 640, 10) VQ_M1(16, 256, 5) VQ_M1(16, 320, 5)
     VQ_M1(16, 640, 5) VQ_M1(32, 640, 5) VQ_M1(64, 640, 5) VQ_M1(16, 256, 6) VQ_M1(16, 320, 6)
     VQ_M1(16, 384, 6) VQ_M1(32, 320, 6) VQ_M1(32, 384, 6) VQ_M1(32, 640, 6) VQ_M1(64, 640, 6)
+    // the 44-row workgroup of one Q4 / Q5 matrix at K = 3072 (M1_WIDE96), bf16 or int8 row
+    if constexpr (F == 4 || F == 5)
+        if constexpr (MR == 1 && MODE != M1_SWIGLU && (PRO == PRO_BF16 || PRO == PRO_INT8))
+            VQ_M1(M1_WIDE96[0], M1_WIDE96[1], M1_WIDE96[2])
 #undef VQ_M1
     // masked exact tilings (KC_ chunks in TS_ * CPL_ slots), one row
 #define VQ_M1K(TS_, NTT_, CPL_, KC_)                                                                \

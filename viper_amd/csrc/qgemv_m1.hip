@@ -109,6 +109,23 @@ static M1Shape m1_shape(int cpr, int N, int cus, int min_ntt, int noct, bool pai
     return best;
 }
 
+// The reference engine's gate / up matrices (K = 3072, N = 10752) on the
+// 384-thread tiling (24 rows, 448 workgroups) load some CUs with 48 rows
+// against a 42-row mean.  One Q4 / Q5 matrix there takes the 44-row
+// workgroup (M1_WIDE96, 245 workgroups) when its grid still covers 95 % of
+// the CUs and it lowers the per-CU rows: N = 10752 Q4 5.06-5.16 -> 4.63-4.68
+// us (int8 row 4.90-4.93 -> 4.72-4.73), Q5 6.04-6.09 -> 5.87-5.90 us,
+// N = 11000 Q4 5.10-5.17 -> 4.69-4.70 us.  Not for Q6 (6.41-6.49 -> 7.03-7.14
+// us) nor a grid that leaves CUs idle (Q4 N = 9000, 205 workgroups:
+// 4.19-4.21 -> 4.25-4.38 us).
+static M1Shape m1_wide96(int qtype, int cpr, int N, int cus, const M1Shape& sh) {
+    if ((qtype != VIPER_QTYPE_Q4_G64 && qtype != VIPER_QTYPE_Q5_G64) || cpr != 96 || sh.ntt == 0) return sh;
+    const M1Shape c{M1_WIDE96[0], M1_WIDE96[1], M1_WIDE96[2]};
+    const long rows = c.ntt / c.ts, groups = (N + rows - 1) / rows;
+    if (groups * 20 < (long)cus * 19) return sh;
+    return m1_load(c, N, cus) < m1_load(sh, N, cus) ? c : sh;
+}
+
 // Upper bound over the launch shapes (an exact tiling's scale block holds at
 // most NTT * CPL bytes).
 size_t lds_m1(int qtype, int K) {
@@ -181,6 +198,7 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
         sh = m1_shape(K / ck, ntot, cus, min_ntt, noct, false, mr);
     }
     if (sh.ntt == 0) return VIPER_INVALID_ARGUMENT;
+    if (!folded && nouts == 1 && mr == 1) sh = m1_wide96(qtype, K / ck, ntot, cus, sh);
     const int group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
     const bool exact = m1_exact(sh, K / ck, K / group);
     const m1_fn fn = m1_kernel(qtype, sh, senc, part != nullptr ? M1_PART : M1_PLAIN, exact, pro, mr);
@@ -211,7 +229,7 @@ int launch_m1_timeline(int qtype, int senc, int K, const void* x, const void* w,
                        uint64_t* stamps, size_t stamp_bytes, int* workgroups, int* waves, hipStream_t st) {
     const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32, group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
     const int noct = K / 8;
-    const M1Shape sh = m1_shape(K / ck, N, device_cus(), 0, noct);
+    const M1Shape sh = m1_wide96(qtype, K / ck, N, device_cus(), m1_shape(K / ck, N, device_cus(), 0, noct));  // as launch_m1
     if (sh.ntt == 0 || !m1_exact(sh, K / ck, K / group)) return VIPER_INVALID_ARGUMENT;
     const m1_fn fn = m1_kernel(qtype, sh, senc, M1_TL, true, PRO_BF16);
     if (fn == nullptr) return VIPER_INTERNAL;
