@@ -503,35 +503,44 @@ def test_engine_shapes_full_size(torch_dev, N, K, M):
 
 # One Q4 / Q5 matrix at K = 3072 takes the 44-row workgroup where its grid
 # covers the CUs (N = 10752, 11000, ragged); N = 9000 and Q6 keep the shape
-# the picker takes by per-CU rows.  Group dots bit-exact, the output against the oracle, the production
-# entry equal to the partials entry bit for bit, and the timeline entry's
-# output equal to the production call's.
-@pytest.mark.parametrize("qtype,N", [(O.Q4_G64, 10752), (O.Q5_G64, 10752), (O.Q4_G64, 11000), (O.Q4_G64, 9000),
-                                     (O.Q6_G64, 10752)])
-def test_k3072_workgroup_choice(torch_dev, qtype, N):
+# the picker takes by per-CU rows.
+# Q5 from a bf16 row at K = 2560 takes one 40-row workgroup per CU where
+# that carries as many rows per CU as two of 20 (N = 10240, 20480); Q4 and
+# Q6 keep two of 20, and so does Q5 at N = 5000.  Group dots bit-exact, the
+# output against the oracle, the production entry equal to the partials
+# entry bit for bit, and the timeline entry's output and grid those of the
+# production call.
+@pytest.mark.parametrize("qtype,N,K", [(O.Q4_G64, 10752, 3072), (O.Q5_G64, 10752, 3072), (O.Q4_G64, 11000, 3072),
+                                       (O.Q4_G64, 9000, 3072), (O.Q6_G64, 10752, 3072), (O.Q5_G64, 10240, 2560),
+                                       (O.Q5_G64, 20480, 2560), (O.Q6_G64, 10240, 2560), (O.Q5_G64, 5000, 2560)])
+def test_m1_workgroup_choice(torch_dev, qtype, N, K):
     import ctypes as C
     torch = torch_dev
     seed = 0xE3000 + N + qtype
-    y_part = run_case(torch, qtype, N, 3072, 1, seed=seed, residual=False)
-    y_prod = run_case(torch, qtype, N, 3072, 1, seed=seed, residual=False, check_partials=False)
+    y_part = run_case(torch, qtype, N, K, 1, seed=seed, residual=False)
+    y_prod = run_case(torch, qtype, N, K, 1, seed=seed, residual=False, check_partials=False)
     np.testing.assert_array_equal(y_prod, y_part)
     G = O.group_size(qtype)
-    packed, scales = O.gen_weights(qtype, N, 3072, seed, O.SCALE_FP16)
-    x = O.gen_act(1, 3072, seed + 1)
-    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, 3072, G, va.ScaleEnc.FP16)
+    packed, scales = O.gen_weights(qtype, N, K, seed, O.SCALE_FP16)
+    x = O.gen_act(1, K, seed + 1)
+    w = va.QuantizedWeight(va.QType(qtype), dev(torch, packed), dev(torch, scales), N, K, G, va.ScaleEnc.FP16)
     yt = torch.zeros((1, N), dtype=torch.int16, device="cuda")
     stamps = torch.zeros(1 << 18, dtype=torch.int64, device="cuda")
     grid, waves = C.c_int(0), C.c_int(0)
-    assert va.lib().viper_hip_qlinear_timeline(qtype, w.data.data_ptr(), w.scales.data_ptr(), 0, G, N, 3072,
+    assert va.lib().viper_hip_qlinear_timeline(qtype, w.data.data_ptr(), w.scales.data_ptr(), 0, G, N, K,
                                                dev(torch, x).data_ptr(), yt.data_ptr(), stamps.data_ptr(),
                                                stamps.numel() * 8, C.byref(grid), C.byref(waves),
                                                torch.cuda.current_stream().cuda_stream) == 0
     torch.cuda.synchronize()
     np.testing.assert_array_equal(host(yt, np.uint16), y_prod)
-    if qtype != O.Q6_G64 and N != 9000:
-        assert (grid.value, waves.value) == ((N + 43) // 44, 11)
+    if K == 3072:
+        if qtype != O.Q6_G64 and N != 9000:
+            assert (grid.value, waves.value) == ((N + 43) // 44, 11)
+        else:
+            assert waves.value != 11
     else:
-        assert waves.value != 11
+        wide = qtype == O.Q5_G64 and N in (10240, 20480)
+        assert (grid.value, waves.value) == (((N + 39) // 40, 10) if wide else ((N + 19) // 20, 5))
 
 
 # Every format at the engine's K (ragged N, both scale encodings, outliers):

@@ -126,6 +126,18 @@ static M1Shape m1_wide96(int qtype, int cpr, int N, int cus, const M1Shape& sh) 
     return m1_load(c, N, cus) < m1_load(sh, N, cus) ? c : sh;
 }
 
+// Q5 from a bf16 row on the 16-lane tiling of K = 2560: where one 40-row
+// workgroup per CU carries as many rows as two of 20, it is faster (the
+// north-star shape, config 4: 4.92-4.99 -> 4.79-4.80 us); Q4 keeps two
+// workgroups of 20 (their quantize and barrier run independently: 3.8
+// against 3.97 us), and so do Q5 from an int8 row (4.86-4.88 against
+// 5.04-5.09 us) and Q6 (equal).
+static M1Shape m1_q5_bf16(int qtype, int pro, int N, int cus, const M1Shape& sh) {
+    if (qtype != VIPER_QTYPE_Q5_G64 || pro != PRO_BF16 || sh.ts != 16 || sh.ntt != 320 || sh.cpl != 5) return sh;
+    const M1Shape c{16, 640, 5};
+    return m1_load(c, N, cus) == m1_load(sh, N, cus) ? c : sh;
+}
+
 // Upper bound over the launch shapes (an exact tiling's scale block holds at
 // most NTT * CPL bytes).
 size_t lds_m1(int qtype, int K) {
@@ -198,7 +210,7 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
         sh = m1_shape(K / ck, ntot, cus, min_ntt, noct, false, mr);
     }
     if (sh.ntt == 0) return VIPER_INVALID_ARGUMENT;
-    if (!folded && nouts == 1 && mr == 1) sh = m1_wide96(qtype, K / ck, ntot, cus, sh);
+    if (!folded && nouts == 1 && mr == 1) sh = m1_q5_bf16(qtype, pro, ntot, cus, m1_wide96(qtype, K / ck, ntot, cus, sh));
     const int group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
     const bool exact = m1_exact(sh, K / ck, K / group);
     const m1_fn fn = m1_kernel(qtype, sh, senc, part != nullptr ? M1_PART : M1_PLAIN, exact, pro, mr);
@@ -229,7 +241,8 @@ int launch_m1_timeline(int qtype, int senc, int K, const void* x, const void* w,
                        uint64_t* stamps, size_t stamp_bytes, int* workgroups, int* waves, hipStream_t st) {
     const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32, group = qtype == VIPER_QTYPE_W8_G32 ? 32 : 64;
     const int noct = K / 8;
-    const M1Shape sh = m1_wide96(qtype, K / ck, N, device_cus(), m1_shape(K / ck, N, device_cus(), 0, noct));  // as launch_m1
+    const int cus = device_cus();
+    const M1Shape sh = m1_q5_bf16(qtype, PRO_BF16, N, cus, m1_wide96(qtype, K / ck, N, cus, m1_shape(K / ck, N, cus, 0, noct)));  // as launch_m1
     if (sh.ntt == 0 || !m1_exact(sh, K / ck, K / group)) return VIPER_INVALID_ARGUMENT;
     const m1_fn fn = m1_kernel(qtype, sh, senc, M1_TL, true, PRO_BF16);
     if (fn == nullptr) return VIPER_INTERNAL;
