@@ -491,9 +491,6 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     //    octet as (ql nibbles, qh nibbles); Q5/Q6 as [k even | k odd] int8;
     //    W8 in k order.
     const int xiters = (noct + ANT - 1) / ANT;
-    // (the up matrix's block follows the gate block: lsc[rr * NGR + g] for every team)
-    if constexpr (EXACT)
-        if (ltid * 16 < nrows * NGR * 2) *(u32x4*)((uint8_t*)lsc + (up ? P * NGR * 2 : 0) + ltid * 16) = sblk;
     // PRO_RMSNORM: the row's sum of squares (per-thread fma chain over its
     // octets in order, DPP within the wave, wave sums in wave order)
     float inv = 0.0f;
@@ -619,6 +616,12 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
                 if (stager && wave0 + ANT * i < noct) quant_store(at + ANT * i, load_x(at + ANT * i));
     }
 
+    // the scale block into LDS after the activation: its loads come from HBM
+    // and arrive after the activation's, and the quantize (and the rmsnorm
+    // prologue's row sum) need not wait for them
+    // (the up matrix's block follows the gate block: lsc[rr * NGR + g] for every team)
+    if constexpr (EXACT)
+        if (ltid * 16 < nrows * NGR * 2) *(u32x4*)((uint8_t*)lsc + (up ? P * NGR * 2 : 0) + ltid * 16) = sblk;
     stamp(3);
     lds_barrier();
     stamp(4);
