@@ -127,6 +127,10 @@ extern "C" {
  * rows is addressed with 32-bit sizes and offsets); longer K is
  * INVALID_ARGUMENT. */
 #define VIPER_QLINEAR_MAX_K (1 << 24)
+/* Most output rows N of one matrix at M = 1 (the launch's row count shares a
+ * word with flags); the M > 1 kernels take fewer than 2^27.  More is
+ * INVALID_ARGUMENT. */
+#define VIPER_QLINEAR_MAX_N ((1 << 30) - 1)
 /* 7: the K split keeps its own per-block counters (no launch before it), so
  *    the fragment-input entry points take an optional workspace;
  *    viper_hip_qlinear_frag_workspace_bytes; the workspace layout's offsets

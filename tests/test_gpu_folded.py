@@ -215,4 +215,9 @@ def test_m1_errors_are_codes(torch_dev):
     assert va.linear_m1([w], P.BF16, x, None, [y]).ok()
     assert va.linear_m1([w] * 4, P.BF16, x, None, [y] * 4).code == va.StatusCode.INVALID_ARGUMENT
     assert va.linear_m1([w], P.BF16, x, None, [y], norm_out=x).code == va.StatusCode.INVALID_ARGUMENT
+    # n0's high bits carry launch flags: 2^30 rows or more are refused before any launch
+    # (the same small buffers: nothing is read)
+    big = va.QuantizedWeight(w.qtype, w.data, w.scales, 1 << 30, w.cols, w.group_size, w.scale_enc)
+    assert va.linear_m1([big], P.BF16, x, None, [y]).code == va.StatusCode.INVALID_ARGUMENT
+    assert va.linear_m1_swiglu(big, big, P.BF16, x, None, y).code == va.StatusCode.INVALID_ARGUMENT
     torch.cuda.synchronize()

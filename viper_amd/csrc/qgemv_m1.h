@@ -2,6 +2,8 @@
 // qgemv_m1_q4.hip ... qgemv_m1_w8.hip so the formats compile in parallel).
 #pragma once
 
+#include <cstddef>
+
 #include "qlinear_host.h"
 
 namespace vq {
@@ -224,6 +226,50 @@ __device__ __forceinline__ void m1_dots_rows(u32x4 (&wv)[CPL], uint32_t (&h0)[CP
     }
 }
 
+// n0's high bits: flags of the launch (the row count of matrix 0 below them,
+// at most VIPER_QLINEAR_MAX_N)
+constexpr int M1_N_EXTRA = VIPER_QLINEAR_MAX_N + 1;  // optional outputs present (xout; the pair's gate / up)
+constexpr int M1_N_MASK = VIPER_QLINEAR_MAX_N;
+
+// qgemv_m1_kernel's parameters in order, as they lie in its kernarg segment
+// (each at its natural alignment): the offsets of those past the preloaded
+// ones, read with vector loads where a scalar load's cache miss would sit on
+// the critical path.
+struct M1KernArgs {
+    const void* x;
+    const uint8_t* w0;
+    const uint16_t* s0;
+    uint16_t* y0;
+    int K, n0, e0, e1;
+    const uint16_t* res;
+    const void* xa;
+    float eps;
+    uint16_t* xout;
+    int32_t* part;
+    const uint8_t* w1;
+    const uint16_t* s1;
+    uint16_t* y1;
+    int n1;
+    const uint8_t* w2;
+    const uint16_t* s2;
+    uint16_t* y2;
+    int n2;
+};
+static_assert(offsetof(M1KernArgs, eps) == 64 && offsetof(M1KernArgs, n2) == 144, "kernarg layout");
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t m1_kernargs() {
+    return buf((const void*)__builtin_amdgcn_kernarg_segment_ptr(), (uint32_t)sizeof(M1KernArgs));
+}
+// xout, read only in the branch that stores it: the offset goes through an
+// opaque zero, so the compiler cannot hoist the scalar load out of the branch
+// (hoisted, its cache miss held every workgroup at its next wait on the scalar
+// and LDS counter)
+__device__ __forceinline__ uint16_t* m1_xout() {
+    int z;
+    asm volatile("s_mov_b32 %0, 0" : "=s"(z));
+    const auto* ka = (const __attribute__((address_space(4))) uint8_t*)__builtin_amdgcn_kernarg_segment_ptr();
+    return *(uint16_t* const __attribute__((address_space(4)))*)(ka + offsetof(M1KernArgs, xout) + z);
+}
+
 // EXACT: every lane's chunks lie inside its row (the row has exactly TS * CPL
 // chunks) and a row's scales fill whole 16-byte words (groups % 8 == 0), so no
 // chunk needs masking and the workgroup's scale block is loaded with one
@@ -237,8 +283,11 @@ __device__ __forceinline__ void m1_dots_rows(u32x4 (&wv)[CPL], uint32_t (&h0)[CP
 // short head start lets its requests through the memory pipeline before the
 // weight stream saturates it, which moves every workgroup's barrier earlier.
 // xa: PRO_INT8 the group scales, PRO_RMSNORM gamma, PRO_SWIGLU up.
-// xout (PRO_RMSNORM, may be null): the bf16 normalized row, written by the
-// first workgroup.
+// xout (PRO_RMSNORM): the bf16 normalized row, written by the first
+// workgroup when n0 carries M1_N_EXTRA.
+// M1_SWIGLU takes the up matrix in the res (weights) and e0 / e1 (scales, low
+// and high half) slots and writes the product to y0; with M1_N_EXTRA, y1 and
+// y2 (each may be null) receive gate and up.
 // MR > 1 (PRO_BF16 / PRO_INT8, one matrix): M = e1 <= MR activation rows
 // (x [M][K], y and the residual [M][N]); every workgroup stages all M rows,
 // each lane decodes its weight chunk once and dots it with every row.  Small
@@ -347,8 +396,9 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     const uint8_t* w = w0;
     const uint16_t* ws = s0;
     uint16_t* y = y0;
-    int N = n0;
-    if (MR == 1 && __builtin_expect(bid >= e0, 0)) {
+    int N = n0 & M1_N_MASK;
+    const bool extra_out = (n0 & M1_N_EXTRA) != 0;  // optional outputs (xout; the pair's gate / up)
+    if (MR == 1 && !SWI && __builtin_expect(bid >= e0, 0)) {
         res = nullptr;
         if (bid >= e1) {
             bid -= e1;
@@ -370,10 +420,14 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     int rt = rr;
     bool up = false;
     if constexpr (SWI) {
+        // the up matrix comes in preloaded slots the pair does not use
+        // otherwise (weights in the residual's, scales in e0 / e1): read
+        // from the kernarg segment past them, the pointers would hold every
+        // up wave's weight requests back by a scalar-cache miss
         up = __builtin_amdgcn_readfirstlane(tid >> 6) * (64 / TS) >= P;  // wave-uniform
         if (up) {
-            w = w1;
-            ws = s1;
+            w = (const uint8_t*)res;
+            ws = (const uint16_t*)(((uint64_t)(uint32_t)e1 << 32) | (uint32_t)e0);
             rt = rr - P;
         }
         res = nullptr;
@@ -447,6 +501,15 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         }
         issue_fence();
     }
+    // eps sits past the preloaded arguments: a scalar load there misses the
+    // scalar cache, and its wait, after the row sum's barrier, held the
+    // rmsnorm launches 0.5 us.  A vector load issued here returns with the
+    // row.
+    float epsv = eps;
+    if constexpr (PRO == PRO_RMSNORM) {
+        epsv = __uint_as_float(bload4(m1_kernargs(), (int)offsetof(M1KernArgs, eps)));
+        issue_fence();
+    }
     const auto sr = buf(ws + (size_t)row0 * NGR, (uint32_t)(nrows * NGR) * 2);
     u32x4 sblk = {0u, 0u, 0u, 0u};
     if constexpr (EXACT) sblk = bload16(sr, ltid * 16);
@@ -514,7 +577,7 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
         float t = 0.0f;
 #pragma unroll
         for (int i = 0; i < NTT / 64; ++i) t += lred[i];
-        inv = __builtin_amdgcn_rsqf(t / (float)K + eps);
+        inv = __builtin_amdgcn_rsqf(t / (float)K + epsv);
     }
     // PRO_RMSNORM / PRO_SWIGLU: the bf16 row element-wise from two inputs
     auto produce = [&](const u32x4& v, const u32x4& a) -> u32x4 {
@@ -602,8 +665,11 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
             if constexpr (TWO) {
                 const int o = at + ANT * i;
                 const u32x4 v = produce(xv[i], av[i]);
-                if (PRO == PRO_RMSNORM && xout != nullptr && blockIdx.x == 0 && o < noct)
-                    *(u32x4*)(xout + (size_t)o * 8) = v;
+                if (PRO == PRO_RMSNORM && __builtin_expect(extra_out, 0) && blockIdx.x == 0) {
+                    // (the flag also marks the pair's gate / up outputs: xout may be null)
+                    uint16_t* xo = m1_xout();
+                    if (xo != nullptr && o < noct) *(u32x4*)(xo + (size_t)o * 8) = v;
+                }
                 quant_store(o, v);
             } else {
                 quant_store(at + ANT * i, xv[i]);
@@ -681,19 +747,19 @@ qgemv_m1_kernel(const void* x, const uint8_t* w0, const uint16_t* s0, uint16_t* 
     stamp(6);
     acc = team_sum<TS>(acc);
     if constexpr (SWI) {
-        // gate values through LDS; y0 / y1 (may be null) receive gate and up,
-        // y2 the product
+        // gate values through LDS; y0 receives the product, y1 / y2 (with
+        // extra_out, each may be null) gate and up
         const uint16_t vb = f2bf(acc);
         if (l == 0 && row_ok) {
             if (!up) {
                 lepi[rt] = vb;
-                if (y0 != nullptr) y0[row] = vb;
-            } else if (y1 != nullptr) {
-                y1[row] = vb;
+                if (__builtin_expect(extra_out, 0) && y1 != nullptr) y1[row] = vb;
+            } else if (__builtin_expect(extra_out, 0) && y2 != nullptr) {
+                y2[row] = vb;
             }
         }
         lds_barrier();
-        if (up && l == 0 && row_ok) y2[row] = f2bf(silu_mul(bf16f(lepi[rt]), bf16f(vb)));
+        if (up && l == 0 && row_ok) y0[row] = f2bf(silu_mul(bf16f(lepi[rt]), bf16f(vb)));
     } else {
         if (l == 0 && row_ok) {
             if (__builtin_expect(res != nullptr, 0)) acc += bf16f(res[row]);

@@ -196,7 +196,11 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32;
     const bool folded = pro == PRO_RMSNORM || pro == PRO_SWIGLU;
     int ntot = 0;
-    for (int i = 0; i < nouts; ++i) ntot += outs[i].n;
+    for (int i = 0; i < nouts; ++i) {
+        // n0's high bits carry flags
+        if (outs[i].n >= M1_N_EXTRA || ntot > INT32_MAX - outs[i].n) return VIPER_INVALID_ARGUMENT;
+        ntot += outs[i].n;
+    }
     // The folded prologues hold the whole row after one load round, and run
     // fastest with one octet per thread (rmsnorm's row sum and swiglu's
     // element work are then a single pass): take such a workgroup when an
@@ -224,7 +228,7 @@ int launch_m1(int qtype, int senc, int K, int pro, const void* x, const void* xa
     const uint8_t *w0 = (const uint8_t*)o0.w, *w1 = (const uint8_t*)o1.w, *w2 = (const uint8_t*)o2.w;
     const uint16_t *s0 = (const uint16_t*)o0.s, *s1 = (const uint16_t*)o1.s, *s2 = (const uint16_t*)o2.s;
     uint16_t *y0 = (uint16_t*)o0.y, *y1 = (uint16_t*)o1.y, *y2 = (uint16_t*)o2.y;
-    int n0 = o0.n, n1 = o1.n, n2 = o2.n;
+    int n0 = o0.n | (pro == PRO_RMSNORM && xout != nullptr ? M1_N_EXTRA : 0), n1 = o1.n, n2 = o2.n;
     int e0 = nb[0], e1 = nb[0] + nb[1];
     if (mr > 1) e1 = M;  // one matrix: e1 carries the activation rows
     const unsigned grid = (unsigned)(nb[0] + nb[1] + nb[2]);
@@ -273,6 +277,7 @@ int launch_m1_swiglu(int qtype, int senc, int K, int pro, const void* x, const v
                      const void* wg, const void* sg, const void* wu, const void* su, int N, void* h, void* g_out,
                      void* u_out, hipStream_t st) {
     if (pro != PRO_BF16 && pro != PRO_RMSNORM) return VIPER_INVALID_ARGUMENT;
+    if (N >= M1_N_EXTRA) return VIPER_INVALID_ARGUMENT;  // n0's high bits carry flags
     const int ck = qtype == VIPER_QTYPE_W8_G32 ? 16 : 32;
     const int noct = K / 8;
     const int cus = device_cus();
@@ -287,14 +292,18 @@ int launch_m1_swiglu(int qtype, int senc, int K, int pro, const void* x, const v
     const int rows = sh.ntt / sh.ts;
     const size_t lds = lds_m1_launch(qtype, K, rows, exact);
     if (lds > (size_t)LDS_MAX) return VIPER_INVALID_ARGUMENT;
-    int n0 = N, n1 = N, n2 = N;
-    int e0 = (N + rows / 2 - 1) / (rows / 2);  // every workgroup is a pair: no second-matrix range
-    int e1 = e0;
-    const unsigned grid = (unsigned)e0;
-    const uint8_t *w0 = (const uint8_t*)wg, *w1 = (const uint8_t*)wu, *w2 = nullptr;
-    const uint16_t *s0 = (const uint16_t*)sg, *s1 = (const uint16_t*)su, *s2 = nullptr;
-    uint16_t *y0 = (uint16_t*)g_out, *y1 = (uint16_t*)u_out, *y2 = (uint16_t*)h;
-    const uint16_t* r = nullptr;
+    // every workgroup is a pair of gate and up rows; the up matrix goes in the
+    // residual's slot (weights) and e0 / e1 (scales), the product to y0, the
+    // optional gate / up outputs to y1 / y2 (flagged in n0)
+    const bool extra = g_out != nullptr || u_out != nullptr || (pro == PRO_RMSNORM && xout != nullptr);
+    int n0 = N | (extra ? M1_N_EXTRA : 0), n1 = N, n2 = N;
+    const unsigned grid = (unsigned)((N + rows / 2 - 1) / (rows / 2));
+    const uint64_t su_bits = (uint64_t)(uintptr_t)su;
+    int e0 = (int)(uint32_t)su_bits, e1 = (int)(uint32_t)(su_bits >> 32);
+    const uint8_t *w0 = (const uint8_t*)wg, *w1 = nullptr, *w2 = nullptr;
+    const uint16_t *s0 = (const uint16_t*)sg, *s1 = nullptr, *s2 = nullptr;
+    uint16_t *y0 = (uint16_t*)h, *y1 = (uint16_t*)g_out, *y2 = (uint16_t*)u_out;
+    const uint16_t* r = (const uint16_t*)wu;
     int32_t* part = nullptr;
     int kg = exact ? (int)grid : K;  // as in launch_m1
     void* args[] = {&x, &w0, &s0, &y0, &kg, &n0, &e0, &e1, &r, &xa, &eps, &xout, &part,
