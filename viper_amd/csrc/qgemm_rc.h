@@ -257,16 +257,16 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     // one or two loads per thread instead of a load per lane, tile and quad
     // (those small loads, queued ahead of every wave's weights: down shape
     // M = 4 9.4 -> 9.1 us, M = 16 10.0 -> 9.7 us).  Rows past the block read
-    // as zero.  Not for RC_BF16: its staging stores would wait for the weight
-    // scales from HBM before the rows' quantize (M = 8 7.5 -> 8.0 us); not
-    // for Q5/Q6, whose high-plane loads follow (8 rows: 8.5 / 8.7 -> 9.1 /
-    // 9.3 us).  (Forming the products ws * xs here, before the weights
+    // as zero.  RC_BF16 stages the weight scales only (its activation scales
+    // are the quantize's), stored after the rows' quantize so that it does not
+    // wait for them from HBM.  Not for Q5/Q6, whose high-plane loads follow (8
+    // rows: 8.5 / 8.7 -> 9.1 / 9.3 us).  (Forming the products ws * xs here, before the weights
     // arrive, took 32-48 more VGPRs: the K split lost its second workgroup
     // per CU.)
-    constexpr bool STG = ONE && AM == RC_FRAG && FM::HQ == 0;
+    constexpr bool STG = ONE && (AM == RC_FRAG || XBF) && FM::HQ == 0;
     constexpr int R8 = 8 * RB;
     constexpr int SI = (R8 * QW + 63) / 64;  // pieces per thread: 8RB * NQ <= 8RB * W * QW
-    uint8_t* wsl = smem + rc_lds_bytes(FM::HSTR, RB, W);
+    uint8_t* wsl = smem + rc_lds_bytes(FM::HSTR, RB, W) + (XBF ? rc_act_lds_bytes(FM::QB, 4 * NQ) : 0);
     uint8_t* xsl = wsl + (size_t)16 * T * NQ * 8;
     u32x2 stw[STG ? SI : 1];
     u32x4 stx = {0u, 0u, 0u, 0u};
@@ -277,7 +277,7 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
             const int c = tid + NTT * i, q = c / R8, r = c - q * R8;
             stw[i] = bload8(wst, q < NQ ? (r * NG + 4 * (q0 + q)) * 2 : OOB);
         }
-        stx = bload16(xsr, tid < NQ * 16 ? tid * 16 : OOB);
+        if constexpr (!XBF) stx = bload16(xsr, tid < NQ * 16 ? tid * 16 : OOB);
     }
 
     auto load = [&](Seg& S, int seg) {
@@ -504,13 +504,19 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                 }
             }
         }
-        lds_barrier();
     };
 
     if constexpr (ONE) {
         Seg S;
         load(S, 0);
         stamp(2);
+        // RC_BF16: the rows' quantize first (its octets arrive ahead of the
+        // weight scales, which come from HBM), then the staging stores, one
+        // barrier for both
+        if constexpr (XBF) {
+            issue_fence();
+            quantize();
+        }
         if constexpr (STG) {
             issue_fence();  // the weight requests stay ahead of the staging stores
 #pragma unroll
@@ -518,10 +524,10 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                 const int c = tid + NTT * i, q = c / R8, r = c - q * R8;
                 if (q < NQ) *(u32x2*)(wsl + (r * NQ + q) * 8) = stw[i];
             }
-            if (tid < NQ * 16) *(u32x4*)(xsl + tid * 16) = stx;
-            lds_barrier();
+            if constexpr (!XBF)
+                if (tid < NQ * 16) *(u32x4*)(xsl + tid * 16) = stx;
         }
-        if constexpr (XBF) quantize();
+        if constexpr (STG || XBF) lds_barrier();
         if constexpr (STG) {
 #pragma unroll
             for (int j = 0; j < QW; ++j) {
@@ -529,8 +535,9 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
                 if (Q < NQ) {
 #pragma unroll
                     for (int t = 0; t < T; ++t) S.S[j][t] = *(const u32x2*)(wsl + ((16 * t + n16) * NQ + Q) * 8);
+                    if constexpr (!XBF)
 #pragma unroll
-                    for (int h = 0; h < 4; ++h) S.XS[j][h] = *(const u32x4*)(xsl + ((4 * Q + h) * 16 + 4 * kb) * 4);
+                        for (int h = 0; h < 4; ++h) S.XS[j][h] = *(const u32x4*)(xsl + ((4 * Q + h) * 16 + 4 * kb) * 4);
                 }
             }
         }
@@ -541,7 +548,10 @@ qgemm_rc_kernel(const int8_t* xq, const float* xs, const uint8_t* w, const uint1
     } else {
         Seg S0, S1;
         load(S0, 0);
-        if constexpr (XBF) quantize();
+        if constexpr (XBF) {
+            quantize();
+            lds_barrier();
+        }
         for (int seg = 0; seg < nseg; seg += 2) {
             load(S1, seg + 1);  // past the last segment every load is out of range: no traffic
             compute(S0, seg);

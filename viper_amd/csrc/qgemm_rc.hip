@@ -128,7 +128,7 @@ static int rc_hstr(int qtype) {
 // LDS bytes of a launch (RC_BF16 adds the workgroup's copy of the fragments).
 static size_t rc_launch_lds(int qtype, const RcShape& sh, int K, int am) {
     const int qb = qtype == VIPER_QTYPE_W8_G32 ? RcFmt<8>::QB : RcFmt<4>::QB;
-    const bool staged = sh.one && am == RC_FRAG && rc_hstr(qtype) == 0;  // the kernel's staged scales
+    const bool staged = sh.one && (am == RC_FRAG || am == RC_BF16) && rc_hstr(qtype) == 0;  // the kernel's staged scales
     const int ngp = K / group_of(qtype) / sh.sk;  // groups of the workgroup's part
     return rc_lds_bytes(rc_hstr(qtype), sh.rb, sh.w) + (am == RC_BF16 ? rc_act_lds_bytes(qb, ngp) : 0) +
            (staged ? rc_stage_bytes(sh.rb, ngp / 4) : 0);
