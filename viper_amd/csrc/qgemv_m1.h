@@ -256,8 +256,9 @@ struct M1KernArgs {
     int n2;
 };
 static_assert(offsetof(M1KernArgs, eps) == 64 && offsetof(M1KernArgs, n2) == 144, "kernarg layout");
+// (the segment ends with n2: no tail padding is read)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t m1_kernargs() {
-    return buf((const void*)__builtin_amdgcn_kernarg_segment_ptr(), (uint32_t)sizeof(M1KernArgs));
+    return buf((const void*)__builtin_amdgcn_kernarg_segment_ptr(), (uint32_t)(offsetof(M1KernArgs, n2) + sizeof(int)));
 }
 // xout, read only in the branch that stores it: the offset goes through an
 // opaque zero, so the compiler cannot hoist the scalar load out of the branch
