@@ -124,18 +124,21 @@ class Stack:
 
     def attention_half(self, l, fused=True):
         """Slot l's q/k/v projections from rmsnorm(x) and the o projection of
-        the fixed attention output added into x."""
+        the fixed attention output added into x.  Slot 0 reads the step's input
+        row x0 (the embedding's output) and its o projection writes x, so a
+        step needs no copy of x0 into x."""
         L, st = self.L, self.torch.cuda.current_stream().cuda_stream
         H, nQ, nKV = self.H, self.nQ, self.nKV
         p = lambda t: t.data_ptr()
         x = self.x
+        xin = self.x0 if l == 0 else x
         wq, wk, wv, wo = self.w[l % self.layers][:4]
         ln = self.ln[2 * (l % self.layers)]
         if fused:
-            self._m1(2, p(x), p(ln), [(wq, self.q), (wk, self.k), (wv, self.v)], eps=self.eps, st=st)
-            self._m1(0, p(self.attn), None, [(wo, x)], residual=p(x), st=st)
+            self._m1(2, p(xin), p(ln), [(wq, self.q), (wk, self.k), (wv, self.v)], eps=self.eps, st=st)
+            self._m1(0, p(self.attn), None, [(wo, x)], residual=p(xin), st=st)
             return
-        self._ok(L.viper_hip_rmsnorm_quantize(p(x), p(ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
+        self._ok(L.viper_hip_rmsnorm_quantize(p(xin), p(ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
                                               p(self.xs), st), "rmsnorm_quantize")
         self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wq[0]), p(wq[1]), 0, 64, nQ, H, p(self.xq), p(self.xs), 1,
                                                   p(self.q), None, st), "q")
@@ -143,7 +146,7 @@ class Stack:
                                                          p(self.xq), p(self.xs), 1, p(self.k), p(self.v), st), "kv")
         self._ok(L.viper_hip_quantize_act(64, p(self.attn), 1, nQ, p(self.xq), p(self.xs), st), "quantize")
         self._ok(L.viper_hip_qlinear_prequantized(Q4, p(wo[0]), p(wo[1]), 0, 64, H, nQ, p(self.xq), p(self.xs), 1,
-                                                  p(x), p(x), st), "o")
+                                                  p(x), p(xin), st), "o")
 
     def mlp_half(self, l, fused=True):
         """Slot l's gate/up projections from rmsnorm(x), h = silu(gate) * up
@@ -197,7 +200,6 @@ class Stack:
 
     def _step(self, fused, prefetch=0):
         torch = self.torch
-        self.x.copy_(self.x0)
         slots = self.layers * self.passes
         if prefetch:
             if self.side is None:
