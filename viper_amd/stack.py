@@ -13,8 +13,10 @@ on this path; its output is a fixed activation):
     swiglu_quantize(gate, up)      -> down GEMV + residual (in place on x)
 
 step_fused() is the same computation in 4 launches per slot instead of 9:
-the producers are folded into the GEMV prologues, q/k/v share a launch
-(viper_hip_qlinear_m1), and the gate/up launch pairs the rows of both matrices
+the producers are folded into the GEMV prologues, q/k/v are one launch over
+their concatenated weight (each layer stores q, k and v row after row, the
+engine's fused qkv matrix; viper_hip_qlinear_m1), and the gate/up launch pairs
+the rows of both matrices
 so its epilogue writes h = silu(gate) * up (viper_hip_qlinear_m1_swiglu,
 bit-identical to the swiglu of the two outputs); the down projection then
 quantizes h in its prologue:
@@ -46,13 +48,32 @@ class Stack:
         H, I, nQ, nKV = self.H, self.I, self.nQ, self.nKV
         shapes = [(nQ, H), (nKV, H), (nKV, H), (H, nQ), (I, H), (I, H), (H, I)]
         self.w = []        # per layer: 7 (packed, scales, N, K), views of the layer's arena
+        self.wqkv = []     # per layer: q, k and v as one matrix of nQ + 2 nKV rows (views of the same bytes)
         self.arenas = []   # per layer: one device buffer, every section at a 256-byte aligned offset
         sec = lambda nbytes: (nbytes + 255) // 256 * 256
+        # q, k and v lie row after row in one packed section and one scale section, so the fused
+        # step reads them as one matrix (the engine's concatenated qkv weight): a launch with one
+        # matrix keeps every workgroup's arguments among the preloaded ones
+        nqkv = nQ + 2 * nKV
+        assert (nQ * (H // 64) * 2) % 16 == 0 and (nKV * (H // 64) * 2) % 16 == 0, "16-byte aligned q/k/v scales"
         for _ in range(layers):
-            arena = torch.empty(sum(sec(n * k // 2) + sec(n * (k // 64) * 2) for n, k in shapes), dtype=torch.uint8,
-                                device="cuda")
-            lw, off = [], 0
-            for (n, k) in shapes:
+            sizes = [sec(nqkv * H // 2), sec(nqkv * (H // 64) * 2)] + \
+                    [sec(n * k // 2) + sec(n * (k // 64) * 2) for n, k in shapes[3:]]
+            arena = torch.empty(sum(sizes), dtype=torch.uint8, device="cuda")
+            lw = []
+            qkv_p, qkv_s = arena[:nqkv * H // 2], arena[sizes[0]:sizes[0] + nqkv * (H // 64) * 2].view(torch.float16)
+            prow, srow = 0, 0
+            for (n, k) in shapes[:3]:
+                packed = qkv_p[prow * (k // 2):(prow + n) * (k // 2)]
+                packed.copy_(torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device="cuda", generator=g))
+                u = torch.rand((n * (k // 64),), device="cuda", generator=g)
+                scales = qkv_s[srow * (k // 64):(srow + n) * (k // 64)]
+                scales.copy_(torch.exp(math.log(1e-3) + u * math.log(10.0)).to(torch.float16))
+                prow += n
+                srow += n
+                lw.append((packed, scales, n, k))
+            off = sizes[0] + sizes[1]
+            for (n, k) in shapes[3:]:
                 packed = arena[off:off + n * k // 2]
                 packed.copy_(torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device="cuda", generator=g))
                 off += sec(n * k // 2)
@@ -62,6 +83,7 @@ class Stack:
                 off += sec(n * (k // 64) * 2)
                 lw.append((packed, scales, n, k))
             self.w.append(lw)
+            self.wqkv.append((qkv_p, qkv_s, nqkv, H))
             self.arenas.append(arena)
         bf = torch.bfloat16
         self.ln = [(1.0 + 0.05 * torch.randn((H,), device="cuda", generator=g)).to(bf) for _ in range(2 * layers)]
@@ -70,9 +92,10 @@ class Stack:
         self.x0 = torch.randn((1, H), device="cuda", generator=g).to(bf)
         self.attn = torch.randn((1, nQ), device="cuda", generator=g).to(bf)
         self.x = torch.empty((1, H), dtype=bf, device="cuda")
-        self.q = torch.empty((1, nQ), dtype=bf, device="cuda")
-        self.k = torch.empty((1, nKV), dtype=bf, device="cuda")
-        self.v = torch.empty((1, nKV), dtype=bf, device="cuda")
+        self.qkv = torch.empty((1, nQ + 2 * nKV), dtype=bf, device="cuda")
+        self.q = self.qkv[:, :nQ]
+        self.k = self.qkv[:, nQ:nQ + nKV]
+        self.v = self.qkv[:, nQ + nKV:]
         self.gt = torch.empty((1, I), dtype=bf, device="cuda")
         self.ut = torch.empty((1, I), dtype=bf, device="cuda")
         self.xn = torch.empty((1, H), dtype=bf, device="cuda")
@@ -135,7 +158,7 @@ class Stack:
         wq, wk, wv, wo = self.w[l % self.layers][:4]
         ln = self.ln[2 * (l % self.layers)]
         if fused:
-            self._m1(2, p(xin), p(ln), [(wq, self.q), (wk, self.k), (wv, self.v)], eps=self.eps, st=st)
+            self._m1(2, p(xin), p(ln), [(self.wqkv[l % self.layers], self.qkv)], eps=self.eps, st=st)
             self._m1(0, p(self.attn), None, [(wo, x)], residual=p(xin), st=st)
             return
         self._ok(L.viper_hip_rmsnorm_quantize(p(xin), p(ln), self.eps, 1, H, 64, p(self.xn), p(self.xq),
