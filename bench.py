@@ -482,21 +482,24 @@ def time_config3(torch, stk, fused, replays=10, prefetch=0):
 
 def time_mlp(torch, L, gen, qtype=4, G=64, forms=("ref", "2launch")):
     """Config 1 (M = 1 MLP: gate+up K=2560 -> 2x10240, SwiGLU, down K=10240 -> 2560, all Q4_G64, weights
-    rotating over >= 512 MB): the reference's launch sequence (fused2 gate/up, swiglu + quantize,
-    prequantized down + residual) and the 2-launch form (gate/up pair with the swiglu epilogue, down
-    quantizing h in its prologue + residual).  Returns {line: value} for the forms asked for."""
+    rotating over >= 512 MB): the reference's launch sequence (gate+up as one concatenated matrix,
+    swiglu + quantize, prequantized down + residual) and the 2-launch form (gate/up pair with the swiglu
+    epilogue, down quantizing h in its prologue + residual).  Returns {line: value} for the forms asked
+    for."""
     N, K = 10240, 2560
     extras = {}
     H, I = 2560, 10240
     step_bytes = 3 * (N * K // 2 + N * (K // G) * 2)
     mcopies = max(2, -(-ROTATE_BYTES // step_bytes) + 1)
-    Wg, Sg = make_weights(torch, mcopies, I, H, gen)
-    Wu, Su = make_weights(torch, mcopies, I, H, gen)
+    # gate and up concatenated (config 1: one K=2560, N=2x10240 matrix per copy, gate rows first):
+    # the reference sequence launches it as one matrix, the 2-launch form pairs its two halves
+    Wgu, Sgu = make_weights(torch, mcopies, 2 * I, H, gen)
+    up_w, up_s = I * H // 2, I * (H // G) * 2   # byte offsets of the up half
     Wdn, Sdn = make_weights(torch, mcopies, H, I, gen)
     xm = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
     rm = torch.randn((1, H), device="cuda", generator=gen).to(torch.bfloat16)
-    gm = torch.empty((1, I), dtype=torch.bfloat16, device="cuda")
-    um = torch.empty((1, I), dtype=torch.bfloat16, device="cuda")
+    gum = torch.empty((1, 2 * I), dtype=torch.bfloat16, device="cuda")
+    gm, um = gum[:, :I], gum[:, I:]
     ym = torch.empty((1, H), dtype=torch.bfloat16, device="cuda")
     xqm = torch.empty((1, I), dtype=torch.int8, device="cuda")
     xsm = torch.empty((1, I // G), dtype=torch.float32, device="cuda")
@@ -504,9 +507,8 @@ def time_mlp(torch, L, gen, qtype=4, G=64, forms=("ref", "2launch")):
     def launch_mlp(i):
         c = i % mcopies
         st = torch.cuda.current_stream().cuda_stream
-        rc = L.viper_hip_qlinear_fused2(qtype, Wg[c].data_ptr(), Sg[c].data_ptr(), Wu[c].data_ptr(),
-                                        Su[c].data_ptr(), 0, G, I, H, xm.data_ptr(), 1, gm.data_ptr(),
-                                        um.data_ptr(), None, 0, st)
+        rc = L.viper_hip_qlinear(qtype, Wgu[c].data_ptr(), Sgu[c].data_ptr(), 0, G, 2 * I, H, xm.data_ptr(), 1,
+                                 gum.data_ptr(), None, None, 0, st)
         rc = rc or L.viper_hip_swiglu_quantize(gm.data_ptr(), um.data_ptr(), 1, I, G, gm.data_ptr(),
                                                xqm.data_ptr(), xsm.data_ptr(), st)
         rc = rc or L.viper_hip_qlinear_prequantized(qtype, Wdn[c].data_ptr(), Sdn[c].data_ptr(), 0, G, H, I,
@@ -531,8 +533,8 @@ def time_mlp(torch, L, gen, qtype=4, G=64, forms=("ref", "2launch")):
         c = i % mcopies
         st = torch.cuda.current_stream().cuda_stream
         rc = L.viper_hip_qlinear_m1_swiglu(qtype, 0, G, H, 0, xm.data_ptr(), None, 0.0, None,
-                                           Wg[c].data_ptr(), Sg[c].data_ptr(), Wu[c].data_ptr(),
-                                           Su[c].data_ptr(), I, gm.data_ptr(), None, None, st)
+                                           Wgu[c].data_ptr(), Sgu[c].data_ptr(), Wgu[c].data_ptr() + up_w,
+                                           Sgu[c].data_ptr() + up_s, I, gm.data_ptr(), None, None, st)
         rc = rc or L.viper_hip_qlinear(qtype, Wdn[c].data_ptr(), Sdn[c].data_ptr(), 0, G, H, I, gm.data_ptr(),
                                        1, ym.data_ptr(), rm.data_ptr(), None, 0, st)
         if rc != 0:
@@ -545,7 +547,7 @@ def time_mlp(torch, L, gen, qtype=4, G=64, forms=("ref", "2launch")):
         mlp2_bytes = step_bytes + H * 2 * 2 + I * 2 * 2 + H * 2
         extras["mlp_config1_2launch_us"] = round(mlp2_us, 3)
         extras["mlp_config1_2launch_gbs"] = round(mlp2_bytes / (mlp2_us * 1e-6) / 1e9, 1)
-    del Wg, Sg, Wu, Su, Wdn, Sdn
+    del Wgu, Sgu, Wdn, Sdn
     return extras
 
 
