@@ -147,6 +147,41 @@ def test_gate_up_swiglu_equals_chain(torch_dev, qtype, N, K, pro):
     assert int(d.max(initial=0)) <= 1, int(d.max())
 
 
+def test_gate_up_swiglu_norm_out_combinations(torch_dev):
+    # the optional outputs of the rmsnorm pair (normalized row, gate, up) are flagged together:
+    # every combination writes exactly the outputs asked for, the same bits each time
+    torch = torch_dev
+    K, N, eps = 2560, 10240, 1e-6
+    wg = weights(torch, O.Q4_G64, N, K, 560)[0]
+    wu = weights(torch, O.Q4_G64, N, K, 561)[0]
+    x = dev(torch, O.gen_act(1, K, 562, outlier_frac=0.02))
+    rng = np.random.default_rng(563)
+    gamma = dev(torch, bf16(1.0 + 0.1 * rng.standard_normal(K)))
+    ref_norm = torch.zeros((1, K), dtype=torch.int16, device="cuda")
+    xq = torch.zeros((1, K), dtype=torch.int8, device="cuda")
+    xs = torch.zeros((1, K // 64), dtype=torch.float32, device="cuda")
+    assert va.rmsnorm_quantize(x, gamma, eps, 64, xq, xs, out=ref_norm).ok()
+    z = lambda n: torch.full((1, n), 0x5555, dtype=torch.int16, device="cuda")
+    h_ref = z(N)
+    assert va.linear_m1_swiglu(wg, wu, P.RMSNORM, x, gamma, h_ref, eps=eps).ok()
+    for want_norm in (False, True):
+        for want_g in (False, True):
+            for want_u in (False, True):
+                h, norm, g, u = z(N), z(K), z(N), z(N)
+                print(f"norm={want_norm} gate={want_g} up={want_u}", flush=True)
+                assert va.linear_m1_swiglu(wg, wu, P.RMSNORM, x, gamma, h, eps=eps,
+                                           norm_out=norm if want_norm else None,
+                                           gate_out=g if want_g else None, up_out=u if want_u else None).ok()
+                torch.cuda.synchronize()
+                np.testing.assert_array_equal(u16(h), u16(h_ref))
+                if want_norm:
+                    np.testing.assert_array_equal(u16(norm), u16(ref_norm))
+                else:
+                    assert (u16(norm) == 0x5555).all()
+                for want, t in ((want_g, g), (want_u, u)):
+                    assert (u16(t) == 0x5555).all() != want
+
+
 def test_gate_up_swiglu_errors(torch_dev):
     torch = torch_dev
     wg = weights(torch, O.Q4_G64, 64, 256, 550)[0]
